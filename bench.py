@@ -1,0 +1,195 @@
+"""Benchmark of the flash-attention backward on one MI355X.
+
+Workload (BASELINE.json metric): B=4, H=12, N=4096, d=64, causal, bf16 inputs
+with fp32 accumulation. Synthetic seeded N(0,1) Q, K, V, dO generated on the
+GPU. The forward (O, LSE) runs once before the timed region, as in the
+reference (02-flash-attention/src/main.rs:599-611). One timed step = one full
+backward pass: Delta preprocess + dK/dV pass + dQ pass, inputs resident in HBM.
+
+Prints one JSON line. ``value`` is the algorithmic backward throughput
+(10 N^2 d per (batch, head), halved for causal) in TFLOP/s; ``roofline`` is the
+dominant kernel's achieved MFMA rate against MI355X's dense bf16 peak; and
+``cpu_baseline`` times the CPU oracle (a C restatement of the reference's CPU
+backward, main.rs:246-300) on a bounded sample of the same workload on this
+host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+       [--B 4 --H 12 --Hkv 12 --N 4096 --d 64 --causal 1 --dtype bf16]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_TFLOPS = {"bf16": 2516.6, "f32": 157.3}  # MI355X dense MFMA (AMD public spec)
+METRIC = "FA bwd TFLOP/s + % MFMA peak at B=4,H=12,N=4096,d=64 causal, 1 MI355X"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--B", type=int, default=4)
+    ap.add_argument("--H", type=int, default=12)
+    ap.add_argument("--Hkv", type=int, default=0, help="0 = same as H")
+    ap.add_argument("--N", type=int, default=4096)
+    ap.add_argument("--d", type=int, default=64)
+    ap.add_argument("--causal", type=int, default=1)
+    ap.add_argument("--dtype", choices=["bf16", "f32"], default="bf16")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    return ap.parse_args()
+
+
+def cpu_baseline(a, hkv):
+    """Times the CPU oracle on a bounded sample of the same workload: the
+    backward of the first 8 (batch, head) slices on one thread (the reference's
+    CPU path is single-threaded), inputs bf16-rounded as the GPU sees them."""
+    import numpy as np
+    import oracle  # the checker; used here only as the timed CPU baseline
+    lib = oracle.load()
+    nheads = min(8, a.B * a.H)
+    N, d = a.N, a.d
+    group = a.H // hkv
+    tot = 0.0
+    for i in range(nheads):
+        h = i % a.H
+        q = oracle.normal(N * d, 1000 + i).reshape(N, d)
+        k = oracle.normal(N * d, 2000 + h // group).reshape(N, d)
+        v = oracle.normal(N * d, 3000 + h // group).reshape(N, d)
+        do = oracle.normal(N * d, 4000 + i).reshape(N, d)
+        if a.dtype == "bf16":
+            q, k, v, do = (oracle.bf16_round(x) for x in (q, k, v, do))
+        t0 = time.perf_counter()
+        oracle.cpu_attention_bwd(q, k, v, do, N, d, bool(a.causal), lib=lib)
+        tot += time.perf_counter() - t0
+    import mx230_amd as mx
+    flops = mx.bwd_flops(1, nheads, N, d, bool(a.causal))
+    del np
+    return {"value": flops / tot / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"backward of {nheads} of the {a.B * a.H} (batch, head) slices at N={N}, "
+                      f"d={d}, causal={bool(a.causal)}, {a.dtype}-rounded inputs, fp32 math, "
+                      f"1 thread; {tot:.1f} s"}
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (got --gpus {a.gpus}); the path shards "
+              "over (batch, KV head) with no exchange, so the one-GPU figure is the per-GPU "
+              "share. Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import mx230_amd as mx
+
+    hkv = a.Hkv or a.H
+    causal = bool(a.causal)
+    bf16 = a.dtype == "bf16"
+    dt = torch.bfloat16 if bf16 else torch.float32
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    mx.init(0)
+    mx.load_library()
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1234)
+    qs, ks = (a.B, a.H, a.N, a.d), (a.B, hkv, a.N, a.d)
+    q = torch.randn(qs, generator=gen, device=dev, dtype=torch.float32).to(dt)
+    k = torch.randn(ks, generator=gen, device=dev, dtype=torch.float32).to(dt)
+    v = torch.randn(ks, generator=gen, device=dev, dtype=torch.float32).to(dt)
+    do = torch.randn(qs, generator=gen, device=dev, dtype=torch.float32).to(dt)
+    o = torch.empty_like(q)
+    lse = torch.empty((a.B, a.H, a.N), device=dev, dtype=torch.float32)
+    delta = torch.empty_like(lse)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
+    # forward once (outside the timed region), also timed on its own
+    stream = torch.cuda.current_stream()
+    fwd_ms = []
+    for i in range(a.warmup + 5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        mx.run_flash_lse(q, k, v, o, lse, causal)
+        e1.record(stream)
+        if i >= a.warmup:
+            fwd_ms.append((e0, e1))
+    torch.cuda.synchronize()
+    fwd_avg = sum(x.elapsed_time(y) for x, y in fwd_ms) / len(fwd_ms)
+
+    def step(evs=None):
+        if evs:
+            evs[0].record(stream)
+        mx.run_preprocess(do, o, delta)
+        if evs:
+            evs[1].record(stream)
+        mx.run_bwd_dkv(q, k, v, do, lse, delta, dk, dv, causal)
+        if evs:
+            evs[2].record(stream)
+        mx.run_bwd_dq(q, k, v, do, lse, delta, dq, causal)
+        if evs:
+            evs[3].record(stream)
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # timed region: exactly K backward steps, synchronised on both sides; the
+    # events between the launches give each kernel's duration on the same stream
+    evsets = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(a.steps)]
+    torch.cuda.synchronize()
+    for evs in evsets:
+        step(evs)
+    torch.cuda.synchronize()
+    ms_per_step = evsets[0][0].elapsed_time(evsets[-1][3]) / a.steps
+    kern = {"preprocess": 0.0, "dkv": 0.0, "dq": 0.0}
+    for evs in evsets:
+        kern["preprocess"] += evs[0].elapsed_time(evs[1])
+        kern["dkv"] += evs[1].elapsed_time(evs[2])
+        kern["dq"] += evs[2].elapsed_time(evs[3])
+    kern = {n: t / a.steps for n, t in kern.items()}
+
+    half = 0.5 if causal else 1.0
+    bwd_flops = mx.bwd_flops(a.B, a.H, a.N, a.d, causal)
+    # algorithmic MFMA work of each kernel per launch: dK/dV pass computes the
+    # S, dP, dV, dK products (8 N^2 d per (batch, query head)); the dQ pass the
+    # S, dP, dQ products (6 N^2 d) -- S and dP are recomputed by both passes
+    kflops = {"dkv": 8.0 * a.N * a.N * a.d * a.B * a.H * half,
+              "dq": 6.0 * a.N * a.N * a.d * a.B * a.H * half}
+    dom = max(("dkv", "dq"), key=lambda n: kern[n])
+    peak = PEAK_TFLOPS[a.dtype]
+    achieved = kflops[dom] / (kern[dom] * 1e-3) / 1e12
+    value = bwd_flops / (ms_per_step * 1e-3) / 1e12
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"traffic_{dom}_{a.dtype}_B{a.B}H{a.H}N{a.N}d{a.d}.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("bytes_per_launch")
+
+    res = {
+        "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": a.dtype,
+        "data": "synthetic (seeded N(0,1) on the GPU)",
+        "config": {"workload": "flash-attention backward (preprocess + dK/dV + dQ), fwd outside timing",
+                   "B": a.B, "Hq": a.H, "Hkv": hkv, "N": a.N, "d": a.d, "causal": causal,
+                   "parallelism": "single GPU"},
+        "pct_peak": round(100.0 * value / peak, 2),
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2), "peak": peak,
+                     "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic},
+        "kernels_ms": {n: round(t, 4) for n, t in kern.items()},
+        "fwd": {"ms": round(fwd_avg, 4),
+                "tflops": round(mx.fwd_flops(a.B, a.H, a.N, a.d, causal) / (fwd_avg * 1e-3) / 1e12, 2)},
+    }
+    if not a.no_cpu:
+        res["cpu_baseline"] = cpu_baseline(a, hkv)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

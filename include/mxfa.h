@@ -1,0 +1,151 @@
+/*
+ * mxfa.h - C ABI of the MI355X (gfx950) flash-attention training path.
+ *
+ * Drop-in for the host wrappers and kernels of the 02-flash-attention crate of
+ * glaucomaa/mx230. Every entry point below names the reference interface it
+ * replaces (paths relative to the reference repository).
+ *
+ * Conventions
+ *   - Plain C types only: device pointers are `void*` / `float*` obtained from
+ *     hipMalloc (or any allocator of device memory); `stream` is a
+ *     hipStream_t passed as `void*` (NULL = the null stream).
+ *   - Layouts (row-major, contiguous):
+ *       Q, O, dO, dQ : [B][Hq][N][d]
+ *       K, V, dK, dV : [B][Hkv][N][d]
+ *       LSE, Delta   : [B][Hq][N]  (always fp32; LSE in natural-log units)
+ *     With B = Hq = Hkv = 1 and d = 64 this is exactly the reference's
+ *     [N][64] layout (attention_flash.cu:17-89).
+ *     Query head h reads KV head h / (Hq / Hkv) (grouped-query attention,
+ *     03-llm-engine/src/cpu.rs:194,224); dK / dV of a KV head are the sum
+ *     over the query heads that share it.
+ *   - dtype MXFA_F32: every tensor above is fp32. dtype MXFA_BF16: Q, K, V,
+ *     O, dO, dQ, dK, dV are bf16 (raw uint16 storage), LSE and Delta fp32,
+ *     and all accumulation is fp32.
+ *   - All launches are asynchronous on `stream`. The library never
+ *     synchronises, never allocates device memory and keeps no per-call
+ *     state, so calls are thread-safe; ordering is the caller's stream order.
+ *   - Errors are returned as negative codes (see mxfa_status); nothing aborts
+ *     and no C++ exception crosses this boundary. The reference panics on a
+ *     launch failure (02-flash-attention/src/main.rs:87,122,142,172,204,209).
+ *   - Device pointers must be 16-byte aligned.
+ */
+#ifndef MXFA_H
+#define MXFA_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    MXFA_OK = 0,
+    MXFA_ERR_NULL = -1,        /* a required pointer is NULL */
+    MXFA_ERR_SHAPE = -2,       /* B, Hq, Hkv, N, d or Hq % Hkv invalid */
+    MXFA_ERR_DTYPE = -3,       /* unknown dtype */
+    MXFA_ERR_UNSUPPORTED = -4, /* valid shape, but no kernel (e.g. d not in {64, 128}) */
+    MXFA_ERR_ALIGN = -5,       /* a device pointer is not 16-byte aligned */
+    MXFA_ERR_LAUNCH = -6,      /* the HIP runtime rejected a launch */
+    MXFA_ERR_DEVICE = -7       /* no usable gfx950 device */
+} mxfa_status;
+
+typedef enum { MXFA_F32 = 0, MXFA_BF16 = 1 } mxfa_dtype;
+
+typedef struct {
+    int B;        /* batch */
+    int Hq;       /* query heads */
+    int Hkv;      /* key/value heads; Hq % Hkv == 0 */
+    int N;        /* sequence length (queries = keys) */
+    int d;        /* head dim: 64 or 128 */
+    int causal;   /* 0 or 1: key j visible to query i iff j <= i (main.rs:218) */
+    int dtype;    /* mxfa_dtype */
+    float scale;  /* softmax scale; 0 selects 1/sqrt(d) (main.rs:214) */
+} mxfa_shape;
+
+/* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
+int mxfa_version(void);
+
+/* Human-readable text of a status code (static storage). */
+const char *mxfa_strerror(int status);
+
+/* Checks that `device` exists and is a gfx950 (MI355X) and makes it current.
+ * Optional: the run_* entry points work on the current device without it.
+ * Replaces CudaContext::new(0) + load_kernels / load_bwd
+ * (02-flash-attention/src/main.rs:392-415, 514). */
+int mxfa_init(int device);
+
+/* Releases nothing (the library holds no resources); kept for symmetry. */
+int mxfa_shutdown(void);
+
+/* Validates a shape exactly as every run_* entry point does; no GPU access. */
+int mxfa_check_shape(const mxfa_shape *shape);
+
+/* Forward, O only.
+ * Replaces run_flash (02-flash-attention/src/main.rs:68-88) and kernel
+ * attn_flash (02-flash-attention/kernels/attention_flash.cu:91-94). */
+int mxfa_run_flash(const mxfa_shape *shape, const void *q, const void *k, const void *v,
+                   void *o, void *stream);
+
+/* Forward, O and the per-row log-sum-exp L_i = m_i + ln(l_i).
+ * Replaces run_flash_lse (main.rs:102-123) and attn_flash_lse
+ * (attention_flash.cu:97-100, LSE at :85-87). */
+int mxfa_run_flash_lse(const mxfa_shape *shape, const void *q, const void *k, const void *v,
+                       void *o, float *lse, void *stream);
+
+/* Delta_i = sum_x dO[i][x] * O[i][x] (fp32 accumulation).
+ * Replaces run_preprocess (main.rs:126-143) and attn_bwd_preprocess
+ * (attention_bwd.cu:32-44). */
+int mxfa_run_preprocess(const mxfa_shape *shape, const void *dout, const void *o, float *delta,
+                        void *stream);
+
+/* dQ pass only (overwrites dQ; atomic-free).
+ * Replaces the attn_bwd_dq launch of run_bwd_flash (main.rs:202-204,
+ * attention_bwd.cu:96-158). */
+int mxfa_run_bwd_dq(const mxfa_shape *shape, const void *q, const void *k, const void *v,
+                    const void *dout, const float *lse, const float *delta, void *dq,
+                    void *stream);
+
+/* dK/dV pass only (overwrites dK, dV; atomic-free; with Hq > Hkv the sum over
+ * the query heads of a group is done inside the kernel).
+ * Replaces the attn_bwd_dkv launch of run_bwd_flash (main.rs:206-209,
+ * attention_bwd.cu:165-243). */
+int mxfa_run_bwd_dkv(const mxfa_shape *shape, const void *q, const void *k, const void *v,
+                     const void *dout, const float *lse, const float *delta, void *dk,
+                     void *dv, void *stream);
+
+/* The tiled backward: dK/dV pass then dQ pass, same stream, outputs
+ * overwritten (no zeroing needed).
+ * Replaces run_bwd_flash (02-flash-attention/src/main.rs:179-210). */
+int mxfa_run_bwd_flash(const mxfa_shape *shape, const void *q, const void *k, const void *v,
+                       const void *dout, const float *lse, const float *delta, void *dq,
+                       void *dk, void *dv, void *stream);
+
+/* Bytes of device workspace the backward needs beyond its inputs and
+ * outputs: always 0 (dQ is a separate atomic-free pass). */
+size_t mxfa_bwd_workspace_bytes(const mxfa_shape *shape);
+
+/* Naive backward baseline: one thread per query row, dK/dV scattered with
+ * atomic adds. fp32 only. dQ, dK, dV MUST be zeroed by the caller.
+ * Replaces run_bwd_naive (main.rs:147-173) and attn_bwd_naive
+ * (attention_bwd.cu:48-90). */
+int mxfa_run_bwd_naive(const mxfa_shape *shape, const void *q, const void *k, const void *v,
+                       const void *dout, const float *lse, const float *delta, void *dq,
+                       void *dk, void *dv, void *stream);
+
+/* Bytes of the N x N fp32 score scratch mxfa_run_naive_fwd needs
+ * (B * Hq * N * N * 4). */
+size_t mxfa_naive_scratch_bytes(const mxfa_shape *shape);
+
+/* Naive forward baseline that materialises the scores: S = QK^T * scale
+ * (masked to -inf above the diagonal when causal), row softmax in place,
+ * O = S V. fp32 only; `s` holds mxfa_naive_scratch_bytes bytes.
+ * Replaces Naive::run (main.rs:32-66) and attn_scores / attn_softmax /
+ * attn_av (attention_naive.cu:8-70). */
+int mxfa_run_naive_fwd(const mxfa_shape *shape, const void *q, const void *k, const void *v,
+                       float *s, void *o, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MXFA_H */

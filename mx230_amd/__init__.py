@@ -1,0 +1,319 @@
+"""MI355X-native flash-attention training path (forward O + LSE, FA-2 backward).
+
+The compute lives in ``libmxfa.so`` (HIP kernels for gfx950 behind the C ABI of
+``include/mxfa.h``, built from ``mx230_amd/csrc``). This module is the host-side
+mirror of the reference crate's Rust wrappers
+(02-flash-attention/src/main.rs:32-210): the same entry points, the same argument
+meaning (caller-owned device buffers, ``n`` implied by the shapes, ``causal``
+flag), the same ownership (the caller allocates O, LSE, Delta, dQ, dK, dV) and the
+same "wrappers only enqueue work" contract. Where the reference panics on a
+launch failure, these raise :class:`MxfaError`.
+
+PyTorch is only plumbing here: tensors provide device memory and the current
+stream. There is no CPU or PyTorch fallback: if ``libmxfa.so`` is missing or the
+tensors are not on a GPU, every call raises.
+
+Tensor layouts (contiguous): Q, O, dO, dQ ``[B, Hq, N, d]``; K, V, dK, dV
+``[B, Hkv, N, d]``; LSE, Delta ``[B, Hq, N]`` float32. A 2-D ``[N, d]`` tensor is
+read as B = H = 1, i.e. the reference's single-head layout.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmxfa.so")
+
+MXFA_F32, MXFA_BF16 = 0, 1
+
+STATUS = {
+    0: "MXFA_OK",
+    -1: "MXFA_ERR_NULL",
+    -2: "MXFA_ERR_SHAPE",
+    -3: "MXFA_ERR_DTYPE",
+    -4: "MXFA_ERR_UNSUPPORTED",
+    -5: "MXFA_ERR_ALIGN",
+    -6: "MXFA_ERR_LAUNCH",
+    -7: "MXFA_ERR_DEVICE",
+}
+
+# Every symbol include/mxfa.h declares (the tests check the library exports them).
+EXPORTS = (
+    "mxfa_version", "mxfa_strerror", "mxfa_init", "mxfa_shutdown", "mxfa_check_shape",
+    "mxfa_run_flash", "mxfa_run_flash_lse", "mxfa_run_preprocess", "mxfa_run_bwd_dq",
+    "mxfa_run_bwd_dkv", "mxfa_run_bwd_flash", "mxfa_bwd_workspace_bytes", "mxfa_run_bwd_naive",
+    "mxfa_naive_scratch_bytes", "mxfa_run_naive_fwd",
+)
+
+
+class MxfaError(RuntimeError):
+    """A non-zero status from libmxfa."""
+
+    def __init__(self, func: str, status: int, text: str):
+        super().__init__(f"{func}: {STATUS.get(status, status)} ({text})")
+        self.status = status
+
+
+class MxfaShape(ctypes.Structure):
+    _fields_ = [("B", ctypes.c_int), ("Hq", ctypes.c_int), ("Hkv", ctypes.c_int), ("N", ctypes.c_int),
+                ("d", ctypes.c_int), ("causal", ctypes.c_int), ("dtype", ctypes.c_int),
+                ("scale", ctypes.c_float)]
+
+
+_lib = None
+
+
+def load_library(path: str | None = None):
+    """Loads libmxfa.so (raises if it has not been built)."""
+    global _lib
+    if path is None and _lib is not None:
+        return _lib
+    p = path or LIB_PATH
+    if not os.path.exists(p):
+        raise ImportError(f"{p} is missing: build it with `make -C mx230_amd/csrc` "
+                          "(or __graft_entry__.build()); there is no fallback path")
+    lib = ctypes.CDLL(p)
+    vp, sp, fp = ctypes.c_void_p, ctypes.POINTER(MxfaShape), ctypes.c_void_p
+    lib.mxfa_version.restype = ctypes.c_int
+    lib.mxfa_strerror.restype = ctypes.c_char_p
+    lib.mxfa_strerror.argtypes = [ctypes.c_int]
+    lib.mxfa_init.argtypes = [ctypes.c_int]
+    lib.mxfa_check_shape.argtypes = [sp]
+    lib.mxfa_run_flash.argtypes = [sp, vp, vp, vp, vp, vp]
+    lib.mxfa_run_flash_lse.argtypes = [sp, vp, vp, vp, vp, fp, vp]
+    lib.mxfa_run_preprocess.argtypes = [sp, vp, vp, fp, vp]
+    lib.mxfa_run_bwd_dq.argtypes = [sp, vp, vp, vp, vp, fp, fp, vp, vp]
+    lib.mxfa_run_bwd_dkv.argtypes = [sp, vp, vp, vp, vp, fp, fp, vp, vp, vp]
+    lib.mxfa_run_bwd_flash.argtypes = [sp, vp, vp, vp, vp, fp, fp, vp, vp, vp, vp]
+    lib.mxfa_run_bwd_naive.argtypes = [sp, vp, vp, vp, vp, fp, fp, vp, vp, vp, vp]
+    lib.mxfa_bwd_workspace_bytes.argtypes = [sp]
+    lib.mxfa_bwd_workspace_bytes.restype = ctypes.c_size_t
+    lib.mxfa_naive_scratch_bytes.argtypes = [sp]
+    lib.mxfa_naive_scratch_bytes.restype = ctypes.c_size_t
+    lib.mxfa_run_naive_fwd.argtypes = [sp, vp, vp, vp, fp, vp, vp]
+    for name in EXPORTS:
+        if name not in ("mxfa_version", "mxfa_strerror", "mxfa_bwd_workspace_bytes",
+                        "mxfa_naive_scratch_bytes"):
+            getattr(lib, name).restype = ctypes.c_int
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def _check(func: str, rc: int):
+    if rc != 0:
+        raise MxfaError(func, rc, load_library().mxfa_strerror(rc).decode())
+
+
+@dataclass(frozen=True)
+class Shape:
+    B: int
+    Hq: int
+    Hkv: int
+    N: int
+    d: int
+    causal: bool
+    bf16: bool
+    scale: float = 0.0
+
+    def c(self) -> MxfaShape:
+        return MxfaShape(self.B, self.Hq, self.Hkv, self.N, self.d, int(self.causal),
+                         MXFA_BF16 if self.bf16 else MXFA_F32, self.scale)
+
+
+# --------------------------------------------------------------- torch glue --
+
+def _torch():
+    import torch
+    return torch
+
+
+def _dims(t, name):
+    if t.dim() == 2:
+        return 1, 1, t.shape[0], t.shape[1]
+    if t.dim() == 4:
+        return tuple(t.shape)
+    raise ValueError(f"{name}: expected [N, d] or [B, H, N, d], got {tuple(t.shape)}")
+
+
+def _ptr(t, name, dtype):
+    torch = _torch()
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: must be a device tensor (got {t.device}); there is no CPU path")
+    if t.dtype != dtype:
+        raise ValueError(f"{name}: dtype {t.dtype}, expected {dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: must be contiguous")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream):
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def shape_of(q, k, causal: bool, scale: float = 0.0) -> Shape:
+    """Shape of an attention call from Q [B,Hq,N,d] and K [B,Hkv,N,d]."""
+    torch = _torch()
+    B, Hq, N, d = _dims(q, "q")
+    Bk, Hkv, Nk, dk = _dims(k, "k")
+    if (Bk, Nk, dk) != (B, N, d):
+        raise ValueError(f"q {tuple(q.shape)} and k {tuple(k.shape)} disagree")
+    if q.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"dtype {q.dtype} not supported (float32 or bfloat16)")
+    return Shape(B, Hq, Hkv, N, d, bool(causal), q.dtype == torch.bfloat16, float(scale))
+
+
+def _expect(t, name, shape4, dtype):
+    dims = _dims(t, name)
+    if tuple(dims) != tuple(shape4):
+        raise ValueError(f"{name}: shape {tuple(t.shape)} does not match {tuple(shape4)}")
+    return _ptr(t, name, dtype)
+
+
+def _io(sh: Shape):
+    torch = _torch()
+    dt = torch.bfloat16 if sh.bf16 else torch.float32
+    qs = (sh.B, sh.Hq, sh.N, sh.d)
+    ks = (sh.B, sh.Hkv, sh.N, sh.d)
+    return dt, qs, ks
+
+
+def _vec_ptr(t, name, sh: Shape):
+    torch = _torch()
+    if t.numel() != sh.B * sh.Hq * sh.N:
+        raise ValueError(f"{name}: expected {sh.B * sh.Hq * sh.N} elements, got {t.numel()}")
+    return _ptr(t, name, torch.float32)
+
+
+# ------------------------------------------- reference-shaped entry points --
+
+def run_flash(q, k, v, o, causal: bool, scale: float = 0.0, stream=None):
+    """Forward, O only (main.rs:68-88)."""
+    sh = shape_of(q, k, causal, scale)
+    dt, qs, ks = _io(sh)
+    args = (_expect(q, "q", qs, dt), _expect(k, "k", ks, dt), _expect(v, "v", ks, dt),
+            _expect(o, "o", qs, dt))
+    _check("mxfa_run_flash", load_library().mxfa_run_flash(ctypes.byref(sh.c()), *args, _stream(stream)))
+
+
+def run_flash_lse(q, k, v, o, lse, causal: bool, scale: float = 0.0, stream=None):
+    """Forward with the log-sum-exp the backward needs (main.rs:102-123)."""
+    sh = shape_of(q, k, causal, scale)
+    dt, qs, ks = _io(sh)
+    args = (_expect(q, "q", qs, dt), _expect(k, "k", ks, dt), _expect(v, "v", ks, dt),
+            _expect(o, "o", qs, dt), _vec_ptr(lse, "lse", sh))
+    _check("mxfa_run_flash_lse",
+           load_library().mxfa_run_flash_lse(ctypes.byref(sh.c()), *args, _stream(stream)))
+
+
+def run_preprocess(do, o, delta, stream=None):
+    """Delta = rowsum(dO * O) (main.rs:126-143)."""
+    sh = shape_of(do, do, False)
+    dt, qs, _ = _io(sh)
+    args = (_expect(do, "do", qs, dt), _expect(o, "o", qs, dt), _vec_ptr(delta, "delta", sh))
+    _check("mxfa_run_preprocess",
+           load_library().mxfa_run_preprocess(ctypes.byref(sh.c()), *args, _stream(stream)))
+
+
+def _bwd_args(q, k, v, do, lse, delta, causal, scale):
+    sh = shape_of(q, k, causal, scale)
+    dt, qs, ks = _io(sh)
+    args = [_expect(q, "q", qs, dt), _expect(k, "k", ks, dt), _expect(v, "v", ks, dt),
+            _expect(do, "do", qs, dt), _vec_ptr(lse, "lse", sh), _vec_ptr(delta, "delta", sh)]
+    return sh, dt, qs, ks, args
+
+
+def run_bwd_flash(q, k, v, do, lse, delta, dq, dk, dv, causal: bool, scale: float = 0.0,
+                  stream=None):
+    """Tiled atomic-free backward: dK/dV pass then dQ pass (main.rs:179-210).
+    Outputs are overwritten."""
+    sh, dt, qs, ks, args = _bwd_args(q, k, v, do, lse, delta, causal, scale)
+    args += [_expect(dq, "dq", qs, dt), _expect(dk, "dk", ks, dt), _expect(dv, "dv", ks, dt)]
+    _check("mxfa_run_bwd_flash",
+           load_library().mxfa_run_bwd_flash(ctypes.byref(sh.c()), *args, _stream(stream)))
+
+
+def run_bwd_dq(q, k, v, do, lse, delta, dq, causal: bool, scale: float = 0.0, stream=None):
+    """dQ pass alone (attention_bwd.cu:96-158)."""
+    sh, dt, qs, ks, args = _bwd_args(q, k, v, do, lse, delta, causal, scale)
+    args += [_expect(dq, "dq", qs, dt)]
+    _check("mxfa_run_bwd_dq", load_library().mxfa_run_bwd_dq(ctypes.byref(sh.c()), *args, _stream(stream)))
+
+
+def run_bwd_dkv(q, k, v, do, lse, delta, dk, dv, causal: bool, scale: float = 0.0, stream=None):
+    """dK/dV pass alone (attention_bwd.cu:165-243)."""
+    sh, dt, qs, ks, args = _bwd_args(q, k, v, do, lse, delta, causal, scale)
+    args += [_expect(dk, "dk", ks, dt), _expect(dv, "dv", ks, dt)]
+    _check("mxfa_run_bwd_dkv",
+           load_library().mxfa_run_bwd_dkv(ctypes.byref(sh.c()), *args, _stream(stream)))
+
+
+def run_bwd_naive(q, k, v, do, lse, delta, dq, dk, dv, causal: bool, scale: float = 0.0,
+                  stream=None):
+    """Naive atomic backward baseline, fp32; outputs must be zeroed (main.rs:147-173)."""
+    sh, dt, qs, ks, args = _bwd_args(q, k, v, do, lse, delta, causal, scale)
+    args += [_expect(dq, "dq", qs, dt), _expect(dk, "dk", ks, dt), _expect(dv, "dv", ks, dt)]
+    _check("mxfa_run_bwd_naive",
+           load_library().mxfa_run_bwd_naive(ctypes.byref(sh.c()), *args, _stream(stream)))
+
+
+def naive_scratch_bytes(q, k, causal: bool) -> int:
+    sh = shape_of(q, k, causal)
+    return int(load_library().mxfa_naive_scratch_bytes(ctypes.byref(sh.c())))
+
+
+def naive_run(q, k, v, s, o, causal: bool, scale: float = 0.0, stream=None):
+    """Naive forward with the materialised N x N scores ``s`` (Naive::run, main.rs:32-66)."""
+    torch = _torch()
+    sh = shape_of(q, k, causal, scale)
+    dt, qs, ks = _io(sh)
+    if s.numel() * 4 < naive_scratch_bytes(q, k, causal):
+        raise ValueError("s: scratch too small (needs B*Hq*N*N float32)")
+    args = (_expect(q, "q", qs, dt), _expect(k, "k", ks, dt), _expect(v, "v", ks, dt),
+            _ptr(s, "s", torch.float32), _expect(o, "o", qs, dt))
+    _check("mxfa_run_naive_fwd",
+           load_library().mxfa_run_naive_fwd(ctypes.byref(sh.c()), *args, _stream(stream)))
+
+
+# ------------------------------------------------------------ conveniences --
+
+def attention_fwd(q, k, v, causal: bool, scale: float = 0.0, stream=None):
+    """Allocates O and LSE and runs the forward; returns (O, LSE)."""
+    torch = _torch()
+    sh = shape_of(q, k, causal, scale)
+    o = torch.empty_like(q)
+    lse = torch.empty((sh.B, sh.Hq, sh.N), dtype=torch.float32, device=q.device)
+    run_flash_lse(q, k, v, o, lse, causal, scale, stream)
+    return o, lse
+
+
+def attention_bwd(q, k, v, o, lse, do, causal: bool, scale: float = 0.0, stream=None):
+    """Allocates Delta, dQ, dK, dV and runs preprocess + backward; returns (dQ, dK, dV)."""
+    torch = _torch()
+    sh = shape_of(q, k, causal, scale)
+    delta = torch.empty((sh.B, sh.Hq, sh.N), dtype=torch.float32, device=q.device)
+    run_preprocess(do, o, delta, stream)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    run_bwd_flash(q, k, v, do, lse, delta, dq, dk, dv, causal, scale, stream)
+    return dq, dk, dv
+
+
+def init(device: int = 0):
+    """mxfa_init: checks that ``device`` is a gfx950 and makes it current."""
+    _check("mxfa_init", load_library().mxfa_init(device))
+
+
+def fwd_flops(B, Hq, N, d, causal) -> float:
+    """Algorithmic forward flops: 4 N^2 d per (batch, query head), halved if causal."""
+    return 4.0 * N * N * d * B * Hq * (0.5 if causal else 1.0)
+
+
+def bwd_flops(B, Hq, N, d, causal) -> float:
+    """Algorithmic backward flops: 10 N^2 d per (batch, query head), halved if causal."""
+    return 10.0 * N * N * d * B * Hq * (0.5 if causal else 1.0)

@@ -1,0 +1,447 @@
+// Flash-attention backward for gfx950 (FA-2 structure, recompute from LSE).
+//
+// Math (attention_bwd.cu:8-14): with p_ij = exp(s_ij * scale - L_i),
+//   Delta_i = sum_x dO[i,x] O[i,x]
+//   dP_ij   = dO_i . v_j
+//   dS_ij   = p_ij (dP_ij - Delta_i)          (the softmax scale is applied once,
+//   dV_j    = sum_i p_ij dO_i                  to dK and dQ, at the end)
+//   dK_j    = scale * sum_i dS_ij q_i
+//   dQ_i    = scale * sum_j dS_ij k_j
+//
+// Two atomic-free passes, as in attention_bwd.cu:96-243, re-tiled for CDNA4:
+//   * dkv_kernel: a workgroup owns 64*KT keys of one (batch, KV head); each of
+//     its 4 waves owns 16*KT keys whose K/V rows sit in registers and whose
+//     dK/dV accumulate in registers. Q/dO/LSE/Delta stream through
+//     double-buffered LDS, 64 queries per stage, for every query head of the
+//     KV head's group in turn, so the grouped-query reduction of dK/dV happens
+//     inside the kernel with no atomics and no extra memory.
+//   * dq_kernel: a workgroup owns 128 queries of one (batch, query head) (32
+//     per wave, Q/dO rows in registers); K/V stream through LDS 64 keys per
+//     stage. It recomputes S and dP (the price of staying atomic-free and O(N)
+//     in memory).
+#include "fa_device.h"
+#include "fa_launch.h"
+
+namespace mxfa {
+
+// ------------------------------------------------------------ preprocess
+
+// Delta_i = sum_x dO[i][x] * O[i][x], 8 lanes per row (attention_bwd.cu:32-44).
+template <class T, int D>
+__global__ __launch_bounds__(256) void preprocess_kernel(const T *dout, const T *o, float *delta,
+                                                         long rows) {
+    const long t = (long)blockIdx.x * 256 + threadIdx.x;
+    const long row = t >> 3;
+    const int part = (int)(t & 7);
+    constexpr int PER = D / 8;  // elements per lane
+    float acc = 0.f;
+    if (row < rows) {
+        const T *a = dout + row * D + part * PER;
+        const T *b = o + row * D + part * PER;
+        if constexpr (sizeof(T) == 4) {
+#pragma unroll
+            for (int i = 0; i < PER; i += 4) {
+                const float4 x = *reinterpret_cast<const float4 *>(a + i);
+                const float4 y = *reinterpret_cast<const float4 *>(b + i);
+                acc += x.x * y.x;
+                acc += x.y * y.y;
+                acc += x.z * y.z;
+                acc += x.w * y.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < PER; i += 8) {
+                const uint4 x = *reinterpret_cast<const uint4 *>(a + i);
+                const uint4 y = *reinterpret_cast<const uint4 *>(b + i);
+                const uint32_t xs[4] = {x.x, x.y, x.z, x.w}, ys[4] = {y.x, y.y, y.z, y.w};
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    acc += __uint_as_float(xs[w] << 16) * __uint_as_float(ys[w] << 16);
+                    acc += __uint_as_float(xs[w] & 0xffff0000u) * __uint_as_float(ys[w] & 0xffff0000u);
+                }
+            }
+        }
+    }
+    acc += __shfl_xor(acc, 4, 8);
+    acc += __shfl_xor(acc, 2, 8);
+    acc += __shfl_xor(acc, 1, 8);
+    if (row < rows && part == 0) delta[row] = acc;
+}
+
+// ------------------------------------------------------------------ dQ pass
+
+template <class Pol, bool CAUSAL>
+__global__ __launch_bounds__(256) void dq_kernel(Params p) {
+    using T = typename Pol::T;
+    using Frag = typename Pol::Frag;
+    constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
+    constexpr int BQ = 128, BK = 64;
+    using SB = StageBlock<Pol>;
+    static_assert(2 * SB::PER_TILE <= 256, "one stage block per thread");
+
+    __shared__ __attribute__((aligned(16))) T sK[2][BK * D];
+    __shared__ __attribute__((aligned(16))) T sV[2][BK * D];
+    __shared__ __attribute__((aligned(16))) T sKt[Pol::kColForm ? 2 : 1][Pol::kColForm ? D * BK : 8];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int g = lane >> 4, l16 = lane & 15;
+    const int N = p.N;
+    const int bh = blockIdx.x;
+    const int nqb = (N + BQ - 1) / BQ;
+    const int qb = CAUSAL ? (nqb - 1 - (int)blockIdx.y) : (int)blockIdx.y;
+    const int b = bh / p.Hq, h = bh % p.Hq, kvh = h / p.group;
+    const T *Q = static_cast<const T *>(p.q) + (size_t)bh * N * D;
+    const T *dO = static_cast<const T *>(p.dout) + (size_t)bh * N * D;
+    const size_t kvoff = ((size_t)b * p.Hkv + kvh) * N * D;
+    const T *K = static_cast<const T *>(p.k) + kvoff;
+    const T *V = static_cast<const T *>(p.v) + kvoff;
+    const int q0 = qb * BQ + wave * 32;
+
+    Frag qf[2][NC], dof[2][NC];
+    float L2[2], Dl[2];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        const int qi = q0 + 16 * qt + l16;
+        const bool ok = qi < N;
+        Pol::gmem_row_frags(qf[qt], Q + (size_t)qi * D, g, ok);
+        Pol::gmem_row_frags(dof[qt], dO + (size_t)qi * D, g, ok);
+        L2[qt] = ok ? p.lse[(size_t)bh * N + qi] * kLog2e : 0.f;
+        Dl[qt] = ok ? p.delta[(size_t)bh * N + qi] : 0.f;
+    }
+    f32x4 acc[XT][2];
+#pragma unroll
+    for (int xt = 0; xt < XT; ++xt) acc[xt][0] = acc[xt][1] = zero4();
+
+    const int kend = CAUSAL ? min(N, qb * BQ + BQ) : N;
+    const int nsteps = (kend + BK - 1) / BK;
+
+    SB sb;
+    const bool stage_k = tid < SB::PER_TILE;
+    const bool stage_v = !stage_k && tid < 2 * SB::PER_TILE;
+    const int sbid = stage_k ? tid : tid - SB::PER_TILE;
+    auto load_stage = [&](int st) {
+        const int k0 = st * BK;
+        if (stage_k) sb.load(K + (size_t)k0 * D, N - k0, sbid);
+        if (stage_v) sb.load(V + (size_t)k0 * D, N - k0, sbid);
+    };
+    auto store_stage = [&](int buf) {
+        if (stage_k) {
+            sb.store_row(sK[buf], sbid);
+            if constexpr (Pol::kColForm) sb.store_col(sKt[buf], sbid);
+        }
+        if (stage_v) sb.store_row(sV[buf], sbid);
+    };
+
+    load_stage(0);
+    store_stage(0);
+    __syncthreads();
+
+    for (int st = 0; st < nsteps; ++st) {
+        const int cur = st & 1;
+        const bool has_next = st + 1 < nsteps;
+        if (has_next) load_stage(st + 1);
+        const int k0 = st * BK;
+        const bool active = !CAUSAL || k0 <= q0 + 31;
+        if (active) {
+            const bool need_mask = (k0 + BK > N) || (CAUSAL && k0 + BK - 1 > q0);
+#pragma unroll
+            for (int blk = 0; blk < 2; ++blk) {
+                f32x4 s[2][2], dp[2][2];  // [t][qt]
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    Frag a[NC];
+                    const int n = 32 * blk + Pol::arow(t, l16);
+                    Pol::lds_row_frags(a, sK[cur], n, g);
+#pragma unroll
+                    for (int qt = 0; qt < 2; ++qt) {
+                        f32x4 c = zero4();
+#pragma unroll
+                        for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], qf[qt][kc], c);
+                        s[t][qt] = c;
+                    }
+                    Pol::lds_row_frags(a, sV[cur], n, g);
+#pragma unroll
+                    for (int qt = 0; qt < 2; ++qt) {
+                        f32x4 c = zero4();
+#pragma unroll
+                        for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], dof[qt][kc], c);
+                        dp[t][qt] = c;
+                    }
+                }
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt) {
+                    const int qi = q0 + 16 * qt + l16;
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            float pv = fast_exp2(s[t][qt][r] * p.scale_log2 - L2[qt]);
+                            if (need_mask) {
+                                const int key = k0 + 32 * blk + Pol::bidx(t, g, r);
+                                if (key >= N || (CAUSAL && key > qi)) pv = 0.f;
+                            }
+                            s[t][qt][r] = pv * (dp[t][qt][r] - Dl[qt]);  // dS / scale
+                        }
+                    }
+                }
+                const T *src = Pol::kColForm ? sKt[cur] : sK[cur];
+#pragma unroll
+                for (int xt = 0; xt < XT; ++xt) {
+#pragma unroll
+                    for (int qt = 0; qt < 2; ++qt) {
+                        acc[xt][qt] = Pol::chain(acc[xt][qt], s[0][qt], s[1][qt], src, 16 * xt + l16, 32 * blk, g);
+                    }
+                }
+            }
+        }
+        if (has_next) store_stage(cur ^ 1);
+        __syncthreads();
+    }
+
+    T *dQ = static_cast<T *>(p.dq) + (size_t)bh * N * D;
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        const int qi = q0 + 16 * qt + l16;
+        if (qi < N) {
+#pragma unroll
+            for (int xt = 0; xt < XT; ++xt) store4<T>(dQ + (size_t)qi * D + 16 * xt + 4 * g, acc[xt][qt], p.scale);
+        }
+    }
+}
+
+// ---------------------------------------------------------------- dK/dV pass
+
+template <class Pol, int KT, bool CAUSAL>
+__global__ __launch_bounds__(256) void dkv_kernel(Params p) {
+    using T = typename Pol::T;
+    using Frag = typename Pol::Frag;
+    constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
+    constexpr int BKV = 64 * KT;  // keys per workgroup
+    constexpr int BQ = 64;        // queries per stage
+    using SB = StageBlock<Pol>;
+    static_assert(2 * SB::PER_TILE <= 256, "one stage block per thread");
+    static_assert(BKV % BQ == 0, "causal start must align to a stage");
+
+    __shared__ __attribute__((aligned(16))) T sQ[2][BQ * D];
+    __shared__ __attribute__((aligned(16))) T sdO[2][BQ * D];
+    __shared__ __attribute__((aligned(16))) T sQt[Pol::kColForm ? 2 : 1][Pol::kColForm ? D * BQ : 8];
+    __shared__ __attribute__((aligned(16))) T sdOt[Pol::kColForm ? 2 : 1][Pol::kColForm ? D * BQ : 8];
+    __shared__ __attribute__((aligned(16))) float sL[2][BQ];
+    __shared__ __attribute__((aligned(16))) float sD[2][BQ];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int g = lane >> 4, l16 = lane & 15;
+    const int N = p.N;
+    const int bkv = blockIdx.x;  // b * Hkv + kvh
+    const int kb = blockIdx.y;   // causal: block 0 (most queries) is dispatched first
+    const int b = bkv / p.Hkv, kvh = bkv % p.Hkv;
+    const size_t kvoff = (size_t)bkv * N * D;
+    const T *K = static_cast<const T *>(p.k) + kvoff;
+    const T *V = static_cast<const T *>(p.v) + kvoff;
+    const int kw0 = kb * BKV + wave * 16 * KT;  // first key of this wave
+
+    Frag kf[KT][NC], vf[KT][NC];
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+        const int key = kw0 + 16 * kt + l16;
+        Pol::gmem_row_frags(kf[kt], K + (size_t)key * D, g, key < N);
+        Pol::gmem_row_frags(vf[kt], V + (size_t)key * D, g, key < N);
+    }
+    f32x4 accK[XT][KT], accV[XT][KT];
+#pragma unroll
+    for (int xt = 0; xt < XT; ++xt) {
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) accK[xt][kt] = accV[xt][kt] = zero4();
+    }
+
+    const int qstart = CAUSAL ? kb * BKV : 0;
+    const int nqs = (N - qstart + BQ - 1) / BQ;  // stages per query head
+    const int nsteps = nqs * p.group;
+
+    SB sb;
+    const bool stage_q = tid < SB::PER_TILE;
+    const bool stage_do = !stage_q && tid < 2 * SB::PER_TILE;
+    const int sbid = stage_q ? tid : tid - SB::PER_TILE;
+    float lval = 0.f;  // LSE*log2e (thread tid < BQ) or Delta (BQ <= tid < 2BQ) of the next stage
+    auto step_head = [&](int st) { return (size_t)b * p.Hq + (size_t)kvh * p.group + st / nqs; };
+    auto step_q0 = [&](int st) { return qstart + (st % nqs) * BQ; };
+    auto load_stage = [&](int st) {
+        const size_t bh = step_head(st);
+        const int qs = step_q0(st);
+        const size_t off = (bh * N + qs) * D;
+        if (stage_q) sb.load(static_cast<const T *>(p.q) + off, N - qs, sbid);
+        if (stage_do) sb.load(static_cast<const T *>(p.dout) + off, N - qs, sbid);
+        if (tid < BQ) {
+            const int qi = qs + tid;
+            lval = qi < N ? p.lse[bh * N + qi] * kLog2e : INFINITY;  // padded rows: p = 0
+        } else if (tid < 2 * BQ) {
+            const int qi = qs + tid - BQ;
+            lval = qi < N ? p.delta[bh * N + qi] : 0.f;
+        }
+    };
+    auto store_stage = [&](int buf) {
+        if (stage_q) {
+            sb.store_row(sQ[buf], sbid);
+            if constexpr (Pol::kColForm) sb.store_col(sQt[buf], sbid);
+        }
+        if (stage_do) {
+            sb.store_row(sdO[buf], sbid);
+            if constexpr (Pol::kColForm) sb.store_col(sdOt[buf], sbid);
+        }
+        if (tid < BQ) {
+            sL[buf][tid] = lval;
+        } else if (tid < 2 * BQ) {
+            sD[buf][tid - BQ] = lval;
+        }
+    };
+
+    if (nsteps > 0) {
+        load_stage(0);
+        store_stage(0);
+    }
+    __syncthreads();
+
+    for (int st = 0; st < nsteps; ++st) {
+        const int cur = st & 1;
+        const bool has_next = st + 1 < nsteps;
+        if (has_next) load_stage(st + 1);
+        const int qs = step_q0(st);
+        const bool active = !CAUSAL || qs + BQ - 1 >= kw0;
+        if (active) {
+            const bool need_mask = CAUSAL && qs < kw0 + 16 * KT - 1;
+            const T *srcQ = Pol::kColForm ? sQt[cur] : sQ[cur];
+            const T *srcdO = Pol::kColForm ? sdOt[cur] : sdO[cur];
+#pragma unroll
+            for (int blk = 0; blk < 2; ++blk) {
+                f32x4 s[2][KT], dp[2][KT];  // [t][kt]
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    Frag a[NC];
+                    const int n = 32 * blk + Pol::arow(t, l16);
+                    Pol::lds_row_frags(a, sQ[cur], n, g);
+#pragma unroll
+                    for (int kt = 0; kt < KT; ++kt) {
+                        f32x4 c = zero4();
+#pragma unroll
+                        for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], kf[kt][kc], c);
+                        s[t][kt] = c;
+                    }
+                    Pol::lds_row_frags(a, sdO[cur], n, g);
+#pragma unroll
+                    for (int kt = 0; kt < KT; ++kt) {
+                        f32x4 c = zero4();
+#pragma unroll
+                        for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], vf[kt][kc], c);
+                        dp[t][kt] = c;
+                    }
+                }
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int qloc = 32 * blk + Pol::bidx(t, g, r);
+                        const float L = sL[cur][qloc];
+                        const float Dv = sD[cur][qloc];
+#pragma unroll
+                        for (int kt = 0; kt < KT; ++kt) {
+                            float pv = fast_exp2(s[t][kt][r] * p.scale_log2 - L);
+                            if (need_mask) {
+                                const int key = kw0 + 16 * kt + l16;
+                                if (qs + qloc < key) pv = 0.f;
+                            }
+                            s[t][kt][r] = pv;
+                            dp[t][kt][r] = pv * (dp[t][kt][r] - Dv);  // dS / scale
+                        }
+                    }
+                }
+#pragma unroll
+                for (int xt = 0; xt < XT; ++xt) {
+#pragma unroll
+                    for (int kt = 0; kt < KT; ++kt) {
+                        accV[xt][kt] = Pol::chain(accV[xt][kt], s[0][kt], s[1][kt], srcdO, 16 * xt + l16, 32 * blk, g);
+                        accK[xt][kt] = Pol::chain(accK[xt][kt], dp[0][kt], dp[1][kt], srcQ, 16 * xt + l16, 32 * blk, g);
+                    }
+                }
+            }
+        }
+        if (has_next) store_stage(cur ^ 1);
+        __syncthreads();
+    }
+
+    T *dK = static_cast<T *>(p.dk) + kvoff;
+    T *dV = static_cast<T *>(p.dv) + kvoff;
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+        const int key = kw0 + 16 * kt + l16;
+        if (key < N) {
+#pragma unroll
+            for (int xt = 0; xt < XT; ++xt) {
+                store4<T>(dK + (size_t)key * D + 16 * xt + 4 * g, accK[xt][kt], p.scale);
+                store4<T>(dV + (size_t)key * D + 16 * xt + 4 * g, accV[xt][kt], 1.0f);
+            }
+        }
+    }
+}
+
+// ----------------------------------------------------------------- launchers
+
+hipError_t launch_preprocess(const Params &p, int dtype_bf16, int d, hipStream_t stream) {
+    const long rows = (long)p.B * p.Hq * p.N;
+    const dim3 grid((unsigned)((rows * 8 + 255) / 256));
+    if (dtype_bf16) {
+        if (d == 64) hipLaunchKernelGGL((preprocess_kernel<u16, 64>), grid, dim3(256), 0, stream,
+                                        static_cast<const u16 *>(p.dout), static_cast<const u16 *>(p.o_in), p.delta, rows);
+        else if (d == 128) hipLaunchKernelGGL((preprocess_kernel<u16, 128>), grid, dim3(256), 0, stream,
+                                              static_cast<const u16 *>(p.dout), static_cast<const u16 *>(p.o_in), p.delta, rows);
+        else return hipErrorInvalidValue;
+    } else {
+        if (d == 64) hipLaunchKernelGGL((preprocess_kernel<float, 64>), grid, dim3(256), 0, stream,
+                                        static_cast<const float *>(p.dout), static_cast<const float *>(p.o_in), p.delta, rows);
+        else return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <class Pol, bool CAUSAL>
+static hipError_t launch_dq_t(const Params &p, hipStream_t stream) {
+    const dim3 grid(p.B * p.Hq, (p.N + 127) / 128);
+    hipLaunchKernelGGL((dq_kernel<Pol, CAUSAL>), grid, dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_bwd_dq(const Params &p, int dtype_bf16, int d, int causal, hipStream_t stream) {
+#define MXFA_DQ(POL, DD)                                                        \
+    if (d == DD) return causal ? launch_dq_t<POL<DD>, true>(p, stream)         \
+                               : launch_dq_t<POL<DD>, false>(p, stream);
+    if (dtype_bf16) {
+        MXFA_DQ(PolBF16, 64)
+        MXFA_DQ(PolBF16, 128)
+    } else {
+        MXFA_DQ(PolF32, 64)
+    }
+#undef MXFA_DQ
+    return hipErrorInvalidValue;
+}
+
+template <class Pol, int KT, bool CAUSAL>
+static hipError_t launch_dkv_t(const Params &p, hipStream_t stream) {
+    const dim3 grid(p.B * p.Hkv, (p.N + 64 * KT - 1) / (64 * KT));
+    hipLaunchKernelGGL((dkv_kernel<Pol, KT, CAUSAL>), grid, dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_bwd_dkv(const Params &p, int dtype_bf16, int d, int causal, hipStream_t stream) {
+#define MXFA_DKV(POL, DD, KT)                                                          \
+    if (d == DD) return causal ? launch_dkv_t<POL<DD>, KT, true>(p, stream)           \
+                               : launch_dkv_t<POL<DD>, KT, false>(p, stream);
+    if (dtype_bf16) {
+        MXFA_DKV(PolBF16, 64, 2)
+        MXFA_DKV(PolBF16, 128, 1)
+    } else {
+        MXFA_DKV(PolF32, 64, 2)
+    }
+#undef MXFA_DKV
+    return hipErrorInvalidValue;
+}
+
+}  // namespace mxfa

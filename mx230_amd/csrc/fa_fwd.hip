@@ -1,0 +1,200 @@
+// Flash-attention forward for gfx950: O = softmax(Q K^T * scale) V and the
+// per-row log-sum-exp, one pass over K/V with an online softmax.
+//
+// Follows the algorithm of attention_flash.cu:17-89 (online softmax, causal
+// tile break, LSE = m + ln l at :85-87), re-tiled for CDNA4:
+//   * workgroup = 4 waves = 128 queries of one (batch, head); each wave owns
+//     32 queries, whose Q rows sit in registers as MFMA B operands;
+//   * K/V advance 64 keys per stage through double-buffered LDS;
+//   * scores are computed transposed, S^T = K Q^T, so each lane owns one query
+//     column: the running max / sum stay per lane and only the max needs a
+//     cross-lane reduction (two permlane swaps);
+//   * the output is accumulated transposed, O^T = V^T P^T, so the per-query
+//     rescale factor is a per-lane scalar as well;
+//   * exponentials are base 2 with log2(e) folded into the scale.
+#include "fa_device.h"
+#include "fa_launch.h"
+
+namespace mxfa {
+
+template <class Pol, bool CAUSAL>
+__global__ __launch_bounds__(256) void fwd_kernel(Params p) {
+    using T = typename Pol::T;
+    using Frag = typename Pol::Frag;
+    constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
+    constexpr int BQ = 128, BK = 64;
+    using SB = StageBlock<Pol>;
+    static_assert(2 * SB::PER_TILE <= 256, "one stage block per thread");
+
+    __shared__ __attribute__((aligned(16))) T sK[2][BK * D];
+    __shared__ __attribute__((aligned(16))) T sV[2][BK * D];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int g = lane >> 4, l16 = lane & 15;
+    const int N = p.N;
+    const int bh = blockIdx.x;
+    const int nqb = (N + BQ - 1) / BQ;
+    const int qb = CAUSAL ? (nqb - 1 - (int)blockIdx.y) : (int)blockIdx.y;  // heaviest first
+    const int b = bh / p.Hq, h = bh % p.Hq, kvh = h / p.group;
+    const T *Q = static_cast<const T *>(p.q) + (size_t)bh * N * D;
+    const size_t kvoff = ((size_t)b * p.Hkv + kvh) * N * D;
+    const T *K = static_cast<const T *>(p.k) + kvoff;
+    const T *V = static_cast<const T *>(p.v) + kvoff;
+    const int q0 = qb * BQ + wave * 32;
+
+    Frag qf[2][NC];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        const int qi = q0 + 16 * qt + l16;
+        Pol::gmem_row_frags(qf[qt], Q + (size_t)qi * D, g, qi < N);
+    }
+    f32x4 acc[XT][2];
+#pragma unroll
+    for (int xt = 0; xt < XT; ++xt) acc[xt][0] = acc[xt][1] = zero4();
+    float m[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.f, 0.f};
+
+    const int kend = CAUSAL ? min(N, qb * BQ + BQ) : N;
+    const int nsteps = (kend + BK - 1) / BK;
+
+    // stage blocks: [0, PER_TILE) -> K (row form), [PER_TILE, 2 PER_TILE) -> V
+    SB sb;
+    const bool stage_k = tid < SB::PER_TILE;
+    const bool stage_v = !stage_k && tid < 2 * SB::PER_TILE;
+    const int sbid = stage_k ? tid : tid - SB::PER_TILE;
+    auto load_stage = [&](int st) {
+        const int k0 = st * BK;
+        if (stage_k) sb.load(K + (size_t)k0 * D, N - k0, sbid);
+        if (stage_v) sb.load(V + (size_t)k0 * D, N - k0, sbid);
+    };
+    auto store_stage = [&](int buf) {
+        if (stage_k) sb.store_row(sK[buf], sbid);
+        if (stage_v) {
+            if constexpr (Pol::kColForm) {
+                sb.store_col(sV[buf], sbid);
+            } else {
+                sb.store_row(sV[buf], sbid);
+            }
+        }
+    };
+
+    load_stage(0);
+    store_stage(0);
+    __syncthreads();
+
+    for (int st = 0; st < nsteps; ++st) {
+        const int cur = st & 1;
+        const bool has_next = st + 1 < nsteps;
+        if (has_next) load_stage(st + 1);
+        const int k0 = st * BK;
+        const bool active = !CAUSAL || k0 <= q0 + 31;
+        if (active) {
+            f32x4 s[2][2][2];  // [block][t][qt]
+#pragma unroll
+            for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    Frag a[NC];
+                    Pol::lds_row_frags(a, sK[cur], 32 * blk + Pol::arow(t, l16), g);
+#pragma unroll
+                    for (int qt = 0; qt < 2; ++qt) {
+                        f32x4 c = zero4();
+#pragma unroll
+                        for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], qf[qt][kc], c);
+                        s[blk][t][qt] = c;
+                    }
+                }
+            }
+            const bool need_mask = (k0 + BK > N) || (CAUSAL && k0 + BK - 1 > q0);
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) {
+                const int qi = q0 + 16 * qt + l16;
+                float mx = -INFINITY;
+#pragma unroll
+                for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            float v = s[blk][t][qt][r] * p.scale_log2;
+                            if (need_mask) {
+                                const int key = k0 + 32 * blk + Pol::bidx(t, g, r);
+                                if (key >= N || (CAUSAL && key > qi)) v = -INFINITY;
+                            }
+                            s[blk][t][qt][r] = v;
+                            mx = fmaxf(mx, v);
+                        }
+                    }
+                }
+                mx = xg_max(mx);
+                const float mnew = fmaxf(m[qt], mx);
+                const float corr = fast_exp2(m[qt] - mnew);
+                m[qt] = mnew;
+                float ls = lsum[qt] * corr;
+#pragma unroll
+                for (int xt = 0; xt < XT; ++xt) acc[xt][qt] *= corr;
+#pragma unroll
+                for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const float pv = fast_exp2(s[blk][t][qt][r] - mnew);
+                            s[blk][t][qt][r] = pv;
+                            ls += pv;
+                        }
+                    }
+                }
+                lsum[qt] = ls;
+            }
+#pragma unroll
+            for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+                for (int xt = 0; xt < XT; ++xt) {
+#pragma unroll
+                    for (int qt = 0; qt < 2; ++qt) {
+                        acc[xt][qt] = Pol::chain(acc[xt][qt], s[blk][0][qt], s[blk][1][qt], sV[cur],
+                                                 16 * xt + l16, 32 * blk, g);
+                    }
+                }
+            }
+        }
+        if (has_next) store_stage(cur ^ 1);
+        __syncthreads();
+    }
+
+    T *O = static_cast<T *>(p.o) + (size_t)bh * N * D;
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        const int qi = q0 + 16 * qt + l16;
+        const float ltot = xg_sum(lsum[qt]);
+        const float inv = 1.0f / ltot;
+        if (qi < N) {
+#pragma unroll
+            for (int xt = 0; xt < XT; ++xt) store4<T>(O + (size_t)qi * D + 16 * xt + 4 * g, acc[xt][qt], inv);
+            if (p.lse != nullptr && g == 0) p.lse[(size_t)bh * N + qi] = (m[qt] + fast_log2(ltot)) * kLn2;
+        }
+    }
+}
+
+template <class Pol, bool CAUSAL>
+static hipError_t launch_fwd_t(const Params &p, hipStream_t stream) {
+    const dim3 grid(p.B * p.Hq, (p.N + 127) / 128);
+    hipLaunchKernelGGL((fwd_kernel<Pol, CAUSAL>), grid, dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_fwd(const Params &p, int dtype_bf16, int d, int causal, hipStream_t stream) {
+#define MXFA_FWD(POL, DD)                                                            \
+    if (d == DD) return causal ? launch_fwd_t<POL<DD>, true>(p, stream)            \
+                               : launch_fwd_t<POL<DD>, false>(p, stream);
+    if (dtype_bf16) {
+        MXFA_FWD(PolBF16, 64)
+        MXFA_FWD(PolBF16, 128)
+    } else {
+        MXFA_FWD(PolF32, 64)
+    }
+#undef MXFA_FWD
+    return hipErrorInvalidValue;
+}
+
+}  // namespace mxfa

@@ -1,0 +1,19 @@
+// Host-side launchers of the flash-attention kernels (internal to libmxfa).
+// Each returns hipSuccess or the launch error; shapes are validated by the
+// C ABI (mxfa_api.cpp) before any of these is called.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "fa_device.h"
+
+namespace mxfa {
+
+hipError_t launch_fwd(const Params &p, int dtype_bf16, int d, int causal, hipStream_t stream);
+hipError_t launch_preprocess(const Params &p, int dtype_bf16, int d, hipStream_t stream);
+hipError_t launch_bwd_dq(const Params &p, int dtype_bf16, int d, int causal, hipStream_t stream);
+hipError_t launch_bwd_dkv(const Params &p, int dtype_bf16, int d, int causal, hipStream_t stream);
+hipError_t launch_bwd_naive(const Params &p, int d, int causal, hipStream_t stream);
+hipError_t launch_naive_fwd(const Params &p, float *s, int d, int causal, hipStream_t stream);
+
+}  // namespace mxfa

@@ -1,0 +1,228 @@
+// C ABI of libmxfa (declared in include/mxfa.h): argument validation, the
+// mapping of mxfa_shape onto kernel parameters, and error translation. No
+// device memory is allocated and nothing synchronises here.
+#include "../../include/mxfa.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+
+#include "fa_launch.h"
+
+namespace {
+
+using mxfa::Params;
+
+constexpr long long kMaxGridY = 65535;
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_shape(const mxfa_shape *s) {
+    if (s == nullptr) return MXFA_ERR_NULL;
+    if (s->dtype != MXFA_F32 && s->dtype != MXFA_BF16) return MXFA_ERR_DTYPE;
+    if (s->B < 1 || s->Hq < 1 || s->Hkv < 1 || s->N < 1 || s->d < 1) return MXFA_ERR_SHAPE;
+    if (s->Hq % s->Hkv != 0) return MXFA_ERR_SHAPE;
+    if (s->causal != 0 && s->causal != 1) return MXFA_ERR_SHAPE;
+    if (!(s->scale >= 0.0f) || std::isinf(s->scale)) return MXFA_ERR_SHAPE;
+    // grid limits: x = B*H (32-bit), y = query/key blocks
+    const long long bh = (long long)s->B * s->Hq;
+    if (bh > 0x7fffffffLL) return MXFA_ERR_SHAPE;
+    if (((long long)s->N + 63) / 64 > kMaxGridY) return MXFA_ERR_SHAPE;
+    if (s->d != 64 && s->d != 128) return MXFA_ERR_UNSUPPORTED;
+    if (s->dtype == MXFA_F32 && s->d != 64) return MXFA_ERR_UNSUPPORTED;
+    return MXFA_OK;
+}
+
+Params make_params(const mxfa_shape *s) {
+    Params p;
+    std::memset(&p, 0, sizeof(p));
+    p.B = s->B;
+    p.Hq = s->Hq;
+    p.Hkv = s->Hkv;
+    p.N = s->N;
+    p.group = s->Hq / s->Hkv;
+    p.scale = s->scale > 0.0f ? s->scale : 1.0f / std::sqrt((float)s->d);
+    p.scale_log2 = p.scale * mxfa::kLog2e;
+    return p;
+}
+
+int from_hip(hipError_t e) { return e == hipSuccess ? MXFA_OK : MXFA_ERR_LAUNCH; }
+
+int check_ptrs(std::initializer_list<const void *> ps) {
+    for (const void *p : ps) {
+        if (p == nullptr) return MXFA_ERR_NULL;
+    }
+    for (const void *p : ps) {
+        if (!aligned16(p)) return MXFA_ERR_ALIGN;
+    }
+    return MXFA_OK;
+}
+
+int fwd_impl(const mxfa_shape *shape, const void *q, const void *k, const void *v, void *o, float *lse,
+             bool want_lse, void *stream) {
+    int rc = check_shape(shape);
+    if (rc != MXFA_OK) return rc;
+    rc = want_lse ? check_ptrs({q, k, v, o, lse}) : check_ptrs({q, k, v, o});
+    if (rc != MXFA_OK) return rc;
+    Params p = make_params(shape);
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    p.o = o;
+    p.lse = want_lse ? lse : nullptr;
+    return from_hip(mxfa::launch_fwd(p, shape->dtype == MXFA_BF16, shape->d, shape->causal,
+                                     static_cast<hipStream_t>(stream)));
+}
+
+Params bwd_params(const mxfa_shape *shape, const void *q, const void *k, const void *v, const void *dout,
+                  const float *lse, const float *delta) {
+    Params p = make_params(shape);
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    p.dout = dout;
+    p.lse = const_cast<float *>(lse);
+    p.delta = const_cast<float *>(delta);
+    return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mxfa_version(void) { return 100; }
+
+const char *mxfa_strerror(int status) {
+    switch (status) {
+        case MXFA_OK: return "ok";
+        case MXFA_ERR_NULL: return "a required pointer is NULL";
+        case MXFA_ERR_SHAPE: return "invalid shape (B, Hq, Hkv, N, d, causal, scale or Hq % Hkv)";
+        case MXFA_ERR_DTYPE: return "unknown dtype";
+        case MXFA_ERR_UNSUPPORTED: return "no kernel for this shape (d must be 64 or 128; fp32 needs d = 64)";
+        case MXFA_ERR_ALIGN: return "a device pointer is not 16-byte aligned";
+        case MXFA_ERR_LAUNCH: return "the HIP runtime rejected a kernel launch";
+        case MXFA_ERR_DEVICE: return "no usable gfx950 device";
+        default: return "unknown status";
+    }
+}
+
+int mxfa_init(int device) {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count) return MXFA_ERR_DEVICE;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) return MXFA_ERR_DEVICE;
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return MXFA_ERR_DEVICE;
+    if (hipSetDevice(device) != hipSuccess) return MXFA_ERR_DEVICE;
+    return MXFA_OK;
+}
+
+int mxfa_shutdown(void) { return MXFA_OK; }
+
+int mxfa_check_shape(const mxfa_shape *shape) { return check_shape(shape); }
+
+int mxfa_run_flash(const mxfa_shape *shape, const void *q, const void *k, const void *v, void *o,
+                   void *stream) {
+    return fwd_impl(shape, q, k, v, o, nullptr, false, stream);
+}
+
+int mxfa_run_flash_lse(const mxfa_shape *shape, const void *q, const void *k, const void *v, void *o,
+                       float *lse, void *stream) {
+    return fwd_impl(shape, q, k, v, o, lse, true, stream);
+}
+
+int mxfa_run_preprocess(const mxfa_shape *shape, const void *dout, const void *o, float *delta, void *stream) {
+    int rc = check_shape(shape);
+    if (rc != MXFA_OK) return rc;
+    rc = check_ptrs({dout, o, delta});
+    if (rc != MXFA_OK) return rc;
+    Params p = make_params(shape);
+    p.dout = dout;
+    p.o_in = o;
+    p.delta = delta;
+    return from_hip(mxfa::launch_preprocess(p, shape->dtype == MXFA_BF16, shape->d,
+                                            static_cast<hipStream_t>(stream)));
+}
+
+int mxfa_run_bwd_dq(const mxfa_shape *shape, const void *q, const void *k, const void *v, const void *dout,
+                    const float *lse, const float *delta, void *dq, void *stream) {
+    int rc = check_shape(shape);
+    if (rc != MXFA_OK) return rc;
+    rc = check_ptrs({q, k, v, dout, lse, delta, dq});
+    if (rc != MXFA_OK) return rc;
+    Params p = bwd_params(shape, q, k, v, dout, lse, delta);
+    p.dq = dq;
+    return from_hip(mxfa::launch_bwd_dq(p, shape->dtype == MXFA_BF16, shape->d, shape->causal,
+                                        static_cast<hipStream_t>(stream)));
+}
+
+int mxfa_run_bwd_dkv(const mxfa_shape *shape, const void *q, const void *k, const void *v, const void *dout,
+                     const float *lse, const float *delta, void *dk, void *dv, void *stream) {
+    int rc = check_shape(shape);
+    if (rc != MXFA_OK) return rc;
+    rc = check_ptrs({q, k, v, dout, lse, delta, dk, dv});
+    if (rc != MXFA_OK) return rc;
+    Params p = bwd_params(shape, q, k, v, dout, lse, delta);
+    p.dk = dk;
+    p.dv = dv;
+    return from_hip(mxfa::launch_bwd_dkv(p, shape->dtype == MXFA_BF16, shape->d, shape->causal,
+                                         static_cast<hipStream_t>(stream)));
+}
+
+int mxfa_run_bwd_flash(const mxfa_shape *shape, const void *q, const void *k, const void *v,
+                       const void *dout, const float *lse, const float *delta, void *dq, void *dk, void *dv,
+                       void *stream) {
+    int rc = check_shape(shape);
+    if (rc != MXFA_OK) return rc;
+    rc = check_ptrs({q, k, v, dout, lse, delta, dq, dk, dv});
+    if (rc != MXFA_OK) return rc;
+    rc = mxfa_run_bwd_dkv(shape, q, k, v, dout, lse, delta, dk, dv, stream);
+    if (rc != MXFA_OK) return rc;
+    return mxfa_run_bwd_dq(shape, q, k, v, dout, lse, delta, dq, stream);
+}
+
+size_t mxfa_bwd_workspace_bytes(const mxfa_shape *shape) {
+    (void)shape;
+    return 0;
+}
+
+int mxfa_run_bwd_naive(const mxfa_shape *shape, const void *q, const void *k, const void *v,
+                       const void *dout, const float *lse, const float *delta, void *dq, void *dk, void *dv,
+                       void *stream) {
+    int rc = check_shape(shape);
+    if (rc != MXFA_OK) return rc;
+    if (shape->dtype != MXFA_F32) return MXFA_ERR_UNSUPPORTED;
+    rc = check_ptrs({q, k, v, dout, lse, delta, dq, dk, dv});
+    if (rc != MXFA_OK) return rc;
+    if ((long long)shape->B * shape->Hq > kMaxGridY) return MXFA_ERR_SHAPE;
+    Params p = bwd_params(shape, q, k, v, dout, lse, delta);
+    p.dq = dq;
+    p.dk = dk;
+    p.dv = dv;
+    return from_hip(mxfa::launch_bwd_naive(p, shape->d, shape->causal, static_cast<hipStream_t>(stream)));
+}
+
+size_t mxfa_naive_scratch_bytes(const mxfa_shape *shape) {
+    if (check_shape(shape) != MXFA_OK) return 0;
+    return (size_t)shape->B * shape->Hq * (size_t)shape->N * (size_t)shape->N * sizeof(float);
+}
+
+int mxfa_run_naive_fwd(const mxfa_shape *shape, const void *q, const void *k, const void *v, float *s, void *o,
+                       void *stream) {
+    int rc = check_shape(shape);
+    if (rc != MXFA_OK) return rc;
+    if (shape->dtype != MXFA_F32) return MXFA_ERR_UNSUPPORTED;
+    rc = check_ptrs({q, k, v, s, o});
+    if (rc != MXFA_OK) return rc;
+    if ((long long)shape->B * shape->Hq > kMaxGridY) return MXFA_ERR_SHAPE;
+    if (((long long)shape->N + 15) / 16 > kMaxGridY) return MXFA_ERR_SHAPE;
+    Params p = make_params(shape);
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    p.o = o;
+    return from_hip(mxfa::launch_naive_fwd(p, s, shape->d, shape->causal, static_cast<hipStream_t>(stream)));
+}
+
+}  // extern "C"

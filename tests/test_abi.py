@@ -1,0 +1,125 @@
+"""CPU-side checks of the C ABI (no GPU needed, no compute launched): the library
+loads, exports every entry point include/mxfa.h declares, and rejects bad
+arguments with the documented status codes before touching the device."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+import mx230_amd as mx
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mxfa.h")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(mx.LIB_PATH):
+        subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "mx230_amd", "csrc")], check=True)
+    return mx.load_library()
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(mxfa_[a-z_]+)\s*\(", text)))
+
+
+def test_header_and_python_agree():
+    assert sorted(mx.EXPORTS) == _declared()
+
+
+def test_every_declared_symbol_is_exported(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", mx.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (mxfa_\w+)", out))
+    for name in _declared():
+        assert name in exported, name
+        assert hasattr(lib, name)
+
+
+def _shape(**kw):
+    base = dict(B=1, Hq=2, Hkv=1, N=128, d=64, causal=1, dtype=mx.MXFA_BF16, scale=0.0)
+    base.update(kw)
+    return mx.MxfaShape(**base)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(), 0),
+    (dict(dtype=7), -3),
+    (dict(B=0), -2),
+    (dict(N=0), -2),
+    (dict(Hq=3, Hkv=2), -2),
+    (dict(causal=2), -2),
+    (dict(scale=-1.0), -2),
+    (dict(scale=float("inf")), -2),
+    (dict(d=96), -4),
+    (dict(d=128, dtype=mx.MXFA_F32), -4),
+    (dict(d=128), 0),
+    (dict(N=64 * 65536), -2),
+])
+def test_check_shape(lib, kw, code):
+    assert lib.mxfa_check_shape(ctypes.byref(_shape(**kw))) == code
+
+
+def test_null_shape_and_pointers(lib):
+    assert lib.mxfa_check_shape(None) == -1
+    sh = _shape()
+    p = ctypes.c_void_p(4096)
+    assert lib.mxfa_run_flash_lse(ctypes.byref(sh), p, p, p, None, p, None) == -1
+    assert lib.mxfa_run_flash_lse(None, p, p, p, p, p, None) == -1
+    assert lib.mxfa_run_bwd_flash(ctypes.byref(sh), p, p, p, p, p, p, p, None, p, None) == -1
+    assert lib.mxfa_run_preprocess(ctypes.byref(sh), None, p, p, None) == -1
+
+
+def test_misaligned_pointer(lib):
+    sh = _shape()
+    ok, bad = ctypes.c_void_p(4096), ctypes.c_void_p(4096 + 8)
+    assert lib.mxfa_run_flash(ctypes.byref(sh), ok, bad, ok, ok, None) == -5
+    assert lib.mxfa_run_bwd_dkv(ctypes.byref(sh), ok, ok, ok, ok, ok, ok, ok, bad, None) == -5
+
+
+def test_naive_paths_are_fp32_only(lib):
+    sh = _shape(dtype=mx.MXFA_BF16)
+    p = ctypes.c_void_p(4096)
+    assert lib.mxfa_run_bwd_naive(ctypes.byref(sh), p, p, p, p, p, p, p, p, p, None) == -4
+    assert lib.mxfa_run_naive_fwd(ctypes.byref(sh), p, p, p, p, p, None) == -4
+
+
+def test_sizes_and_strings(lib):
+    sh = _shape(B=2, Hq=3, Hkv=3, N=100, dtype=mx.MXFA_F32)
+    assert lib.mxfa_bwd_workspace_bytes(ctypes.byref(sh)) == 0
+    assert lib.mxfa_naive_scratch_bytes(ctypes.byref(sh)) == 2 * 3 * 100 * 100 * 4
+    assert lib.mxfa_version() >= 100
+    for code in mx.STATUS:
+        assert lib.mxfa_strerror(code)
+    assert lib.mxfa_strerror(12345) == b"unknown status"
+    assert lib.mxfa_shutdown() == 0
+
+
+def test_python_layer_rejects_host_tensors():
+    import torch
+    q = torch.zeros(1, 1, 16, 64)
+    with pytest.raises(ValueError, match="device tensor"):
+        mx.run_flash(q, q, q, torch.zeros_like(q), causal=False)
+    with pytest.raises(ValueError):
+        mx.shape_of(torch.zeros(16, 64, dtype=torch.float16), torch.zeros(16, 64, dtype=torch.float16), False)
+
+
+def test_product_never_touches_the_oracle():
+    """The checker (oracle/) is test infrastructure: the package must not
+    import, load or call it."""
+    pkg = os.path.join(ROOT, "mx230_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".cpp", ".h", "Makefile")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert "oracle" not in text.lower(), os.path.join(dirpath, f)
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(ImportError, match="no fallback"):
+        mx.load_library(str(tmp_path / "libmxfa.so"))
