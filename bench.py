@@ -44,7 +44,23 @@ def parse():
     ap.add_argument("--causal", type=int, default=1)
     ap.add_argument("--dtype", choices=["bf16", "f32"], default="bf16")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="instead of the benchmark, run a plain device-to-device copy of MIB "
+                         "MiB three times (calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     return ap.parse_args()
+
+
+def copy_probe(mib):
+    """A plain copy kernel of known size: reads and writes exactly mib MiB per
+    launch, so FETCH_SIZE / WRITE_SIZE read for it give the counters' scale."""
+    import torch
+    n = mib * (1 << 20) // 4
+    x = torch.ones(n, device="cuda", dtype=torch.float32)
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_per_launch": n * 4, "launches": 3}), flush=True)
 
 
 def cpu_baseline(a, hkv):
@@ -80,6 +96,9 @@ def cpu_baseline(a, hkv):
 
 def main():
     a = parse()
+    if a.copy_probe:
+        copy_probe(a.copy_probe)
+        return
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {a.gpus}); the path shards "
               "over (batch, KV head) with no exchange, so the one-GPU figure is the per-GPU "

@@ -71,6 +71,13 @@ def load_library(path: str | None = None):
     if path is None and _lib is not None:
         return _lib
     p = path or LIB_PATH
+    # torch first: libmxfa then binds to the HIP runtime torch already loaded, so
+    # the device pointers and streams it receives from torch are valid for it
+    # (loading libmxfa first would pull in a second HIP runtime)
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     if not os.path.exists(p):
         raise ImportError(f"{p} is missing: build it with `make -C mx230_amd/csrc` "
                           "(or __graft_entry__.build()); there is no fallback path")

@@ -12,7 +12,8 @@
 //   * dkv_kernel: a workgroup owns 64*KT keys of one (batch, KV head); each of
 //     its 4 waves owns 16*KT keys whose K/V rows sit in registers and whose
 //     dK/dV accumulate in registers. Q/dO/LSE/Delta stream through
-//     double-buffered LDS, 64 queries per stage, for every query head of the
+//     double-buffered LDS (direct global->LDS loads issued one stage ahead),
+//     64 queries per stage, for every query head of the
 //     KV head's group in turn, so the grouped-query reduction of dK/dV happens
 //     inside the kernel with no atomics and no extra memory.
 //   * dq_kernel: a workgroup owns 128 queries of one (batch, query head) (32
@@ -23,6 +24,10 @@
 #include "fa_launch.h"
 
 namespace mxfa {
+
+#ifndef MXFA_DKV_WPE
+#define MXFA_DKV_WPE 1
+#endif
 
 // ------------------------------------------------------------ preprocess
 
@@ -68,6 +73,20 @@ __global__ __launch_bounds__(256) void preprocess_kernel(const T *dout, const T 
     if (row < rows && part == 0) delta[row] = acc;
 }
 
+// One dK/dV stage: BQ query rows (from qs) of Q and dO of head bh, and their
+// LSE and Delta, into LDS buffers.
+template <class Pol, int BQ>
+__device__ __forceinline__ void stage_qdo(typename Pol::T *sq, typename Pol::T *sdo, float *sl, float *sd,
+                                          const Params &p, size_t bh, int qs, int N, int tid, int wave,
+                                          int lane) {
+    using T = typename Pol::T;
+    const size_t off = (bh * N + qs) * Pol::D;
+    stage_rows<Pol, BQ>(sq, static_cast<const T *>(p.q) + off, N - qs, tid, wave);
+    stage_rows<Pol, BQ>(sdo, static_cast<const T *>(p.dout) + off, N - qs, tid, wave);
+    if (wave == 0) stage_vec64(sl, p.lse + bh * N + qs, N - qs, lane);
+    if (wave == 1) stage_vec64(sd, p.delta + bh * N + qs, N - qs, lane);
+}
+
 // ------------------------------------------------------------------ dQ pass
 
 template <class Pol, bool CAUSAL>
@@ -76,14 +95,12 @@ __global__ __launch_bounds__(256) void dq_kernel(Params p) {
     using Frag = typename Pol::Frag;
     constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
     constexpr int BQ = 128, BK = 64;
-    using SB = StageBlock<Pol>;
-    static_assert(2 * SB::PER_TILE <= 256, "one stage block per thread");
 
     __shared__ __attribute__((aligned(16))) T sK[2][BK * D];
     __shared__ __attribute__((aligned(16))) T sV[2][BK * D];
-    __shared__ __attribute__((aligned(16))) T sKt[Pol::kColForm ? 2 : 1][Pol::kColForm ? D * BK : 8];
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, l16 = lane & 15;
     const int N = p.N;
     const int bh = blockIdx.x;
@@ -115,31 +132,13 @@ __global__ __launch_bounds__(256) void dq_kernel(Params p) {
     const int kend = CAUSAL ? min(N, qb * BQ + BQ) : N;
     const int nsteps = (kend + BK - 1) / BK;
 
-    SB sb;
-    const bool stage_k = tid < SB::PER_TILE;
-    const bool stage_v = !stage_k && tid < 2 * SB::PER_TILE;
-    const int sbid = stage_k ? tid : tid - SB::PER_TILE;
-    auto load_stage = [&](int st) {
-        const int k0 = st * BK;
-        if (stage_k) sb.load(K + (size_t)k0 * D, N - k0, sbid);
-        if (stage_v) sb.load(V + (size_t)k0 * D, N - k0, sbid);
-    };
-    auto store_stage = [&](int buf) {
-        if (stage_k) {
-            sb.store_row(sK[buf], sbid);
-            if constexpr (Pol::kColForm) sb.store_col(sKt[buf], sbid);
-        }
-        if (stage_v) sb.store_row(sV[buf], sbid);
-    };
-
-    load_stage(0);
-    store_stage(0);
+    stage_kv<Pol, BK>(sK[0], sV[0], K, V, 0, N, tid, wave);
+    wait_stage();
     __syncthreads();
 
     for (int st = 0; st < nsteps; ++st) {
         const int cur = st & 1;
-        const bool has_next = st + 1 < nsteps;
-        if (has_next) load_stage(st + 1);
+        if (st + 1 < nsteps) stage_kv<Pol, BK>(sK[cur ^ 1], sV[cur ^ 1], K, V, (st + 1) * BK, N, tid, wave);
         const int k0 = st * BK;
         const bool active = !CAUSAL || k0 <= q0 + 31;
         if (active) {
@@ -184,17 +183,16 @@ __global__ __launch_bounds__(256) void dq_kernel(Params p) {
                         }
                     }
                 }
-                const T *src = Pol::kColForm ? sKt[cur] : sK[cur];
 #pragma unroll
                 for (int xt = 0; xt < XT; ++xt) {
 #pragma unroll
                     for (int qt = 0; qt < 2; ++qt) {
-                        acc[xt][qt] = Pol::chain(acc[xt][qt], s[0][qt], s[1][qt], src, 16 * xt + l16, 32 * blk, g);
+                        acc[xt][qt] = Pol::chain(acc[xt][qt], s[0][qt], s[1][qt], sK[cur], 16 * xt, 32 * blk, g, l16);
                     }
                 }
             }
         }
-        if (has_next) store_stage(cur ^ 1);
+        wait_stage();
         __syncthreads();
     }
 
@@ -212,24 +210,21 @@ __global__ __launch_bounds__(256) void dq_kernel(Params p) {
 // ---------------------------------------------------------------- dK/dV pass
 
 template <class Pol, int KT, bool CAUSAL>
-__global__ __launch_bounds__(256) void dkv_kernel(Params p) {
+__global__ __launch_bounds__(256, MXFA_DKV_WPE) void dkv_kernel(Params p) {
     using T = typename Pol::T;
     using Frag = typename Pol::Frag;
     constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
     constexpr int BKV = 64 * KT;  // keys per workgroup
     constexpr int BQ = 64;        // queries per stage
-    using SB = StageBlock<Pol>;
-    static_assert(2 * SB::PER_TILE <= 256, "one stage block per thread");
     static_assert(BKV % BQ == 0, "causal start must align to a stage");
 
     __shared__ __attribute__((aligned(16))) T sQ[2][BQ * D];
     __shared__ __attribute__((aligned(16))) T sdO[2][BQ * D];
-    __shared__ __attribute__((aligned(16))) T sQt[Pol::kColForm ? 2 : 1][Pol::kColForm ? D * BQ : 8];
-    __shared__ __attribute__((aligned(16))) T sdOt[Pol::kColForm ? 2 : 1][Pol::kColForm ? D * BQ : 8];
     __shared__ __attribute__((aligned(16))) float sL[2][BQ];
     __shared__ __attribute__((aligned(16))) float sD[2][BQ];
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, l16 = lane & 15;
     const int N = p.N;
     const int bkv = blockIdx.x;  // b * Hkv + kvh
@@ -258,59 +253,24 @@ __global__ __launch_bounds__(256) void dkv_kernel(Params p) {
     const int nqs = (N - qstart + BQ - 1) / BQ;  // stages per query head
     const int nsteps = nqs * p.group;
 
-    SB sb;
-    const bool stage_q = tid < SB::PER_TILE;
-    const bool stage_do = !stage_q && tid < 2 * SB::PER_TILE;
-    const int sbid = stage_q ? tid : tid - SB::PER_TILE;
-    float lval = 0.f;  // LSE*log2e (thread tid < BQ) or Delta (BQ <= tid < 2BQ) of the next stage
-    auto step_head = [&](int st) { return (size_t)b * p.Hq + (size_t)kvh * p.group + st / nqs; };
-    auto step_q0 = [&](int st) { return qstart + (st % nqs) * BQ; };
-    auto load_stage = [&](int st) {
-        const size_t bh = step_head(st);
-        const int qs = step_q0(st);
-        const size_t off = (bh * N + qs) * D;
-        if (stage_q) sb.load(static_cast<const T *>(p.q) + off, N - qs, sbid);
-        if (stage_do) sb.load(static_cast<const T *>(p.dout) + off, N - qs, sbid);
-        if (tid < BQ) {
-            const int qi = qs + tid;
-            lval = qi < N ? p.lse[bh * N + qi] * kLog2e : INFINITY;  // padded rows: p = 0
-        } else if (tid < 2 * BQ) {
-            const int qi = qs + tid - BQ;
-            lval = qi < N ? p.delta[bh * N + qi] : 0.f;
-        }
-    };
-    auto store_stage = [&](int buf) {
-        if (stage_q) {
-            sb.store_row(sQ[buf], sbid);
-            if constexpr (Pol::kColForm) sb.store_col(sQt[buf], sbid);
-        }
-        if (stage_do) {
-            sb.store_row(sdO[buf], sbid);
-            if constexpr (Pol::kColForm) sb.store_col(sdOt[buf], sbid);
-        }
-        if (tid < BQ) {
-            sL[buf][tid] = lval;
-        } else if (tid < 2 * BQ) {
-            sD[buf][tid - BQ] = lval;
-        }
-    };
-
-    if (nsteps > 0) {
-        load_stage(0);
-        store_stage(0);
-    }
+    const size_t bh0 = (size_t)b * p.Hq + (size_t)kvh * p.group;
+    stage_qdo<Pol, BQ>(sQ[0], sdO[0], sL[0], sD[0], p, bh0, qstart, N, tid, wave, lane);
+    wait_stage();
     __syncthreads();
 
     for (int st = 0; st < nsteps; ++st) {
         const int cur = st & 1;
-        const bool has_next = st + 1 < nsteps;
-        if (has_next) load_stage(st + 1);
-        const int qs = step_q0(st);
+        if (st + 1 < nsteps) {
+            const int nx = st + 1;
+            stage_qdo<Pol, BQ>(sQ[cur ^ 1], sdO[cur ^ 1], sL[cur ^ 1], sD[cur ^ 1], p, bh0 + nx / nqs,
+                               qstart + (nx % nqs) * BQ, N, tid, wave, lane);
+        }
+        const int qs = qstart + (st % nqs) * BQ;
         const bool active = !CAUSAL || qs + BQ - 1 >= kw0;
         if (active) {
-            const bool need_mask = CAUSAL && qs < kw0 + 16 * KT - 1;
-            const T *srcQ = Pol::kColForm ? sQt[cur] : sQ[cur];
-            const T *srcdO = Pol::kColForm ? sdOt[cur] : sdO[cur];
+            // rows past N re-read row N-1 and must get p = 0; causal diagonal
+            // stages mask queries before the key
+            const bool need_mask = (qs + BQ > N) || (CAUSAL && qs < kw0 + 16 * KT - 1);
 #pragma unroll
             for (int blk = 0; blk < 2; ++blk) {
                 f32x4 s[2][KT], dp[2][KT];  // [t][kt]
@@ -340,14 +300,15 @@ __global__ __launch_bounds__(256) void dkv_kernel(Params p) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const int qloc = 32 * blk + Pol::bidx(t, g, r);
-                        const float L = sL[cur][qloc];
+                        const float L = sL[cur][qloc] * kLog2e;
                         const float Dv = sD[cur][qloc];
 #pragma unroll
                         for (int kt = 0; kt < KT; ++kt) {
                             float pv = fast_exp2(s[t][kt][r] * p.scale_log2 - L);
                             if (need_mask) {
                                 const int key = kw0 + 16 * kt + l16;
-                                if (qs + qloc < key) pv = 0.f;
+                                const int qi = qs + qloc;
+                                if (qi >= N || (CAUSAL && qi < key)) pv = 0.f;
                             }
                             s[t][kt][r] = pv;
                             dp[t][kt][r] = pv * (dp[t][kt][r] - Dv);  // dS / scale
@@ -358,13 +319,13 @@ __global__ __launch_bounds__(256) void dkv_kernel(Params p) {
                 for (int xt = 0; xt < XT; ++xt) {
 #pragma unroll
                     for (int kt = 0; kt < KT; ++kt) {
-                        accV[xt][kt] = Pol::chain(accV[xt][kt], s[0][kt], s[1][kt], srcdO, 16 * xt + l16, 32 * blk, g);
-                        accK[xt][kt] = Pol::chain(accK[xt][kt], dp[0][kt], dp[1][kt], srcQ, 16 * xt + l16, 32 * blk, g);
+                        accV[xt][kt] = Pol::chain(accV[xt][kt], s[0][kt], s[1][kt], sdO[cur], 16 * xt, 32 * blk, g, l16);
+                        accK[xt][kt] = Pol::chain(accK[xt][kt], dp[0][kt], dp[1][kt], sQ[cur], 16 * xt, 32 * blk, g, l16);
                     }
                 }
             }
         }
-        if (has_next) store_stage(cur ^ 1);
+        wait_stage();
         __syncthreads();
     }
 

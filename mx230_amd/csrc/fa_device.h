@@ -11,10 +11,10 @@
 //     g = l/16. For bf16 that puts rows 8g..8g+7 in one lane, which is exactly
 //     one k-slice of the next MFMA: the scores feed the next GEMM (P*V, dS*K,
 //     P^T*dO, dS^T*Q) straight from registers, no shuffle.
-//   * "Row form" LDS tiles are [n][D] (rows = keys or queries), 16-byte chunks
-//     XOR-swizzled per row. The bf16 chained GEMMs contract over n, so they also
-//     stage a transposed "col form" tile [D][64] (chunks swizzled per row);
-//     the fp32 chained GEMMs read the row form one element at a time.
+//   * LDS tiles are row form, [n][D] (rows = keys or queries), with 16-byte
+//     chunks XOR-swizzled per row. The chained GEMMs contract over n: bf16 reads
+//     their operand transposed with ds_read_b64_tr_b16, fp32 reads it one
+//     element at a time.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -68,6 +68,9 @@ __device__ __forceinline__ u16 to_bf16_bits(float x) {
 
 // ------------------------------------------------------------------ policies
 
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
 // bf16 inputs, fp32 accumulation: v_mfma_f32_16x16x32_bf16.
 template <int D_>
 struct PolBF16 {
@@ -76,19 +79,23 @@ struct PolBF16 {
     using Frag = bf16x8;
     static constexpr int EPC = 8;      // elements per 16-byte chunk
     static constexpr int NC = D / 32;  // MFMAs over D per first-GEMM tile
-    static constexpr bool kColForm = true;
 
     __device__ static __forceinline__ int arow(int t, int m) {
         return ((m >> 2) << 3) + (t << 2) + (m & 3);
     }
     __device__ static __forceinline__ int bidx(int t, int g, int r) { return (g << 3) + (t << 2) + r; }
-    // row-form swizzle: the 8 rows one ds_read_b128 phase touches (arow of
-    // m = 0..7 or 8..15) land in 8 distinct 16-byte bank groups
-    __device__ static __forceinline__ int rswz(int n) { return (n & 3) | ((n >> 1) & 4); }
-    __device__ static __forceinline__ int cswz(int y) { return (y ^ (y >> 3)) & 7; }
+    // Chunk swizzle of row-form tiles. Two read patterns must be conflict free:
+    // ds_read_b128 of one chunk from the 8 rows arow(t, 0..7) (or 8..15), and
+    // the transposing ds_read_b64_tr_b16 of 32 bytes from 4 consecutive rows.
+    // Bits 1-2 of the swizzle come from row bits 0-1 (4 consecutive rows hit 4
+    // different 32-byte pairs), bit 0 from row bit 3 (separates arow's halves).
+    __device__ static __forceinline__ int rswz(int n) { return ((n & 3) << 1) | ((n >> 3) & 1); }
 
     __device__ static __forceinline__ f32x4 mma(Frag a, Frag b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+    __device__ static __forceinline__ int lds_off(int row, int col) {
+        return row * D + ((((col >> 3) ^ rswz(row))) << 3) + (col & 7);
     }
     // k-slot (g, e) of MFMA c <-> element 32c + 8g + e of the row
     __device__ static __forceinline__ void lds_row_frags(Frag (&f)[NC], const T *tile, int n, int g) {
@@ -108,10 +115,14 @@ struct PolBF16 {
             }
         }
     }
-    // acc += Other[y][blk .. blk+31] * chain, where chain element (t, r) of this
-    // lane is block row bidx(t, g, r) and Other comes from the col-form tile.
+    // acc += Other * chain over the 32-row block starting at blk, where Other[y][n]
+    // = tile[n][y0 + y] is read transposed from the row-form tile with
+    // ds_read_b64_tr_b16 (lane (g, j) of a 16-lane group addresses row
+    // blk + 8g + 4h + j/4, columns y0 + 4(j%4)..+3, and receives column y0 + j
+    // of those 4 rows), and chain element (t, r) of this lane is block row
+    // bidx(t, g, r) = 8g + 4t + r: both sides use k-slot e <-> row blk + 8g + e.
     __device__ static __forceinline__ f32x4 chain(f32x4 acc, const f32x4 &c0, const f32x4 &c1,
-                                                  const T *col_tile, int y, int blk, int g) {
+                                                  const T *tile, int y0, int blk, int g, int l16) {
         Frag b;
         b[0] = (__bf16)c0[0];
         b[1] = (__bf16)c0[1];
@@ -121,9 +132,12 @@ struct PolBF16 {
         b[5] = (__bf16)c1[1];
         b[6] = (__bf16)c1[2];
         b[7] = (__bf16)c1[3];
-        const int chunk = (blk >> 3) + g;
-        const Frag a = *reinterpret_cast<const Frag *>(col_tile + y * 64 + ((chunk ^ cswz(y)) * EPC));
-        return mma(a, b, acc);
+        const int r0 = blk + 8 * g + (l16 >> 2);
+        const int col = y0 + 4 * (l16 & 3);
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(tile + lds_off(r0, col)));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(tile + lds_off(r0 + 4, col)));
+        const short __attribute__((ext_vector_type(8))) av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        return mma(__builtin_bit_cast(Frag, av), b, acc);
     }
 };
 
@@ -135,12 +149,10 @@ struct PolF32 {
     using Frag = float;
     static constexpr int EPC = 4;
     static constexpr int NC = D / 4;
-    static constexpr bool kColForm = false;
 
     __device__ static __forceinline__ int arow(int t, int m) { return (t << 4) + m; }
     __device__ static __forceinline__ int bidx(int t, int g, int r) { return (t << 4) + (g << 2) + r; }
     __device__ static __forceinline__ int rswz(int n) { return n & 7; }
-    __device__ static __forceinline__ int cswz(int) { return 0; }
 
     __device__ static __forceinline__ f32x4 mma(Frag a, Frag b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -168,16 +180,17 @@ struct PolF32 {
             f[4 * i + 3] = v.w;
         }
     }
-    // Other comes from the row-form tile [n][D]: the k-slot g of MFMA (t, r) is
-    // block row 16t + 4g + r, matching the C layout of the chain tiles.
+    // Other[y][n] = tile[n][y0 + y] read element-wise: the k-slot g of MFMA
+    // (t, r) is block row 16t + 4g + r, matching the C layout of the chain tiles.
     __device__ static __forceinline__ f32x4 chain(f32x4 acc, const f32x4 &c0, const f32x4 &c1,
-                                                  const T *row_tile, int y, int blk, int g) {
+                                                  const T *tile, int y0, int blk, int g, int l16) {
+        const int y = y0 + l16;
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int n = blk + (t << 4) + (g << 2) + r;
-                const float a = row_tile[n * D + (((y >> 2) ^ rswz(n)) << 2) + (y & 3)];
+                const float a = tile[n * D + (((y >> 2) ^ rswz(n)) << 2) + (y & 3)];
                 acc = mma(a, t ? c1[r] : c0[r], acc);
             }
         }
@@ -187,57 +200,54 @@ struct PolF32 {
 
 // --------------------------------------------------------------- LDS staging
 
-// One "stage block": 8 consecutive rows x one 16-byte chunk of a 64 x D tile.
-// Block b of a tile covers rows 8*(b / CPR) .. +7 and chunk b % CPR, CPR = D /
-// EPC chunks per row, so 8 (bf16) or 16 (fp32) consecutive threads read whole
-// rows (coalesced).
-template <class Pol>
-struct StageBlock {
-    static constexpr int CPR = Pol::D / Pol::EPC;
-    static constexpr int PER_TILE = 8 * CPR;
-    uint4 r[8];
+// Copies rows [0, ROWS) of a row-major [*, D] matrix into a swizzled row-form
+// LDS tile with direct global->LDS loads (global_load_lds_dwordx4: no VGPRs, no
+// VALU; lane i of a wave-wide load lands at LDS base + 16 i, so each lane
+// fetches the global chunk that belongs at its LDS position). Rows >= nvalid
+// re-read row nvalid-1 (in bounds; the kernels mask their scores). Called by
+// all 256 threads; completion is awaited with wait_stage() + a barrier.
+template <class Pol, int ROWS>
+__device__ __forceinline__ void stage_rows(typename Pol::T *tile, const typename Pol::T *src, int nvalid,
+                                           int tid, int wave) {
+    constexpr int CPR = Pol::D / Pol::EPC;
+    constexpr int NCH = ROWS * CPR;
+    static_assert(NCH % 256 == 0, "whole wave-wide loads");
+    // (device pass only: the host pass rejects the LDS address-space cast, and
+    // clang then refuses the next call site of the same specialization)
+#if defined(__HIP_DEVICE_COMPILE__)
+#pragma unroll
+    for (int k = 0; k < NCH / 256; ++k) {
+        const int P = k * 256 + tid;
+        const int row = P / CPR;
+        const int c = (P % CPR) ^ Pol::rswz(row);
+        const int grow = min(row, nvalid - 1);
+        const typename Pol::T *g = src + (size_t)grow * Pol::D + c * Pol::EPC;
+        auto *dst = (__attribute__((address_space(3))) void *)(reinterpret_cast<char *>(tile) +
+                                                                (k * 256 + wave * 64) * 16);
+        __builtin_amdgcn_global_load_lds(g, dst, 16, 0, 0);
+    }
+#endif
+}
 
-    __device__ __forceinline__ void load(const typename Pol::T *src, int nvalid, int b) {
-        const int cb = b % CPR, rb = b / CPR;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int row = 8 * rb + e;
-            if (row < nvalid) {
-                r[e] = *reinterpret_cast<const uint4 *>(src + (size_t)row * Pol::D + cb * Pol::EPC);
-            } else {
-                r[e] = make_uint4(0u, 0u, 0u, 0u);
-            }
-        }
-    }
-    __device__ __forceinline__ void store_row(typename Pol::T *tile, int b) const {
-        const int cb = b % CPR, rb = b / CPR;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int n = 8 * rb + e;
-            *reinterpret_cast<uint4 *>(tile + n * Pol::D + ((cb ^ Pol::rswz(n)) * Pol::EPC)) = r[e];
-        }
-    }
-    // bf16 only: transpose the 8x8 block in registers and write it to the
-    // col-form tile [D][64]: row y = 8*cb + c holds column c of the block at
-    // chunk rb.
-    __device__ __forceinline__ void store_col(typename Pol::T *ctile, int b) const {
-        const int cb = b % CPR, rb = b / CPR;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const int word = c >> 1;
-            uint32_t out[4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint32_t lo = reinterpret_cast<const uint32_t *>(&r[2 * k])[word];
-                const uint32_t hi = reinterpret_cast<const uint32_t *>(&r[2 * k + 1])[word];
-                out[k] = (c & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
-            }
-            const int y = 8 * cb + c;
-            *reinterpret_cast<uint4 *>(ctile + y * 64 + ((rb ^ Pol::cswz(y)) * 8)) =
-                make_uint4(out[0], out[1], out[2], out[3]);
-        }
-    }
-};
+// One K/V stage: ROWS key rows from k0 of K and V into LDS buffers.
+template <class Pol, int ROWS>
+__device__ __forceinline__ void stage_kv(typename Pol::T *sk, typename Pol::T *sv, const typename Pol::T *K,
+                                         const typename Pol::T *V, int k0, int N, int tid, int wave) {
+    stage_rows<Pol, ROWS>(sk, K + (size_t)k0 * Pol::D, N - k0, tid, wave);
+    stage_rows<Pol, ROWS>(sv, V + (size_t)k0 * Pol::D, N - k0, tid, wave);
+}
+
+// 64 fp32 values v[min(i0 + l, nvalid - 1)] -> dst[l], by one wave.
+__device__ __forceinline__ void stage_vec64(float *dst, const float *src, int nvalid, int lane) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const float *g = src + min(lane, nvalid - 1);
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)dst, 4, 0, 0);
+#endif
+}
+
+// Waits for this wave's outstanding global->LDS loads (the caller then
+// barriers so every wave's loads are visible).
+__device__ __forceinline__ void wait_stage() { __builtin_amdgcn_s_waitcnt(0); }
 
 // Store four consecutive elements x0..x0+3 of one output row.
 template <class T>

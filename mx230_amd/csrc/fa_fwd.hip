@@ -5,7 +5,8 @@
 // tile break, LSE = m + ln l at :85-87), re-tiled for CDNA4:
 //   * workgroup = 4 waves = 128 queries of one (batch, head); each wave owns
 //     32 queries, whose Q rows sit in registers as MFMA B operands;
-//   * K/V advance 64 keys per stage through double-buffered LDS;
+//   * K/V advance 64 keys per stage through double-buffered LDS, filled by
+//     direct global->LDS loads issued one stage ahead;
 //   * scores are computed transposed, S^T = K Q^T, so each lane owns one query
 //     column: the running max / sum stay per lane and only the max needs a
 //     cross-lane reduction (two permlane swaps);
@@ -23,13 +24,12 @@ __global__ __launch_bounds__(256) void fwd_kernel(Params p) {
     using Frag = typename Pol::Frag;
     constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
     constexpr int BQ = 128, BK = 64;
-    using SB = StageBlock<Pol>;
-    static_assert(2 * SB::PER_TILE <= 256, "one stage block per thread");
 
     __shared__ __attribute__((aligned(16))) T sK[2][BK * D];
     __shared__ __attribute__((aligned(16))) T sV[2][BK * D];
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, l16 = lane & 15;
     const int N = p.N;
     const int bh = blockIdx.x;
@@ -56,35 +56,14 @@ __global__ __launch_bounds__(256) void fwd_kernel(Params p) {
     const int kend = CAUSAL ? min(N, qb * BQ + BQ) : N;
     const int nsteps = (kend + BK - 1) / BK;
 
-    // stage blocks: [0, PER_TILE) -> K (row form), [PER_TILE, 2 PER_TILE) -> V
-    SB sb;
-    const bool stage_k = tid < SB::PER_TILE;
-    const bool stage_v = !stage_k && tid < 2 * SB::PER_TILE;
-    const int sbid = stage_k ? tid : tid - SB::PER_TILE;
-    auto load_stage = [&](int st) {
-        const int k0 = st * BK;
-        if (stage_k) sb.load(K + (size_t)k0 * D, N - k0, sbid);
-        if (stage_v) sb.load(V + (size_t)k0 * D, N - k0, sbid);
-    };
-    auto store_stage = [&](int buf) {
-        if (stage_k) sb.store_row(sK[buf], sbid);
-        if (stage_v) {
-            if constexpr (Pol::kColForm) {
-                sb.store_col(sV[buf], sbid);
-            } else {
-                sb.store_row(sV[buf], sbid);
-            }
-        }
-    };
-
-    load_stage(0);
-    store_stage(0);
+    stage_kv<Pol, BK>(sK[0], sV[0], K, V, 0, N, tid, wave);
+    wait_stage();
     __syncthreads();
 
     for (int st = 0; st < nsteps; ++st) {
         const int cur = st & 1;
         const bool has_next = st + 1 < nsteps;
-        if (has_next) load_stage(st + 1);
+        if (has_next) stage_kv<Pol, BK>(sK[cur ^ 1], sV[cur ^ 1], K, V, (st + 1) * BK, N, tid, wave);
         const int k0 = st * BK;
         const bool active = !CAUSAL || k0 <= q0 + 31;
         if (active) {
@@ -153,12 +132,12 @@ __global__ __launch_bounds__(256) void fwd_kernel(Params p) {
 #pragma unroll
                     for (int qt = 0; qt < 2; ++qt) {
                         acc[xt][qt] = Pol::chain(acc[xt][qt], s[blk][0][qt], s[blk][1][qt], sV[cur],
-                                                 16 * xt + l16, 32 * blk, g);
+                                                 16 * xt, 32 * blk, g, l16);
                     }
                 }
             }
         }
-        if (has_next) store_stage(cur ^ 1);
+        wait_stage();
         __syncthreads();
     }
 
