@@ -25,10 +25,6 @@
 
 namespace mxfa {
 
-#ifndef MXFA_DKV_WPE
-#define MXFA_DKV_WPE 1
-#endif
-
 // ------------------------------------------------------------ preprocess
 
 // Delta_i = sum_x dO[i][x] * O[i][x], 8 lanes per row (attention_bwd.cu:32-44).
@@ -90,7 +86,7 @@ __device__ __forceinline__ void stage_qdo(typename Pol::T *sq, typename Pol::T *
 // ------------------------------------------------------------------ dQ pass
 
 template <class Pol, bool CAUSAL>
-__global__ __launch_bounds__(256) void dq_kernel(Params p) {
+__global__ __launch_bounds__(256, Pol::kWaves) void dq_kernel(Params p) {
     using T = typename Pol::T;
     using Frag = typename Pol::Frag;
     constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
@@ -210,7 +206,7 @@ __global__ __launch_bounds__(256) void dq_kernel(Params p) {
 // ---------------------------------------------------------------- dK/dV pass
 
 template <class Pol, int KT, bool CAUSAL>
-__global__ __launch_bounds__(256, MXFA_DKV_WPE) void dkv_kernel(Params p) {
+__global__ __launch_bounds__(256, Pol::kWavesDkv) void dkv_kernel(Params p) {
     using T = typename Pol::T;
     using Frag = typename Pol::Frag;
     constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;

@@ -79,6 +79,10 @@ struct PolBF16 {
     using Frag = bf16x8;
     static constexpr int EPC = 8;      // elements per 16-byte chunk
     static constexpr int NC = D / 32;  // MFMAs over D per first-GEMM tile
+    // waves per SIMD the forward / dQ kernels (kWaves) and the dK/dV kernel
+    // (kWavesDkv) are compiled for: the largest count that fits without spills
+    static constexpr int kWaves = D == 64 ? 2 : 1;
+    static constexpr int kWavesDkv = 2;
 
     __device__ static __forceinline__ int arow(int t, int m) {
         return ((m >> 2) << 3) + (t << 2) + (m & 3);
@@ -149,6 +153,8 @@ struct PolF32 {
     using Frag = float;
     static constexpr int EPC = 4;
     static constexpr int NC = D / 4;
+    static constexpr int kWaves = 1;
+    static constexpr int kWavesDkv = 1;
 
     __device__ static __forceinline__ int arow(int t, int m) { return (t << 4) + m; }
     __device__ static __forceinline__ int bidx(int t, int g, int r) { return (t << 4) + (g << 2) + r; }

@@ -19,7 +19,7 @@
 namespace mxfa {
 
 template <class Pol, bool CAUSAL>
-__global__ __launch_bounds__(256) void fwd_kernel(Params p) {
+__global__ __launch_bounds__(256, Pol::kWaves) void fwd_kernel(Params p) {
     using T = typename Pol::T;
     using Frag = typename Pol::Frag;
     constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
