@@ -69,28 +69,90 @@ __global__ __launch_bounds__(256) void preprocess_kernel(const T *dout, const T 
     if (row < rows && part == 0) delta[row] = acc;
 }
 
-// One dK/dV stage: BQ query rows (from qs) of Q and dO of head bh, and their
-// LSE and Delta, into LDS buffers.
-template <class Pol, int BQ>
+// One dK/dV stage: the Pol::ROWS query rows from qs of Q and dO of head bh,
+// and their LSE and Delta, into LDS buffers.
+template <class Pol>
 __device__ __forceinline__ void stage_qdo(typename Pol::T *sq, typename Pol::T *sdo, float *sl, float *sd,
                                           const Params &p, size_t bh, int qs, int N, int tid, int wave,
                                           int lane) {
     using T = typename Pol::T;
     const size_t off = (bh * N + qs) * Pol::D;
-    stage_rows<Pol, BQ>(sq, static_cast<const T *>(p.q) + off, N - qs, tid, wave);
-    stage_rows<Pol, BQ>(sdo, static_cast<const T *>(p.dout) + off, N - qs, tid, wave);
+    stage_rows<Pol>(sq, static_cast<const T *>(p.q) + off, N - qs, tid, wave);
+    stage_rows<Pol>(sdo, static_cast<const T *>(p.dout) + off, N - qs, tid, wave);
     if (wave == 0) stage_vec64(sl, p.lse + bh * N + qs, N - qs, lane);
     if (wave == 1) stage_vec64(sd, p.delta + bh * N + qs, N - qs, lane);
 }
 
 // ------------------------------------------------------------------ dQ pass
 
+// One 64-key stage of the dQ pass for one wave (32 queries). dof holds -dO and
+// the dP accumulators start at Delta, so they come out as Delta - dP and the
+// MFMAs accumulate -dQ / scale (the epilogue multiplies by -scale).
+template <class Pol, bool CAUSAL, bool MASK>
+__device__ __forceinline__ void dq_stage(f32x4 (&acc)[Pol::D / 16][2], const typename Pol::Frag (&qf)[2][Pol::NC],
+                                         const typename Pol::Frag (&dof)[2][Pol::NC], const float (&L2)[2],
+                                         const float (&Dl)[2], const typename Pol::T *sk,
+                                         const typename Pol::T *sv, int k0, int q0, int N, float scale_log2,
+                                         int g, int l16) {
+    using Frag = typename Pol::Frag;
+    constexpr int NC = Pol::NC, XT = Pol::D / 16;
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+        f32x4 s[2][2], dp[2][2];  // [t][qt]
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            Frag a[NC];
+            const int n = 32 * blk + Pol::arow(t, l16);
+            Pol::lds_row_frags(a, sk, n, g);
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) {
+                f32x4 c = zero4();
+#pragma unroll
+                for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], qf[qt][kc], c);
+                s[t][qt] = c;
+            }
+            Pol::lds_row_frags(a, sv, n, g);
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) {
+                f32x4 c = f32x4{Dl[qt], Dl[qt], Dl[qt], Dl[qt]};
+#pragma unroll
+                for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], dof[qt][kc], c);
+                dp[t][qt] = c;
+            }
+        }
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+            const int qi = q0 + 16 * qt + l16;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float pv = fast_exp2(s[t][qt][r] * scale_log2 - L2[qt]);
+                    if constexpr (MASK) {
+                        const int key = k0 + 32 * blk + Pol::bidx(t, g, r);
+                        if (key >= N || (CAUSAL && key > qi)) pv = 0.f;
+                    }
+                    s[t][qt][r] = pv * dp[t][qt][r];  // -dS / scale
+                }
+            }
+        }
+        typename Pol::ChainB cb[2];
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) cb[qt] = Pol::pack(s[0][qt], s[1][qt]);
+#pragma unroll
+        for (int xt = 0; xt < XT; ++xt) {
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) acc[xt][qt] = Pol::chain(acc[xt][qt], cb[qt], sk, 16 * xt, 32 * blk, g, l16);
+        }
+    }
+}
+
 template <class Pol, bool CAUSAL>
 __global__ __launch_bounds__(256, Pol::kWaves) void dq_kernel(Params p) {
     using T = typename Pol::T;
     using Frag = typename Pol::Frag;
     constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
-    constexpr int BQ = 128, BK = 64;
+    constexpr int BQ = 128, BK = Pol::ROWS;
 
     __shared__ __attribute__((aligned(16))) T sK[2][BK * D];
     __shared__ __attribute__((aligned(16))) T sV[2][BK * D];
@@ -118,6 +180,8 @@ __global__ __launch_bounds__(256, Pol::kWaves) void dq_kernel(Params p) {
         const bool ok = qi < N;
         Pol::gmem_row_frags(qf[qt], Q + (size_t)qi * D, g, ok);
         Pol::gmem_row_frags(dof[qt], dO + (size_t)qi * D, g, ok);
+#pragma unroll
+        for (int kc = 0; kc < NC; ++kc) dof[qt][kc] = Pol::neg(dof[qt][kc]);
         L2[qt] = ok ? p.lse[(size_t)bh * N + qi] * kLog2e : 0.f;
         Dl[qt] = ok ? p.delta[(size_t)bh * N + qi] : 0.f;
     }
@@ -128,64 +192,20 @@ __global__ __launch_bounds__(256, Pol::kWaves) void dq_kernel(Params p) {
     const int kend = CAUSAL ? min(N, qb * BQ + BQ) : N;
     const int nsteps = (kend + BK - 1) / BK;
 
-    stage_kv<Pol, BK>(sK[0], sV[0], K, V, 0, N, tid, wave);
+    stage_kv<Pol>(sK[0], sV[0], K, V, 0, N, tid, wave);
     wait_stage();
     __syncthreads();
 
     for (int st = 0; st < nsteps; ++st) {
         const int cur = st & 1;
-        if (st + 1 < nsteps) stage_kv<Pol, BK>(sK[cur ^ 1], sV[cur ^ 1], K, V, (st + 1) * BK, N, tid, wave);
+        if (st + 1 < nsteps) stage_kv<Pol>(sK[cur ^ 1], sV[cur ^ 1], K, V, (st + 1) * BK, N, tid, wave);
         const int k0 = st * BK;
-        const bool active = !CAUSAL || k0 <= q0 + 31;
-        if (active) {
+        if (!CAUSAL || k0 <= q0 + 31) {
             const bool need_mask = (k0 + BK > N) || (CAUSAL && k0 + BK - 1 > q0);
-#pragma unroll
-            for (int blk = 0; blk < 2; ++blk) {
-                f32x4 s[2][2], dp[2][2];  // [t][qt]
-#pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    Frag a[NC];
-                    const int n = 32 * blk + Pol::arow(t, l16);
-                    Pol::lds_row_frags(a, sK[cur], n, g);
-#pragma unroll
-                    for (int qt = 0; qt < 2; ++qt) {
-                        f32x4 c = zero4();
-#pragma unroll
-                        for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], qf[qt][kc], c);
-                        s[t][qt] = c;
-                    }
-                    Pol::lds_row_frags(a, sV[cur], n, g);
-#pragma unroll
-                    for (int qt = 0; qt < 2; ++qt) {
-                        f32x4 c = zero4();
-#pragma unroll
-                        for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], dof[qt][kc], c);
-                        dp[t][qt] = c;
-                    }
-                }
-#pragma unroll
-                for (int qt = 0; qt < 2; ++qt) {
-                    const int qi = q0 + 16 * qt + l16;
-#pragma unroll
-                    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            float pv = fast_exp2(s[t][qt][r] * p.scale_log2 - L2[qt]);
-                            if (need_mask) {
-                                const int key = k0 + 32 * blk + Pol::bidx(t, g, r);
-                                if (key >= N || (CAUSAL && key > qi)) pv = 0.f;
-                            }
-                            s[t][qt][r] = pv * (dp[t][qt][r] - Dl[qt]);  // dS / scale
-                        }
-                    }
-                }
-#pragma unroll
-                for (int xt = 0; xt < XT; ++xt) {
-#pragma unroll
-                    for (int qt = 0; qt < 2; ++qt) {
-                        acc[xt][qt] = Pol::chain(acc[xt][qt], s[0][qt], s[1][qt], sK[cur], 16 * xt, 32 * blk, g, l16);
-                    }
-                }
+            if (need_mask) {
+                dq_stage<Pol, CAUSAL, true>(acc, qf, dof, L2, Dl, sK[cur], sV[cur], k0, q0, N, p.scale_log2, g, l16);
+            } else {
+                dq_stage<Pol, CAUSAL, false>(acc, qf, dof, L2, Dl, sK[cur], sV[cur], k0, q0, N, p.scale_log2, g, l16);
             }
         }
         wait_stage();
@@ -198,20 +218,95 @@ __global__ __launch_bounds__(256, Pol::kWaves) void dq_kernel(Params p) {
         const int qi = q0 + 16 * qt + l16;
         if (qi < N) {
 #pragma unroll
-            for (int xt = 0; xt < XT; ++xt) store4<T>(dQ + (size_t)qi * D + 16 * xt + 4 * g, acc[xt][qt], p.scale);
+            for (int xt = 0; xt < XT; ++xt) store4<T>(dQ + (size_t)qi * D + 16 * xt + 4 * g, acc[xt][qt], -p.scale);
         }
     }
 }
 
 // ---------------------------------------------------------------- dK/dV pass
 
+// One 64-query stage of the dK/dV pass for one wave (16*KT keys). vf holds -V
+// and the dP accumulators start at Delta, so they come out as Delta - dP and
+// accK accumulates -dK / scale (the epilogue multiplies by -scale).
+template <class Pol, int KT, bool CAUSAL, bool MASK>
+__device__ __forceinline__ void dkv_stage(f32x4 (&accK)[Pol::D / 16][KT], f32x4 (&accV)[Pol::D / 16][KT],
+                                          const typename Pol::Frag (&kf)[KT][Pol::NC],
+                                          const typename Pol::Frag (&vf)[KT][Pol::NC], const typename Pol::T *sq,
+                                          const typename Pol::T *sdo, const float *sl, const float *sd, int qs,
+                                          int kw0, int N, float scale_log2, int g, int l16) {
+    using Frag = typename Pol::Frag;
+    constexpr int NC = Pol::NC, XT = Pol::D / 16;
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+        f32x4 s[2][KT], dp[2][KT];  // [t][kt]
+        f32x4 L2[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            // block rows bidx(t, g, 0..3) are consecutive: one 16-byte LDS read
+            const int q4 = 32 * blk + Pol::bidx(t, g, 0);
+            L2[t] = *reinterpret_cast<const f32x4 *>(sl + q4) * kLog2e;
+            const f32x4 dl = *reinterpret_cast<const f32x4 *>(sd + q4);
+            Frag a[NC];
+            const int n = 32 * blk + Pol::arow(t, l16);
+            Pol::lds_row_frags(a, sq, n, g);
+#pragma unroll
+            for (int kt = 0; kt < KT; ++kt) {
+                f32x4 c = zero4();
+#pragma unroll
+                for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], kf[kt][kc], c);
+                s[t][kt] = c;
+            }
+            Pol::lds_row_frags(a, sdo, n, g);
+#pragma unroll
+            for (int kt = 0; kt < KT; ++kt) {
+                f32x4 c = dl;
+#pragma unroll
+                for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], vf[kt][kc], c);
+                dp[t][kt] = c;
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+#pragma unroll
+                for (int kt = 0; kt < KT; ++kt) {
+                    float pv = fast_exp2(s[t][kt][r] * scale_log2 - L2[t][r]);
+                    if constexpr (MASK) {
+                        // rows past N re-read row N-1; causal: queries before the key
+                        const int qi = qs + 32 * blk + Pol::bidx(t, g, r);
+                        const int key = kw0 + 16 * kt + l16;
+                        if (qi >= N || (CAUSAL && qi < key)) pv = 0.f;
+                    }
+                    s[t][kt][r] = pv;
+                    dp[t][kt][r] = pv * dp[t][kt][r];  // -dS / scale
+                }
+            }
+        }
+        typename Pol::ChainB cp[KT], cds[KT];
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) {
+            cp[kt] = Pol::pack(s[0][kt], s[1][kt]);
+            cds[kt] = Pol::pack(dp[0][kt], dp[1][kt]);
+        }
+#pragma unroll
+        for (int xt = 0; xt < XT; ++xt) {
+#pragma unroll
+            for (int kt = 0; kt < KT; ++kt) {
+                accV[xt][kt] = Pol::chain(accV[xt][kt], cp[kt], sdo, 16 * xt, 32 * blk, g, l16);
+                accK[xt][kt] = Pol::chain(accK[xt][kt], cds[kt], sq, 16 * xt, 32 * blk, g, l16);
+            }
+        }
+    }
+}
+
 template <class Pol, int KT, bool CAUSAL>
 __global__ __launch_bounds__(256, Pol::kWavesDkv) void dkv_kernel(Params p) {
     using T = typename Pol::T;
     using Frag = typename Pol::Frag;
     constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
-    constexpr int BKV = 64 * KT;  // keys per workgroup
-    constexpr int BQ = 64;        // queries per stage
+    constexpr int BKV = 64 * KT;      // keys per workgroup
+    constexpr int BQ = Pol::ROWS;     // queries per stage
     static_assert(BKV % BQ == 0, "causal start must align to a stage");
 
     __shared__ __attribute__((aligned(16))) T sQ[2][BQ * D];
@@ -237,6 +332,8 @@ __global__ __launch_bounds__(256, Pol::kWavesDkv) void dkv_kernel(Params p) {
         const int key = kw0 + 16 * kt + l16;
         Pol::gmem_row_frags(kf[kt], K + (size_t)key * D, g, key < N);
         Pol::gmem_row_frags(vf[kt], V + (size_t)key * D, g, key < N);
+#pragma unroll
+        for (int kc = 0; kc < NC; ++kc) vf[kt][kc] = Pol::neg(vf[kt][kc]);
     }
     f32x4 accK[XT][KT], accV[XT][KT];
 #pragma unroll
@@ -248,9 +345,9 @@ __global__ __launch_bounds__(256, Pol::kWavesDkv) void dkv_kernel(Params p) {
     const int qstart = CAUSAL ? kb * BKV : 0;
     const int nqs = (N - qstart + BQ - 1) / BQ;  // stages per query head
     const int nsteps = nqs * p.group;
-
     const size_t bh0 = (size_t)b * p.Hq + (size_t)kvh * p.group;
-    stage_qdo<Pol, BQ>(sQ[0], sdO[0], sL[0], sD[0], p, bh0, qstart, N, tid, wave, lane);
+
+    stage_qdo<Pol>(sQ[0], sdO[0], sL[0], sD[0], p, bh0, qstart, N, tid, wave, lane);
     wait_stage();
     __syncthreads();
 
@@ -258,67 +355,19 @@ __global__ __launch_bounds__(256, Pol::kWavesDkv) void dkv_kernel(Params p) {
         const int cur = st & 1;
         if (st + 1 < nsteps) {
             const int nx = st + 1;
-            stage_qdo<Pol, BQ>(sQ[cur ^ 1], sdO[cur ^ 1], sL[cur ^ 1], sD[cur ^ 1], p, bh0 + nx / nqs,
-                               qstart + (nx % nqs) * BQ, N, tid, wave, lane);
+            stage_qdo<Pol>(sQ[cur ^ 1], sdO[cur ^ 1], sL[cur ^ 1], sD[cur ^ 1], p, bh0 + nx / nqs,
+                           qstart + (nx % nqs) * BQ, N, tid, wave, lane);
         }
         const int qs = qstart + (st % nqs) * BQ;
-        const bool active = !CAUSAL || qs + BQ - 1 >= kw0;
-        if (active) {
-            // rows past N re-read row N-1 and must get p = 0; causal diagonal
-            // stages mask queries before the key
+        // a wave whose keys all follow the stage's queries has nothing to do
+        if (!CAUSAL || qs + BQ - 1 >= kw0) {
             const bool need_mask = (qs + BQ > N) || (CAUSAL && qs < kw0 + 16 * KT - 1);
-#pragma unroll
-            for (int blk = 0; blk < 2; ++blk) {
-                f32x4 s[2][KT], dp[2][KT];  // [t][kt]
-#pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    Frag a[NC];
-                    const int n = 32 * blk + Pol::arow(t, l16);
-                    Pol::lds_row_frags(a, sQ[cur], n, g);
-#pragma unroll
-                    for (int kt = 0; kt < KT; ++kt) {
-                        f32x4 c = zero4();
-#pragma unroll
-                        for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], kf[kt][kc], c);
-                        s[t][kt] = c;
-                    }
-                    Pol::lds_row_frags(a, sdO[cur], n, g);
-#pragma unroll
-                    for (int kt = 0; kt < KT; ++kt) {
-                        f32x4 c = zero4();
-#pragma unroll
-                        for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], vf[kt][kc], c);
-                        dp[t][kt] = c;
-                    }
-                }
-#pragma unroll
-                for (int t = 0; t < 2; ++t) {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int qloc = 32 * blk + Pol::bidx(t, g, r);
-                        const float L = sL[cur][qloc] * kLog2e;
-                        const float Dv = sD[cur][qloc];
-#pragma unroll
-                        for (int kt = 0; kt < KT; ++kt) {
-                            float pv = fast_exp2(s[t][kt][r] * p.scale_log2 - L);
-                            if (need_mask) {
-                                const int key = kw0 + 16 * kt + l16;
-                                const int qi = qs + qloc;
-                                if (qi >= N || (CAUSAL && qi < key)) pv = 0.f;
-                            }
-                            s[t][kt][r] = pv;
-                            dp[t][kt][r] = pv * (dp[t][kt][r] - Dv);  // dS / scale
-                        }
-                    }
-                }
-#pragma unroll
-                for (int xt = 0; xt < XT; ++xt) {
-#pragma unroll
-                    for (int kt = 0; kt < KT; ++kt) {
-                        accV[xt][kt] = Pol::chain(accV[xt][kt], s[0][kt], s[1][kt], sdO[cur], 16 * xt, 32 * blk, g, l16);
-                        accK[xt][kt] = Pol::chain(accK[xt][kt], dp[0][kt], dp[1][kt], sQ[cur], 16 * xt, 32 * blk, g, l16);
-                    }
-                }
+            if (need_mask) {
+                dkv_stage<Pol, KT, CAUSAL, true>(accK, accV, kf, vf, sQ[cur], sdO[cur], sL[cur], sD[cur], qs, kw0,
+                                                 N, p.scale_log2, g, l16);
+            } else {
+                dkv_stage<Pol, KT, CAUSAL, false>(accK, accV, kf, vf, sQ[cur], sdO[cur], sL[cur], sD[cur], qs, kw0,
+                                                  N, p.scale_log2, g, l16);
             }
         }
         wait_stage();
@@ -333,7 +382,7 @@ __global__ __launch_bounds__(256, Pol::kWavesDkv) void dkv_kernel(Params p) {
         if (key < N) {
 #pragma unroll
             for (int xt = 0; xt < XT; ++xt) {
-                store4<T>(dK + (size_t)key * D + 16 * xt + 4 * g, accK[xt][kt], p.scale);
+                store4<T>(dK + (size_t)key * D + 16 * xt + 4 * g, accK[xt][kt], -p.scale);
                 store4<T>(dV + (size_t)key * D + 16 * xt + 4 * g, accV[xt][kt], 1.0f);
             }
         }

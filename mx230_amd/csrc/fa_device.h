@@ -69,9 +69,20 @@ __device__ __forceinline__ u16 to_bf16_bits(float x) {
 // ------------------------------------------------------------------ policies
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 // bf16 inputs, fp32 accumulation: v_mfma_f32_16x16x32_bf16.
+//
+// LDS tiles (64 rows x D) are stored column-group major: the 32 bytes of
+// columns 16x..16x+15 of all 64 rows are contiguous (2 KB per group), and the
+// two 16-byte halves of a row's group swap when row bit 3 is set. Then
+//   * the transposing read of 4 consecutive rows of one group (ds_read_b64_tr_b16,
+//     16 lanes) touches 128 contiguous bytes, and
+//   * the 16-byte A-operand reads of rows arow(t, 0..7) hit 8 distinct 16-byte
+//     bank slots,
+// and every offset that depends on the loop position (group, block) is a
+// plain addition, so it folds into the instructions' immediate offsets.
 template <int D_>
 struct PolBF16 {
     static constexpr int D = D_;
@@ -79,6 +90,7 @@ struct PolBF16 {
     using Frag = bf16x8;
     static constexpr int EPC = 8;      // elements per 16-byte chunk
     static constexpr int NC = D / 32;  // MFMAs over D per first-GEMM tile
+    static constexpr int ROWS = 64;    // rows of every LDS tile
     // waves per SIMD the forward / dQ kernels (kWaves) and the dK/dV kernel
     // (kWavesDkv) are compiled for: the largest count that fits without spills
     static constexpr int kWaves = D == 64 ? 2 : 1;
@@ -88,26 +100,26 @@ struct PolBF16 {
         return ((m >> 2) << 3) + (t << 2) + (m & 3);
     }
     __device__ static __forceinline__ int bidx(int t, int g, int r) { return (g << 3) + (t << 2) + r; }
-    // Chunk swizzle of row-form tiles. Two read patterns must be conflict free:
-    // ds_read_b128 of one chunk from the 8 rows arow(t, 0..7) (or 8..15), and
-    // the transposing ds_read_b64_tr_b16 of 32 bytes from 4 consecutive rows.
-    // Bits 1-2 of the swizzle come from row bits 0-1 (4 consecutive rows hit 4
-    // different 32-byte pairs), bit 0 from row bit 3 (separates arow's halves).
-    __device__ static __forceinline__ int rswz(int n) { return ((n & 3) << 1) | ((n >> 3) & 1); }
+
+    // byte offset of 16-byte chunk `chunk` (columns 8 chunk..+7) of row `row`
+    __device__ static __forceinline__ int chunk_off(int row, int chunk) {
+        return (chunk >> 1) * (ROWS * 32) + row * 32 + (((chunk & 1) ^ ((row >> 3) & 1)) << 4);
+    }
+    // inverse map for the stager: the chunk stored at 16-byte position P
+    __device__ static __forceinline__ void chunk_at(int P, int &row, int &chunk) {
+        const int grp = P / (ROWS * 2), rem = P % (ROWS * 2);
+        row = rem >> 1;
+        chunk = 2 * grp + ((rem & 1) ^ ((row >> 3) & 1));
+    }
 
     __device__ static __forceinline__ f32x4 mma(Frag a, Frag b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
     }
-    __device__ static __forceinline__ int lds_off(int row, int col) {
-        return row * D + ((((col >> 3) ^ rswz(row))) << 3) + (col & 7);
-    }
     // k-slot (g, e) of MFMA c <-> element 32c + 8g + e of the row
     __device__ static __forceinline__ void lds_row_frags(Frag (&f)[NC], const T *tile, int n, int g) {
+        const char *base = reinterpret_cast<const char *>(tile);
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            const int chunk = 4 * c + g;
-            f[c] = *reinterpret_cast<const Frag *>(tile + n * D + ((chunk ^ rswz(n)) * EPC));
-        }
+        for (int c = 0; c < NC; ++c) f[c] = *reinterpret_cast<const Frag *>(base + chunk_off(n, 4 * c + g));
     }
     __device__ static __forceinline__ void gmem_row_frags(Frag (&f)[NC], const T *row, int g, bool valid) {
 #pragma unroll
@@ -119,14 +131,14 @@ struct PolBF16 {
             }
         }
     }
-    // acc += Other * chain over the 32-row block starting at blk, where Other[y][n]
-    // = tile[n][y0 + y] is read transposed from the row-form tile with
-    // ds_read_b64_tr_b16 (lane (g, j) of a 16-lane group addresses row
-    // blk + 8g + 4h + j/4, columns y0 + 4(j%4)..+3, and receives column y0 + j
-    // of those 4 rows), and chain element (t, r) of this lane is block row
-    // bidx(t, g, r) = 8g + 4t + r: both sides use k-slot e <-> row blk + 8g + e.
-    __device__ static __forceinline__ f32x4 chain(f32x4 acc, const f32x4 &c0, const f32x4 &c1,
-                                                  const T *tile, int y0, int blk, int g, int l16) {
+    // flips the sign of every element (bf16 sign bits)
+    __device__ static __forceinline__ Frag neg(Frag f) {
+        return __builtin_bit_cast(Frag, __builtin_bit_cast(i16x8, f) ^ (short)0x8000);
+    }
+    // The chain operand of one 32-row block: this lane's elements (t, r) of the
+    // two C tiles, as bf16, k-slot e = 4t + r <-> block row bidx(t, g, r) = 8g + e.
+    using ChainB = Frag;
+    __device__ static __forceinline__ ChainB pack(const f32x4 &c0, const f32x4 &c1) {
         Frag b;
         b[0] = (__bf16)c0[0];
         b[1] = (__bf16)c0[1];
@@ -136,11 +148,22 @@ struct PolBF16 {
         b[5] = (__bf16)c1[1];
         b[6] = (__bf16)c1[2];
         b[7] = (__bf16)c1[3];
+        return b;
+    }
+    // acc += Other * chain over the 32-row block starting at blk, where Other[y][n]
+    // = tile[n][y0 + y] is read transposed from the tile with ds_read_b64_tr_b16
+    // (lane (g, j) of a 16-lane group addresses row blk + 8g + 4h + j/4,
+    // columns y0 + 4(j%4)..+3, and receives column y0 + j of those 4 rows):
+    // k-slot e of both operands <-> row blk + 8g + e.
+    __device__ static __forceinline__ f32x4 chain(f32x4 acc, const ChainB &b, const T *tile, int y0, int blk,
+                                                  int g, int l16) {
+        const char *base = reinterpret_cast<const char *>(tile);
         const int r0 = blk + 8 * g + (l16 >> 2);
         const int col = y0 + 4 * (l16 & 3);
-        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(tile + lds_off(r0, col)));
-        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(tile + lds_off(r0 + 4, col)));
-        const short __attribute__((ext_vector_type(8))) av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        const int off = chunk_off(r0, col >> 3) + ((col & 7) << 1);
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(base + off));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(base + off + 4 * 32));
+        const i16x8 av = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         return mma(__builtin_bit_cast(Frag, av), b, acc);
     }
 };
@@ -153,12 +176,21 @@ struct PolF32 {
     using Frag = float;
     static constexpr int EPC = 4;
     static constexpr int NC = D / 4;
+    static constexpr int ROWS = 64;
     static constexpr int kWaves = 1;
     static constexpr int kWavesDkv = 1;
 
     __device__ static __forceinline__ int arow(int t, int m) { return (t << 4) + m; }
     __device__ static __forceinline__ int bidx(int t, int g, int r) { return (t << 4) + (g << 2) + r; }
+    // Row-major tiles, 16-byte chunks XOR-swizzled by the low row bits.
     __device__ static __forceinline__ int rswz(int n) { return n & 7; }
+    __device__ static __forceinline__ int chunk_off(int row, int chunk) {
+        return row * (D * 4) + ((chunk ^ rswz(row)) << 4);
+    }
+    __device__ static __forceinline__ void chunk_at(int P, int &row, int &chunk) {
+        row = P / (D / 4);
+        chunk = (P % (D / 4)) ^ rswz(row);
+    }
 
     __device__ static __forceinline__ f32x4 mma(Frag a, Frag b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -186,10 +218,16 @@ struct PolF32 {
             f[4 * i + 3] = v.w;
         }
     }
+    __device__ static __forceinline__ Frag neg(Frag f) { return -f; }
+    // The chain operand of one 32-row block: the two C tiles themselves.
+    struct ChainB {
+        f32x4 c0, c1;
+    };
+    __device__ static __forceinline__ ChainB pack(const f32x4 &c0, const f32x4 &c1) { return ChainB{c0, c1}; }
     // Other[y][n] = tile[n][y0 + y] read element-wise: the k-slot g of MFMA
     // (t, r) is block row 16t + 4g + r, matching the C layout of the chain tiles.
-    __device__ static __forceinline__ f32x4 chain(f32x4 acc, const f32x4 &c0, const f32x4 &c1,
-                                                  const T *tile, int y0, int blk, int g, int l16) {
+    __device__ static __forceinline__ f32x4 chain(f32x4 acc, const ChainB &b, const T *tile, int y0, int blk,
+                                                  int g, int l16) {
         const int y = y0 + l16;
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
@@ -197,7 +235,7 @@ struct PolF32 {
             for (int r = 0; r < 4; ++r) {
                 const int n = blk + (t << 4) + (g << 2) + r;
                 const float a = tile[n * D + (((y >> 2) ^ rswz(n)) << 2) + (y & 3)];
-                acc = mma(a, t ? c1[r] : c0[r], acc);
+                acc = mma(a, t ? b.c1[r] : b.c0[r], acc);
             }
         }
         return acc;
@@ -206,17 +244,17 @@ struct PolF32 {
 
 // --------------------------------------------------------------- LDS staging
 
-// Copies rows [0, ROWS) of a row-major [*, D] matrix into a swizzled row-form
-// LDS tile with direct global->LDS loads (global_load_lds_dwordx4: no VGPRs, no
+// Copies rows [0, Pol::ROWS) of a row-major [*, D] matrix into an LDS tile in
+// the policy's layout with direct global->LDS loads (global_load_lds_dwordx4: no VGPRs, no
 // VALU; lane i of a wave-wide load lands at LDS base + 16 i, so each lane
 // fetches the global chunk that belongs at its LDS position). Rows >= nvalid
 // re-read row nvalid-1 (in bounds; the kernels mask their scores). Called by
 // all 256 threads; completion is awaited with wait_stage() + a barrier.
-template <class Pol, int ROWS>
+template <class Pol>
 __device__ __forceinline__ void stage_rows(typename Pol::T *tile, const typename Pol::T *src, int nvalid,
                                            int tid, int wave) {
     constexpr int CPR = Pol::D / Pol::EPC;
-    constexpr int NCH = ROWS * CPR;
+    constexpr int NCH = Pol::ROWS * CPR;
     static_assert(NCH % 256 == 0, "whole wave-wide loads");
     // (device pass only: the host pass rejects the LDS address-space cast, and
     // clang then refuses the next call site of the same specialization)
@@ -224,8 +262,8 @@ __device__ __forceinline__ void stage_rows(typename Pol::T *tile, const typename
 #pragma unroll
     for (int k = 0; k < NCH / 256; ++k) {
         const int P = k * 256 + tid;
-        const int row = P / CPR;
-        const int c = (P % CPR) ^ Pol::rswz(row);
+        int row, c;
+        Pol::chunk_at(P, row, c);
         const int grow = min(row, nvalid - 1);
         const typename Pol::T *g = src + (size_t)grow * Pol::D + c * Pol::EPC;
         auto *dst = (__attribute__((address_space(3))) void *)(reinterpret_cast<char *>(tile) +
@@ -235,12 +273,12 @@ __device__ __forceinline__ void stage_rows(typename Pol::T *tile, const typename
 #endif
 }
 
-// One K/V stage: ROWS key rows from k0 of K and V into LDS buffers.
-template <class Pol, int ROWS>
+// One K/V stage: Pol::ROWS key rows from k0 of K and V into LDS buffers.
+template <class Pol>
 __device__ __forceinline__ void stage_kv(typename Pol::T *sk, typename Pol::T *sv, const typename Pol::T *K,
                                          const typename Pol::T *V, int k0, int N, int tid, int wave) {
-    stage_rows<Pol, ROWS>(sk, K + (size_t)k0 * Pol::D, N - k0, tid, wave);
-    stage_rows<Pol, ROWS>(sv, V + (size_t)k0 * Pol::D, N - k0, tid, wave);
+    stage_rows<Pol>(sk, K + (size_t)k0 * Pol::D, N - k0, tid, wave);
+    stage_rows<Pol>(sv, V + (size_t)k0 * Pol::D, N - k0, tid, wave);
 }
 
 // 64 fp32 values v[min(i0 + l, nvalid - 1)] -> dst[l], by one wave.

@@ -12,18 +12,98 @@
 //     cross-lane reduction (two permlane swaps);
 //   * the output is accumulated transposed, O^T = V^T P^T, so the per-query
 //     rescale factor is a per-lane scalar as well;
-//   * exponentials are base 2 with log2(e) folded into the scale.
+//   * exponentials are base 2 with log2(e) folded into the scale;
+//   * only stages that straddle the causal diagonal or the end of the sequence
+//     run the masking code (a separate instantiation of the stage body).
 #include "fa_device.h"
 #include "fa_launch.h"
 
 namespace mxfa {
+
+// One 64-key stage for one wave: scores, online-softmax update, O^T += V^T P^T.
+template <class Pol, bool CAUSAL, bool MASK>
+__device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][2], float (&m)[2], float (&lsum)[2],
+                                          const typename Pol::Frag (&qf)[2][Pol::NC],
+                                          const typename Pol::T *sk, const typename Pol::T *sv, int k0, int q0,
+                                          int N, float scale_log2, int g, int l16) {
+    using Frag = typename Pol::Frag;
+    constexpr int NC = Pol::NC, XT = Pol::D / 16;
+    f32x4 s[2][2][2];  // [block][t][qt]
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            Frag a[NC];
+            Pol::lds_row_frags(a, sk, 32 * blk + Pol::arow(t, l16), g);
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) {
+                f32x4 c = zero4();
+#pragma unroll
+                for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], qf[qt][kc], c);
+                s[blk][t][qt] = c;
+            }
+        }
+    }
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        const int qi = q0 + 16 * qt + l16;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float v = s[blk][t][qt][r] * scale_log2;
+                    if constexpr (MASK) {
+                        const int key = k0 + 32 * blk + Pol::bidx(t, g, r);
+                        if (key >= N || (CAUSAL && key > qi)) v = -INFINITY;
+                    }
+                    s[blk][t][qt][r] = v;
+                    mx = fmaxf(mx, v);
+                }
+            }
+        }
+        mx = xg_max(mx);
+        const float mnew = fmaxf(m[qt], mx);
+        const float corr = fast_exp2(m[qt] - mnew);
+        m[qt] = mnew;
+        float ls = lsum[qt] * corr;
+#pragma unroll
+        for (int xt = 0; xt < XT; ++xt) acc[xt][qt] *= corr;
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float pv = fast_exp2(s[blk][t][qt][r] - mnew);
+                    s[blk][t][qt][r] = pv;
+                    ls += pv;
+                }
+            }
+        }
+        lsum[qt] = ls;
+    }
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+        typename Pol::ChainB cb[2];
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) cb[qt] = Pol::pack(s[blk][0][qt], s[blk][1][qt]);
+#pragma unroll
+        for (int xt = 0; xt < XT; ++xt) {
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) acc[xt][qt] = Pol::chain(acc[xt][qt], cb[qt], sv, 16 * xt, 32 * blk, g, l16);
+        }
+    }
+}
 
 template <class Pol, bool CAUSAL>
 __global__ __launch_bounds__(256, Pol::kWaves) void fwd_kernel(Params p) {
     using T = typename Pol::T;
     using Frag = typename Pol::Frag;
     constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
-    constexpr int BQ = 128, BK = 64;
+    constexpr int BQ = 128, BK = Pol::ROWS;
 
     __shared__ __attribute__((aligned(16))) T sK[2][BK * D];
     __shared__ __attribute__((aligned(16))) T sV[2][BK * D];
@@ -56,85 +136,21 @@ __global__ __launch_bounds__(256, Pol::kWaves) void fwd_kernel(Params p) {
     const int kend = CAUSAL ? min(N, qb * BQ + BQ) : N;
     const int nsteps = (kend + BK - 1) / BK;
 
-    stage_kv<Pol, BK>(sK[0], sV[0], K, V, 0, N, tid, wave);
+    stage_kv<Pol>(sK[0], sV[0], K, V, 0, N, tid, wave);
     wait_stage();
     __syncthreads();
 
     for (int st = 0; st < nsteps; ++st) {
         const int cur = st & 1;
-        const bool has_next = st + 1 < nsteps;
-        if (has_next) stage_kv<Pol, BK>(sK[cur ^ 1], sV[cur ^ 1], K, V, (st + 1) * BK, N, tid, wave);
+        if (st + 1 < nsteps) stage_kv<Pol>(sK[cur ^ 1], sV[cur ^ 1], K, V, (st + 1) * BK, N, tid, wave);
         const int k0 = st * BK;
-        const bool active = !CAUSAL || k0 <= q0 + 31;
-        if (active) {
-            f32x4 s[2][2][2];  // [block][t][qt]
-#pragma unroll
-            for (int blk = 0; blk < 2; ++blk) {
-#pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    Frag a[NC];
-                    Pol::lds_row_frags(a, sK[cur], 32 * blk + Pol::arow(t, l16), g);
-#pragma unroll
-                    for (int qt = 0; qt < 2; ++qt) {
-                        f32x4 c = zero4();
-#pragma unroll
-                        for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], qf[qt][kc], c);
-                        s[blk][t][qt] = c;
-                    }
-                }
-            }
+        // a wave whose queries all precede the stage's keys has nothing to do
+        if (!CAUSAL || k0 <= q0 + 31) {
             const bool need_mask = (k0 + BK > N) || (CAUSAL && k0 + BK - 1 > q0);
-#pragma unroll
-            for (int qt = 0; qt < 2; ++qt) {
-                const int qi = q0 + 16 * qt + l16;
-                float mx = -INFINITY;
-#pragma unroll
-                for (int blk = 0; blk < 2; ++blk) {
-#pragma unroll
-                    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            float v = s[blk][t][qt][r] * p.scale_log2;
-                            if (need_mask) {
-                                const int key = k0 + 32 * blk + Pol::bidx(t, g, r);
-                                if (key >= N || (CAUSAL && key > qi)) v = -INFINITY;
-                            }
-                            s[blk][t][qt][r] = v;
-                            mx = fmaxf(mx, v);
-                        }
-                    }
-                }
-                mx = xg_max(mx);
-                const float mnew = fmaxf(m[qt], mx);
-                const float corr = fast_exp2(m[qt] - mnew);
-                m[qt] = mnew;
-                float ls = lsum[qt] * corr;
-#pragma unroll
-                for (int xt = 0; xt < XT; ++xt) acc[xt][qt] *= corr;
-#pragma unroll
-                for (int blk = 0; blk < 2; ++blk) {
-#pragma unroll
-                    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            const float pv = fast_exp2(s[blk][t][qt][r] - mnew);
-                            s[blk][t][qt][r] = pv;
-                            ls += pv;
-                        }
-                    }
-                }
-                lsum[qt] = ls;
-            }
-#pragma unroll
-            for (int blk = 0; blk < 2; ++blk) {
-#pragma unroll
-                for (int xt = 0; xt < XT; ++xt) {
-#pragma unroll
-                    for (int qt = 0; qt < 2; ++qt) {
-                        acc[xt][qt] = Pol::chain(acc[xt][qt], s[blk][0][qt], s[blk][1][qt], sV[cur],
-                                                 16 * xt, 32 * blk, g, l16);
-                    }
-                }
+            if (need_mask) {
+                fwd_stage<Pol, CAUSAL, true>(acc, m, lsum, qf, sK[cur], sV[cur], k0, q0, N, p.scale_log2, g, l16);
+            } else {
+                fwd_stage<Pol, CAUSAL, false>(acc, m, lsum, qf, sK[cur], sV[cur], k0, q0, N, p.scale_log2, g, l16);
             }
         }
         wait_stage();
