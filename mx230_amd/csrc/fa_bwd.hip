@@ -20,6 +20,8 @@
 //     per wave, Q/dO rows in registers); K/V stream through LDS 64 keys per
 //     stage. It recomputes S and dP (the price of staying atomic-free and O(N)
 //     in memory).
+#include <type_traits>
+
 #include "fa_device.h"
 #include "fa_launch.h"
 
@@ -79,8 +81,9 @@ __device__ __forceinline__ void stage_qdo(typename Pol::T *sq, typename Pol::T *
     const size_t off = (bh * N + qs) * Pol::D;
     stage_rows<Pol>(sq, static_cast<const T *>(p.q) + off, N - qs, tid, wave);
     stage_rows<Pol>(sdo, static_cast<const T *>(p.dout) + off, N - qs, tid, wave);
-    if (wave == 0) stage_vec64(sl, p.lse + bh * N + qs, N - qs, lane);
-    if (wave == 1) stage_vec64(sd, p.delta + bh * N + qs, N - qs, lane);
+    // rows past N: LSE = +inf makes their p (and so dS) exactly 0
+    if (wave == 0) stage_vec64(sl, p.lse + bh * N + qs, N - qs, lane, &kPosInf);
+    if (wave == 1) stage_vec64(sd, p.delta + bh * N + qs, N - qs, lane, p.delta + bh * N + qs);
 }
 
 // ------------------------------------------------------------------ dQ pass
@@ -127,11 +130,12 @@ __device__ __forceinline__ void dq_stage(f32x4 (&acc)[Pol::D / 16][2], const typ
             for (int t = 0; t < 2; ++t) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    float pv = fast_exp2(s[t][qt][r] * scale_log2 - L2[qt]);
+                    float x = s[t][qt][r] * scale_log2 - L2[qt];
                     if constexpr (MASK) {
                         const int key = k0 + 32 * blk + Pol::bidx(t, g, r);
-                        if (key >= N || (CAUSAL && key > qi)) pv = 0.f;
+                        x = (key >= N || (CAUSAL && key > qi)) ? -INFINITY : x;
                     }
+                    const float pv = fast_exp2(x);
                     s[t][qt][r] = pv * dp[t][qt][r];  // -dS / scale
                 }
             }
@@ -271,13 +275,13 @@ __device__ __forceinline__ void dkv_stage(f32x4 (&accK)[Pol::D / 16][KT], f32x4 
             for (int r = 0; r < 4; ++r) {
 #pragma unroll
                 for (int kt = 0; kt < KT; ++kt) {
-                    float pv = fast_exp2(s[t][kt][r] * scale_log2 - L2[t][r]);
+                    float x = s[t][kt][r] * scale_log2 - L2[t][r];
                     if constexpr (MASK) {
-                        // rows past N re-read row N-1; causal: queries before the key
-                        const int qi = qs + 32 * blk + Pol::bidx(t, g, r);
-                        const int key = kw0 + 16 * kt + l16;
-                        if (qi >= N || (CAUSAL && qi < key)) pv = 0.f;
+                        // causal: query qs + 32 blk + bidx(t, g, r) before key kw0 + 16 kt + l16
+                        const bool before = Pol::bidx(t, g, r) - l16 < kw0 - qs + 16 * kt - 32 * blk;
+                        x = before ? -INFINITY : x;
                     }
+                    const float pv = fast_exp2(x);
                     s[t][kt][r] = pv;
                     dp[t][kt][r] = pv * dp[t][kt][r];  // -dS / scale
                 }
@@ -298,6 +302,7 @@ __device__ __forceinline__ void dkv_stage(f32x4 (&accK)[Pol::D / 16][KT], f32x4 
             }
         }
     }
+
 }
 
 template <class Pol, int KT, bool CAUSAL>
@@ -351,7 +356,14 @@ __global__ __launch_bounds__(256, Pol::kWavesDkv) void dkv_kernel(Params p) {
     wait_stage();
     __syncthreads();
 
-    for (int st = 0; st < nsteps; ++st) {
+    // One stage: prefetch stage st+1, compute stage st, then wait + barrier.
+    // Causal: the stages that straddle the diagonal are the first
+    // ceil(BKV / BQ) of each query head (queries from kb * BKV); they run in a
+    // loop of their own with the masked body, so neither loop carries the
+    // other's code (two bodies behind one branch make the register allocator
+    // spill).
+    auto run = [&](auto mask_tag, int st) __attribute__((always_inline)) {
+        constexpr bool MASK = decltype(mask_tag)::value;
         const int cur = st & 1;
         if (st + 1 < nsteps) {
             const int nx = st + 1;
@@ -361,17 +373,17 @@ __global__ __launch_bounds__(256, Pol::kWavesDkv) void dkv_kernel(Params p) {
         const int qs = qstart + (st % nqs) * BQ;
         // a wave whose keys all follow the stage's queries has nothing to do
         if (!CAUSAL || qs + BQ - 1 >= kw0) {
-            const bool need_mask = (qs + BQ > N) || (CAUSAL && qs < kw0 + 16 * KT - 1);
-            if (need_mask) {
-                dkv_stage<Pol, KT, CAUSAL, true>(accK, accV, kf, vf, sQ[cur], sdO[cur], sL[cur], sD[cur], qs, kw0,
-                                                 N, p.scale_log2, g, l16);
-            } else {
-                dkv_stage<Pol, KT, CAUSAL, false>(accK, accV, kf, vf, sQ[cur], sdO[cur], sL[cur], sD[cur], qs, kw0,
-                                                  N, p.scale_log2, g, l16);
-            }
+            dkv_stage<Pol, KT, CAUSAL, MASK>(accK, accV, kf, vf, sQ[cur], sdO[cur], sL[cur], sD[cur], qs, kw0, N,
+                                             p.scale_log2, g, l16);
         }
         wait_stage();
         __syncthreads();
+    };
+    // rows past N get p = 0 from LSE = +inf, so only the causal diagonal masks
+    const int ndiag = CAUSAL ? min(nqs, BKV / BQ) : 0;
+    for (int hh = 0, st = 0; hh < p.group; ++hh) {
+        for (int i = 0; i < ndiag; ++i, ++st) run(std::true_type{}, st);
+        for (int i = ndiag; i < nqs; ++i, ++st) run(std::false_type{}, st);
     }
 
     T *dK = static_cast<T *>(p.dk) + kvoff;

@@ -75,14 +75,18 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 // bf16 inputs, fp32 accumulation: v_mfma_f32_16x16x32_bf16.
 //
 // LDS tiles (64 rows x D) are stored column-group major: the 32 bytes of
-// columns 16x..16x+15 of all 64 rows are contiguous (2 KB per group), and the
-// two 16-byte halves of a row's group swap when row bit 3 is set. Then
-//   * the transposing read of 4 consecutive rows of one group (ds_read_b64_tr_b16,
-//     16 lanes) touches 128 contiguous bytes, and
-//   * the 16-byte A-operand reads of rows arow(t, 0..7) hit 8 distinct 16-byte
-//     bank slots,
-// and every offset that depends on the loop position (group, block) is a
-// plain addition, so it folds into the instructions' immediate offsets.
+// columns 16x..16x+15 of all 64 rows are contiguous (2 KB per group). Within a
+// group, row r (bits r0..r5) sits at slot prow(r), whose bits are
+// (r0, r1, r3^r4, r2, r4, r5), and its two 16-byte halves swap when r3 is set.
+// Then, with either 128 or 256 bytes of banks per cycle,
+//   * the 16-byte A-operand reads of rows arow(t, 0..15) hit 16 distinct
+//     16-byte slots of a 256-byte window (8 distinct in every 128 bytes), and
+//   * the transposing reads (ds_read_b64_tr_b16) of 4 consecutive rows of a
+//     group touch 128 contiguous bytes, and the two 16-lane groups g, g+1 (rows
+//     r, r+8) land in different 128-byte halves of a 256-byte window;
+// and the row bits that depend on the loop position (r2: tile t or half h,
+// r5: block) and the group map to fixed slot bits, so those offsets are plain
+// additions that fold into the instructions' immediate offsets.
 template <int D_>
 struct PolBF16 {
     static constexpr int D = D_;
@@ -101,14 +105,22 @@ struct PolBF16 {
     }
     __device__ static __forceinline__ int bidx(int t, int g, int r) { return (g << 3) + (t << 2) + r; }
 
+    // slot of row r within a column group, and its inverse
+    __device__ static __forceinline__ int prow(int r) {
+        return (r & 3) | ((((r >> 3) ^ (r >> 4)) & 1) << 2) | (((r >> 2) & 1) << 3) | (r & 48);
+    }
+    __device__ static __forceinline__ int prow_inv(int s) {
+        const int b4 = (s >> 4) & 1, b3 = ((s >> 2) & 1) ^ b4;
+        return (s & 3) | (((s >> 3) & 1) << 2) | (b3 << 3) | (s & 48);
+    }
     // byte offset of 16-byte chunk `chunk` (columns 8 chunk..+7) of row `row`
     __device__ static __forceinline__ int chunk_off(int row, int chunk) {
-        return (chunk >> 1) * (ROWS * 32) + row * 32 + (((chunk & 1) ^ ((row >> 3) & 1)) << 4);
+        return (chunk >> 1) * (ROWS * 32) + prow(row) * 32 + (((chunk & 1) ^ ((row >> 3) & 1)) << 4);
     }
     // inverse map for the stager: the chunk stored at 16-byte position P
     __device__ static __forceinline__ void chunk_at(int P, int &row, int &chunk) {
         const int grp = P / (ROWS * 2), rem = P % (ROWS * 2);
-        row = rem >> 1;
+        row = prow_inv(rem >> 1);
         chunk = 2 * grp + ((rem & 1) ^ ((row >> 3) & 1));
     }
 
@@ -160,9 +172,10 @@ struct PolBF16 {
         const char *base = reinterpret_cast<const char *>(tile);
         const int r0 = blk + 8 * g + (l16 >> 2);
         const int col = y0 + 4 * (l16 & 3);
-        const int off = chunk_off(r0, col >> 3) + ((col & 7) << 1);
-        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(base + off));
-        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(base + off + 4 * 32));
+        const int off_lo = chunk_off(r0, col >> 3) + ((col & 7) << 1);
+        const int off_hi = chunk_off(r0 + 4, col >> 3) + ((col & 7) << 1);
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(base + off_lo));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(base + off_hi));
         const i16x8 av = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         return mma(__builtin_bit_cast(Frag, av), b, acc);
     }
@@ -281,10 +294,13 @@ __device__ __forceinline__ void stage_kv(typename Pol::T *sk, typename Pol::T *s
     stage_rows<Pol>(sv, V + (size_t)k0 * Pol::D, N - k0, tid, wave);
 }
 
-// 64 fp32 values v[min(i0 + l, nvalid - 1)] -> dst[l], by one wave.
-__device__ __forceinline__ void stage_vec64(float *dst, const float *src, int nvalid, int lane) {
+// Read by lanes past the end of a staged vector (see stage_vec64).
+__device__ const float kPosInf = __builtin_inff();
+
+// 64 fp32 values src[l] (l < nvalid, else *pad) -> dst[l], by one wave.
+__device__ __forceinline__ void stage_vec64(float *dst, const float *src, int nvalid, int lane, const float *pad) {
 #if defined(__HIP_DEVICE_COMPILE__)
-    const float *g = src + min(lane, nvalid - 1);
+    const float *g = lane < nvalid ? src + lane : pad;
     __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)dst, 4, 0, 0);
 #endif
 }

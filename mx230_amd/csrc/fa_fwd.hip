@@ -57,7 +57,7 @@ __device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][2], float (&
                     float v = s[blk][t][qt][r] * scale_log2;
                     if constexpr (MASK) {
                         const int key = k0 + 32 * blk + Pol::bidx(t, g, r);
-                        if (key >= N || (CAUSAL && key > qi)) v = -INFINITY;
+                        v = (key >= N || (CAUSAL && key > qi)) ? -INFINITY : v;
                     }
                     s[blk][t][qt][r] = v;
                     mx = fmaxf(mx, v);
