@@ -65,12 +65,12 @@ def copy_probe(mib):
 
 def cpu_baseline(a, hkv):
     """Times the CPU oracle on a bounded sample of the same workload: the
-    backward of the first 8 (batch, head) slices on one thread (the reference's
+    backward of the first 16 (batch, head) slices on one thread (the reference's
     CPU path is single-threaded), inputs bf16-rounded as the GPU sees them."""
     import numpy as np
     import oracle  # the checker; used here only as the timed CPU baseline
     lib = oracle.load()
-    nheads = min(8, a.B * a.H)
+    nheads = min(16, a.B * a.H)
     N, d = a.N, a.d
     group = a.H // hkv
     tot = 0.0

@@ -302,7 +302,6 @@ __device__ __forceinline__ void dkv_stage(f32x4 (&accK)[Pol::D / 16][KT], f32x4 
             }
         }
     }
-
 }
 
 template <class Pol, int KT, bool CAUSAL>
@@ -314,10 +313,12 @@ __global__ __launch_bounds__(256, Pol::kWavesDkv) void dkv_kernel(Params p) {
     constexpr int BQ = Pol::ROWS;     // queries per stage
     static_assert(BKV % BQ == 0, "causal start must align to a stage");
 
-    __shared__ __attribute__((aligned(16))) T sQ[2][BQ * D];
-    __shared__ __attribute__((aligned(16))) T sdO[2][BQ * D];
-    __shared__ __attribute__((aligned(16))) float sL[2][BQ];
-    __shared__ __attribute__((aligned(16))) float sD[2][BQ];
+    // NBUF-deep ring of stages: loads are issued NBUF-1 stages ahead
+    constexpr int NBUF = Pol::kDkvBuffers;
+    __shared__ __attribute__((aligned(16))) T sQ[NBUF][BQ * D];
+    __shared__ __attribute__((aligned(16))) T sdO[NBUF][BQ * D];
+    __shared__ __attribute__((aligned(16))) float sL[NBUF][BQ];
+    __shared__ __attribute__((aligned(16))) float sD[NBUF][BQ];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -352,31 +353,47 @@ __global__ __launch_bounds__(256, Pol::kWavesDkv) void dkv_kernel(Params p) {
     const int nsteps = nqs * p.group;
     const size_t bh0 = (size_t)b * p.Hq + (size_t)kvh * p.group;
 
-    stage_qdo<Pol>(sQ[0], sdO[0], sL[0], sD[0], p, bh0, qstart, N, tid, wave, lane);
-    wait_stage();
+    auto issue = [&](int st) __attribute__((always_inline)) {
+        const int bf = st % NBUF;
+        stage_qdo<Pol>(sQ[bf], sdO[bf], sL[bf], sD[bf], p, bh0 + st / nqs, qstart + (st % nqs) * BQ, N, tid,
+                       wave, lane);
+    };
+    // loads of one stage per thread: the Q and dO tiles (+1 vector on waves
+    // 0-1, which the waits below may over-wait by one load)
+    constexpr int kLoads = 2 * tile_loads<Pol>();
+#pragma unroll
+    for (int i = 0; i < NBUF - 1; ++i) {
+        if (i < nsteps) issue(i);
+    }
+    if (NBUF > 2 && nsteps > 1) {
+        wait_vmcnt<kLoads>();
+    } else {
+        wait_stage();
+    }
     __syncthreads();
 
-    // One stage: prefetch stage st+1, compute stage st, then wait + barrier.
-    // Causal: the stages that straddle the diagonal are the first
-    // ceil(BKV / BQ) of each query head (queries from kb * BKV); they run in a
-    // loop of their own with the masked body, so neither loop carries the
-    // other's code (two bodies behind one branch make the register allocator
-    // spill).
+    // One stage: prefetch stage st + NBUF - 1, compute stage st, then wait for
+    // stage st + 1 and barrier. Causal: the stages that straddle the diagonal
+    // are the first ceil(BKV / BQ) of each query head (queries from kb * BKV);
+    // they run in a loop of their own with the masked body, so neither loop
+    // carries the other's code (two bodies behind one branch make the register
+    // allocator spill).
     auto run = [&](auto mask_tag, int st) __attribute__((always_inline)) {
         constexpr bool MASK = decltype(mask_tag)::value;
-        const int cur = st & 1;
-        if (st + 1 < nsteps) {
-            const int nx = st + 1;
-            stage_qdo<Pol>(sQ[cur ^ 1], sdO[cur ^ 1], sL[cur ^ 1], sD[cur ^ 1], p, bh0 + nx / nqs,
-                           qstart + (nx % nqs) * BQ, N, tid, wave, lane);
-        }
+        const int cur = st % NBUF;
+        const bool ahead = st + NBUF - 1 < nsteps;
+        if (ahead) issue(st + NBUF - 1);
         const int qs = qstart + (st % nqs) * BQ;
         // a wave whose keys all follow the stage's queries has nothing to do
         if (!CAUSAL || qs + BQ - 1 >= kw0) {
             dkv_stage<Pol, KT, CAUSAL, MASK>(accK, accV, kf, vf, sQ[cur], sdO[cur], sL[cur], sD[cur], qs, kw0, N,
                                              p.scale_log2, g, l16);
         }
-        wait_stage();
+        if (NBUF > 2 && ahead) {
+            wait_vmcnt<kLoads>();
+        } else {
+            wait_stage();
+        }
         __syncthreads();
     };
     // rows past N get p = 0 from LSE = +inf, so only the causal diagonal masks

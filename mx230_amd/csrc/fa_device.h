@@ -99,6 +99,9 @@ struct PolBF16 {
     // (kWavesDkv) are compiled for: the largest count that fits without spills
     static constexpr int kWaves = D == 64 ? 2 : 1;
     static constexpr int kWavesDkv = 2;
+    // dK/dV stage ring depth (loads issued kDkvBuffers - 1 stages ahead); a
+    // third buffer measured no faster at d = 64
+    static constexpr int kDkvBuffers = 2;
 
     __device__ static __forceinline__ int arow(int t, int m) {
         return ((m >> 2) << 3) + (t << 2) + (m & 3);
@@ -192,6 +195,7 @@ struct PolF32 {
     static constexpr int ROWS = 64;
     static constexpr int kWaves = 1;
     static constexpr int kWavesDkv = 1;
+    static constexpr int kDkvBuffers = 2;
 
     __device__ static __forceinline__ int arow(int t, int m) { return (t << 4) + m; }
     __device__ static __forceinline__ int bidx(int t, int g, int r) { return (t << 4) + (g << 2) + r; }
@@ -308,6 +312,22 @@ __device__ __forceinline__ void stage_vec64(float *dst, const float *src, int nv
 // Waits for this wave's outstanding global->LDS loads (the caller then
 // barriers so every wave's loads are visible).
 __device__ __forceinline__ void wait_stage() { __builtin_amdgcn_s_waitcnt(0); }
+
+// Waits until at most VM of this wave's vector-memory loads are outstanding
+// (s_waitcnt vmcnt(VM); expcnt and lgkmcnt left unconstrained): with loads
+// issued for two stages ahead, the older stage is complete while the newer
+// one stays in flight.
+template <int VM>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(VM >= 0 && VM < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Global->LDS loads one thread issues for one Pol::ROWS x D tile.
+template <class Pol>
+constexpr int tile_loads() {
+    return Pol::ROWS * (Pol::D / Pol::EPC) / 256;
+}
 
 // Store four consecutive elements x0..x0+3 of one output row.
 template <class T>
