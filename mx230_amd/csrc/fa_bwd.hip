@@ -394,7 +394,7 @@ __global__ __launch_bounds__(256, Pol::kWavesDkv) void dkv_kernel(Params p) {
         } else {
             wait_stage();
         }
-        __syncthreads();
+        barrier_lds();
     };
     // rows past N get p = 0 from LSE = +inf, so only the causal diagonal masks
     const int ndiag = CAUSAL ? min(nqs, BKV / BQ) : 0;

@@ -60,6 +60,13 @@ __device__ __forceinline__ float xg_sum(float x) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// Makes x opaque to the optimiser (an empty asm that "modifies" it), so a value
+// computed once before a loop is not recomputed inside it.
+template <class X>
+__device__ __forceinline__ void pin_regs(X &x) {
+    asm volatile("" : "+v"(x));
+}
+
 // fp32 -> bf16 bits, round to nearest even (v_cvt_pk_bf16_f32 on gfx950).
 __device__ __forceinline__ u16 to_bf16_bits(float x) {
     __bf16 h = (__bf16)x;
@@ -101,7 +108,11 @@ struct PolBF16 {
     static constexpr int kWavesDkv = 2;
     // dK/dV stage ring depth (loads issued kDkvBuffers - 1 stages ahead); a
     // third buffer measured no faster at d = 64
+#ifdef MXFA_DKV_NBUF
+    static constexpr int kDkvBuffers = MXFA_DKV_NBUF;
+#else
     static constexpr int kDkvBuffers = 2;
+#endif
 
     __device__ static __forceinline__ int arow(int t, int m) {
         return ((m >> 2) << 3) + (t << 2) + (m & 3);
@@ -146,9 +157,14 @@ struct PolBF16 {
             }
         }
     }
-    // flips the sign of every element (bf16 sign bits)
+    // flips the sign of every element (bf16 sign bits, two per dword). The
+    // result is pinned (pin_regs) so the compiler keeps the negated fragment
+    // live instead of recomputing it from the original inside the stage loop.
     __device__ static __forceinline__ Frag neg(Frag f) {
-        return __builtin_bit_cast(Frag, __builtin_bit_cast(i16x8, f) ^ (short)0x8000);
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        Frag r = __builtin_bit_cast(Frag, __builtin_bit_cast(u32x4, f) ^ 0x80008000u);
+        pin_regs(r);
+        return r;
     }
     // The chain operand of one 32-row block: this lane's elements (t, r) of the
     // two C tiles, as bf16, k-slot e = 4t + r <-> block row bidx(t, g, r) = 8g + e.
@@ -195,7 +211,11 @@ struct PolF32 {
     static constexpr int ROWS = 64;
     static constexpr int kWaves = 1;
     static constexpr int kWavesDkv = 1;
+#ifdef MXFA_DKV_NBUF
+    static constexpr int kDkvBuffers = MXFA_DKV_NBUF;
+#else
     static constexpr int kDkvBuffers = 2;
+#endif
 
     __device__ static __forceinline__ int arow(int t, int m) { return (t << 4) + m; }
     __device__ static __forceinline__ int bidx(int t, int g, int r) { return (t << 4) + (g << 2) + r; }
@@ -261,33 +281,68 @@ struct PolF32 {
 
 // --------------------------------------------------------------- LDS staging
 
+// Wave-wide direct global->LDS loads (global_load_lds_dwordx4 / _dword: no
+// VGPRs, no VALU). Lane i's bytes from src land at LDS address base + 16 i
+// (+ 4 i for the dword form); base is wave-uniform and goes through M0.
+//
+// They are issued from asm on purpose. The compiler's wait-count pass cannot
+// tell which LDS buffer an in-flight global->LDS load writes, so after a
+// builtin load it makes the next LDS read of ANY buffer wait for it
+// (s_waitcnt vmcnt(0)): a prefetch of the next stage would then complete
+// before the current stage computes. Loads it does not see leave the waits
+// to the kernels: wait_stage() / wait_vmcnt<>() and a barrier before a stage
+// is read, and a barrier after a buffer's last read before it is refilled.
+// M0 is saved and restored around each load, so the compiler's own uses of
+// M0 are unaffected; the s_nop covers the M0-write -> LDS-DMA hazard.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the host pass rejects the address-space cast
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+#else
+    return 0;
+#endif
+}
+__device__ __forceinline__ void lds_dma16(uint32_t base, const void *src) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    uint32_t save;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+        : "=&s"(save)
+        : "v"(src), "s"(__builtin_amdgcn_readfirstlane(base)));
+#endif
+}
+__device__ __forceinline__ void lds_dma4(uint32_t base, const void *src) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    uint32_t save;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\t"
+        "global_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+        : "=&s"(save)
+        : "v"(src), "s"(__builtin_amdgcn_readfirstlane(base)));
+#endif
+}
+
 // Copies rows [0, Pol::ROWS) of a row-major [*, D] matrix into an LDS tile in
-// the policy's layout with direct global->LDS loads (global_load_lds_dwordx4: no VGPRs, no
-// VALU; lane i of a wave-wide load lands at LDS base + 16 i, so each lane
-// fetches the global chunk that belongs at its LDS position). Rows >= nvalid
-// re-read row nvalid-1 (in bounds; the kernels mask their scores). Called by
-// all 256 threads; completion is awaited with wait_stage() + a barrier.
-template <class Pol>
+// the policy's layout: load k of the wave fills 16-byte positions
+// P = k NT + 64 wave + lane, and each lane fetches the global chunk that
+// belongs at its position. Rows >= nvalid re-read row nvalid-1 (in bounds; the
+// kernels mask or zero their scores). Called by all NT threads of the
+// workgroup.
+template <class Pol, int NT = 256>
 __device__ __forceinline__ void stage_rows(typename Pol::T *tile, const typename Pol::T *src, int nvalid,
                                            int tid, int wave) {
     constexpr int CPR = Pol::D / Pol::EPC;
     constexpr int NCH = Pol::ROWS * CPR;
-    static_assert(NCH % 256 == 0, "whole wave-wide loads");
-    // (device pass only: the host pass rejects the LDS address-space cast, and
-    // clang then refuses the next call site of the same specialization)
-#if defined(__HIP_DEVICE_COMPILE__)
+    static_assert(NCH % NT == 0, "whole wave-wide loads");
+    const uint32_t base = lds_addr(tile) + wave * 64 * 16;
 #pragma unroll
-    for (int k = 0; k < NCH / 256; ++k) {
-        const int P = k * 256 + tid;
+    for (int k = 0; k < NCH / NT; ++k) {
+        const int P = k * NT + tid;
         int row, c;
         Pol::chunk_at(P, row, c);
         const int grow = min(row, nvalid - 1);
-        const typename Pol::T *g = src + (size_t)grow * Pol::D + c * Pol::EPC;
-        auto *dst = (__attribute__((address_space(3))) void *)(reinterpret_cast<char *>(tile) +
-                                                                (k * 256 + wave * 64) * 16);
-        __builtin_amdgcn_global_load_lds(g, dst, 16, 0, 0);
+        lds_dma16(base + k * NT * 16, src + (size_t)grow * Pol::D + c * Pol::EPC);
     }
-#endif
 }
 
 // One K/V stage: Pol::ROWS key rows from k0 of K and V into LDS buffers.
@@ -303,15 +358,19 @@ __device__ const float kPosInf = __builtin_inff();
 
 // 64 fp32 values src[l] (l < nvalid, else *pad) -> dst[l], by one wave.
 __device__ __forceinline__ void stage_vec64(float *dst, const float *src, int nvalid, int lane, const float *pad) {
-#if defined(__HIP_DEVICE_COMPILE__)
-    const float *g = lane < nvalid ? src + lane : pad;
-    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)dst, 4, 0, 0);
-#endif
+    lds_dma4(lds_addr(dst), lane < nvalid ? src + lane : pad);
 }
 
 // Waits for this wave's outstanding global->LDS loads (the caller then
 // barriers so every wave's loads are visible).
 __device__ __forceinline__ void wait_stage() { __builtin_amdgcn_s_waitcnt(0); }
+
+// Workgroup barrier that waits only for this wave's LDS operations.
+// __syncthreads() also waits for every outstanding vector-memory operation
+// (s_waitcnt vmcnt(0) before s_barrier), which would drain global->LDS loads
+// issued for later stages; this one leaves them in flight. The asm is a
+// compiler memory barrier, so no LDS access moves across it.
+__device__ __forceinline__ void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Waits until at most VM of this wave's vector-memory loads are outstanding
 // (s_waitcnt vmcnt(VM); expcnt and lgkmcnt left unconstrained): with loads
