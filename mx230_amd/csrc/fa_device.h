@@ -108,11 +108,7 @@ struct PolBF16 {
     static constexpr int kWavesDkv = 2;
     // dK/dV stage ring depth (loads issued kDkvBuffers - 1 stages ahead); a
     // third buffer measured no faster at d = 64
-#ifdef MXFA_DKV_NBUF
-    static constexpr int kDkvBuffers = MXFA_DKV_NBUF;
-#else
     static constexpr int kDkvBuffers = 2;
-#endif
 
     __device__ static __forceinline__ int arow(int t, int m) {
         return ((m >> 2) << 3) + (t << 2) + (m & 3);
@@ -186,8 +182,7 @@ struct PolBF16 {
     // (lane (g, j) of a 16-lane group addresses row blk + 8g + 4h + j/4,
     // columns y0 + 4(j%4)..+3, and receives column y0 + j of those 4 rows):
     // k-slot e of both operands <-> row blk + 8g + e.
-    __device__ static __forceinline__ f32x4 chain(f32x4 acc, const ChainB &b, const T *tile, int y0, int blk,
-                                                  int g, int l16) {
+    __device__ static __forceinline__ Frag chain_a(const T *tile, int y0, int blk, int g, int l16) {
         const char *base = reinterpret_cast<const char *>(tile);
         const int r0 = blk + 8 * g + (l16 >> 2);
         const int col = y0 + 4 * (l16 & 3);
@@ -195,8 +190,11 @@ struct PolBF16 {
         const int off_hi = chunk_off(r0 + 4, col >> 3) + ((col & 7) << 1);
         const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(base + off_lo));
         const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(base + off_hi));
-        const i16x8 av = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-        return mma(__builtin_bit_cast(Frag, av), b, acc);
+        return __builtin_bit_cast(Frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+    __device__ static __forceinline__ f32x4 chain(f32x4 acc, const ChainB &b, const T *tile, int y0, int blk,
+                                                  int g, int l16) {
+        return mma(chain_a(tile, y0, blk, g, l16), b, acc);
     }
 };
 
@@ -211,11 +209,7 @@ struct PolF32 {
     static constexpr int ROWS = 64;
     static constexpr int kWaves = 1;
     static constexpr int kWavesDkv = 1;
-#ifdef MXFA_DKV_NBUF
-    static constexpr int kDkvBuffers = MXFA_DKV_NBUF;
-#else
     static constexpr int kDkvBuffers = 2;
-#endif
 
     __device__ static __forceinline__ int arow(int t, int m) { return (t << 4) + m; }
     __device__ static __forceinline__ int bidx(int t, int g, int r) { return (t << 4) + (g << 2) + r; }
