@@ -153,12 +153,12 @@ __device__ __forceinline__ void dq_stage(f32x4 (&acc)[Pol::D / 16][2], const typ
     }
 }
 
-template <class Pol, bool CAUSAL>
-__global__ __launch_bounds__(256, Pol::kWaves) void dq_kernel(Params p) {
+template <class Pol, bool CAUSAL, int NW>
+__global__ __launch_bounds__(64 * NW, Pol::kWaves * 4 / NW) void dq_kernel(Params p) {
     using T = typename Pol::T;
     using Frag = typename Pol::Frag;
     constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
-    constexpr int BQ = 128, BK = Pol::ROWS;
+    constexpr int BQ = 32 * NW, BK = Pol::ROWS, NT = 64 * NW;
 
     __shared__ __attribute__((aligned(16))) T sK[2][BK * D];
     __shared__ __attribute__((aligned(16))) T sV[2][BK * D];
@@ -198,13 +198,13 @@ __global__ __launch_bounds__(256, Pol::kWaves) void dq_kernel(Params p) {
     const int kend = CAUSAL ? min(N, qb * BQ + BQ) : N;
     const int nsteps = (kend + BK - 1) / BK;
 
-    stage_kv<Pol>(sK[0], sV[0], K, V, 0, N, tid, wave);
+    stage_kv<Pol, NT>(sK[0], sV[0], K, V, 0, N, tid, wave);
     wait_stage();
     __syncthreads();
 
     for (int st = 0; st < nsteps; ++st) {
         const int cur = st & 1;
-        if (st + 1 < nsteps) stage_kv<Pol>(sK[cur ^ 1], sV[cur ^ 1], K, V, (st + 1) * BK, N, tid, wave);
+        if (st + 1 < nsteps) stage_kv<Pol, NT>(sK[cur ^ 1], sV[cur ^ 1], K, V, (st + 1) * BK, N, tid, wave);
         const int k0 = st * BK;
         if (!CAUSAL || k0 <= q0 + 31) {
             const bool need_mask = (k0 + BK > N) || (CAUSAL && k0 + BK - 1 > q0);
@@ -231,216 +231,9 @@ __global__ __launch_bounds__(256, Pol::kWaves) void dq_kernel(Params p) {
 
 // ---------------------------------------------------------------- dK/dV pass
 
-// One 64-query stage of the dK/dV pass for one wave (16*KT keys). vf holds -V
-// and the dP accumulators start at Delta, so they come out as Delta - dP and
-// accK accumulates -dK / scale (the epilogue multiplies by -scale).
-template <class Pol, int KT, bool CAUSAL, bool MASK>
-__device__ __forceinline__ void dkv_stage(f32x4 (&accK)[Pol::D / 16][KT], f32x4 (&accV)[Pol::D / 16][KT],
-                                          const typename Pol::Frag (&kf)[KT][Pol::NC],
-                                          const typename Pol::Frag (&vf)[KT][Pol::NC], const typename Pol::T *sq,
-                                          const typename Pol::T *sdo, const float *sl, const float *sd, int qs,
-                                          int kw0, int N, float scale_log2, int g, int l16) {
-    using Frag = typename Pol::Frag;
-    constexpr int NC = Pol::NC, XT = Pol::D / 16;
-#pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
-        f32x4 s[2][KT], dp[2][KT];  // [t][kt]
-        f32x4 L2[2];
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            // block rows bidx(t, g, 0..3) are consecutive: one 16-byte LDS read
-            const int q4 = 32 * blk + Pol::bidx(t, g, 0);
-            L2[t] = *reinterpret_cast<const f32x4 *>(sl + q4) * kLog2e;
-            const f32x4 dl = *reinterpret_cast<const f32x4 *>(sd + q4);
-            Frag a[NC];
-            const int n = 32 * blk + Pol::arow(t, l16);
-            Pol::lds_row_frags(a, sq, n, g);
-#pragma unroll
-            for (int kt = 0; kt < KT; ++kt) {
-                f32x4 c = zero4();
-#pragma unroll
-                for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], kf[kt][kc], c);
-                s[t][kt] = c;
-            }
-            Pol::lds_row_frags(a, sdo, n, g);
-#pragma unroll
-            for (int kt = 0; kt < KT; ++kt) {
-                f32x4 c = dl;
-#pragma unroll
-                for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], vf[kt][kc], c);
-                dp[t][kt] = c;
-            }
-        }
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-#pragma unroll
-                for (int kt = 0; kt < KT; ++kt) {
-                    float x = s[t][kt][r] * scale_log2 - L2[t][r];
-                    if constexpr (MASK) {
-                        // causal: query qs + 32 blk + bidx(t, g, r) before key kw0 + 16 kt + l16
-                        const bool before = Pol::bidx(t, g, r) - l16 < kw0 - qs + 16 * kt - 32 * blk;
-                        x = before ? -INFINITY : x;
-                    }
-                    const float pv = fast_exp2(x);
-                    s[t][kt][r] = pv;
-                    dp[t][kt][r] = pv * dp[t][kt][r];  // -dS / scale
-                }
-            }
-        }
-        typename Pol::ChainB cp[KT], cds[KT];
-#pragma unroll
-        for (int kt = 0; kt < KT; ++kt) {
-            cp[kt] = Pol::pack(s[0][kt], s[1][kt]);
-            cds[kt] = Pol::pack(dp[0][kt], dp[1][kt]);
-        }
-#pragma unroll
-        for (int xt = 0; xt < XT; ++xt) {
-#pragma unroll
-            for (int kt = 0; kt < KT; ++kt) {
-                accV[xt][kt] = Pol::chain(accV[xt][kt], cp[kt], sdo, 16 * xt, 32 * blk, g, l16);
-                accK[xt][kt] = Pol::chain(accK[xt][kt], cds[kt], sq, 16 * xt, 32 * blk, g, l16);
-            }
-        }
-    }
-}
-
-template <class Pol, int KT, bool CAUSAL>
-__global__ __launch_bounds__(256, Pol::kWavesDkv) void dkv_kernel(Params p) {
-    using T = typename Pol::T;
-    using Frag = typename Pol::Frag;
-    constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
-    constexpr int BKV = 64 * KT;      // keys per workgroup
-    constexpr int BQ = Pol::ROWS;     // queries per stage
-    static_assert(BKV % BQ == 0, "causal start must align to a stage");
-
-    // NBUF-deep ring of stages: loads are issued NBUF-1 stages ahead
-    constexpr int NBUF = Pol::kDkvBuffers;
-    __shared__ __attribute__((aligned(16))) T sQ[NBUF][BQ * D];
-    __shared__ __attribute__((aligned(16))) T sdO[NBUF][BQ * D];
-    __shared__ __attribute__((aligned(16))) float sL[NBUF][BQ];
-    __shared__ __attribute__((aligned(16))) float sD[NBUF][BQ];
-
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int g = lane >> 4, l16 = lane & 15;
-    const int N = p.N;
-    const int bkv = blockIdx.x;  // b * Hkv + kvh
-    const int kb = blockIdx.y;   // causal: block 0 (most queries) is dispatched first
-    const int b = bkv / p.Hkv, kvh = bkv % p.Hkv;
-    const size_t kvoff = (size_t)bkv * N * D;
-    const T *K = static_cast<const T *>(p.k) + kvoff;
-    const T *V = static_cast<const T *>(p.v) + kvoff;
-    const int kw0 = kb * BKV + wave * 16 * KT;  // first key of this wave
-
-    Frag kf[KT][NC], vf[KT][NC];
-#pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
-        const int key = kw0 + 16 * kt + l16;
-        Pol::gmem_row_frags(kf[kt], K + (size_t)key * D, g, key < N);
-        Pol::gmem_row_frags(vf[kt], V + (size_t)key * D, g, key < N);
-#pragma unroll
-        for (int kc = 0; kc < NC; ++kc) vf[kt][kc] = Pol::neg(vf[kt][kc]);
-    }
-    f32x4 accK[XT][KT], accV[XT][KT];
-#pragma unroll
-    for (int xt = 0; xt < XT; ++xt) {
-#pragma unroll
-        for (int kt = 0; kt < KT; ++kt) accK[xt][kt] = accV[xt][kt] = zero4();
-    }
-
-    const int qstart = CAUSAL ? kb * BKV : 0;
-    const int nqs = (N - qstart + BQ - 1) / BQ;  // stages per query head
-    const int nsteps = nqs * p.group;
-    const size_t bh0 = (size_t)b * p.Hq + (size_t)kvh * p.group;
-
-    auto issue = [&](int st) __attribute__((always_inline)) {
-        const int bf = st % NBUF;
-        stage_qdo<Pol>(sQ[bf], sdO[bf], sL[bf], sD[bf], p, bh0 + st / nqs, qstart + (st % nqs) * BQ, N, tid,
-                       wave, lane);
-    };
-    // loads of one stage per thread: the Q and dO tiles (+1 vector on waves
-    // 0-1, which the waits below may over-wait by one load)
-    constexpr int kLoads = 2 * tile_loads<Pol>();
-#pragma unroll
-    for (int i = 0; i < NBUF - 1; ++i) {
-        if (i < nsteps) issue(i);
-    }
-    if (NBUF > 2 && nsteps > 1) {
-        wait_vmcnt<kLoads>();
-    } else {
-        wait_stage();
-    }
-    __syncthreads();
-
-    // One stage: prefetch stage st + NBUF - 1, compute stage st, then wait for
-    // stage st + 1 and barrier. Causal: the stages that straddle the diagonal
-    // are the first ceil(BKV / BQ) of each query head (queries from kb * BKV);
-    // they run in a loop of their own with the masked body, so neither loop
-    // carries the other's code (two bodies behind one branch make the register
-    // allocator spill).
-    auto run = [&](auto mask_tag, int st) __attribute__((always_inline)) {
-        constexpr bool MASK = decltype(mask_tag)::value;
-        const int cur = st % NBUF;
-        const bool ahead = st + NBUF - 1 < nsteps;
-        if (ahead) issue(st + NBUF - 1);
-        const int qs = qstart + (st % nqs) * BQ;
-        // a wave whose keys all follow the stage's queries has nothing to do
-        if (!CAUSAL || qs + BQ - 1 >= kw0) {
-            dkv_stage<Pol, KT, CAUSAL, MASK>(accK, accV, kf, vf, sQ[cur], sdO[cur], sL[cur], sD[cur], qs, kw0, N,
-                                             p.scale_log2, g, l16);
-        }
-        if (NBUF > 2 && ahead) {
-            wait_vmcnt<kLoads>();
-        } else {
-            wait_stage();
-        }
-        barrier_lds();
-    };
-    // rows past N get p = 0 from LSE = +inf, so only the causal diagonal masks
-    const int ndiag = CAUSAL ? min(nqs, BKV / BQ) : 0;
-    for (int hh = 0, st = 0; hh < p.group; ++hh) {
-        for (int i = 0; i < ndiag; ++i, ++st) run(std::true_type{}, st);
-        for (int i = ndiag; i < nqs; ++i, ++st) run(std::false_type{}, st);
-    }
-
-    T *dK = static_cast<T *>(p.dk) + kvoff;
-    T *dV = static_cast<T *>(p.dv) + kvoff;
-#pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
-        const int key = kw0 + 16 * kt + l16;
-        if (key < N) {
-#pragma unroll
-            for (int xt = 0; xt < XT; ++xt) {
-                store4<T>(dK + (size_t)key * D + 16 * xt + 4 * g, accK[xt][kt], -p.scale);
-                store4<T>(dV + (size_t)key * D + 16 * xt + 4 * g, accV[xt][kt], 1.0f);
-            }
-        }
-    }
-}
-
-// ------------------------------------------------- dK/dV pass, ping-pong form
-
-// The dK/dV pass for bf16, d = 64, with two wave groups per workgroup that
-// take turns on the matrix cores. A workgroup owns 128 keys; waves w and w + 4
-// (which the hardware places on the same SIMD) both own keys 32w..32w+31.
-// Group A (waves 0-3) takes query block 0 (rows 0-31) of every 64-query stage
-// and group B (waves 4-7) block 1, so each wave handles one block per stage in
-// two phases:
-//   M: the chained GEMMs of its previous block (dV += P^T dO, dK += dS^T Q,
-//      16 MFMAs, their LDS operands already in registers) and the scores and
-//      dP of the current block (16 MFMAs);
-//   V: the softmax recompute and dS of the current block (VALU and exp), the
-//      transposed LDS reads of that block's chain operands for the next M, and
-//      the group's share of the global->LDS loads of stage + 2.
-// Group B runs one phase behind group A and a barrier separates the phases,
-// so while one wave of a SIMD issues MFMAs the other issues VALU, LDS and
-// global-load work. The loads are split between the groups (B: Q tiles,
-// A: dO tiles and the LSE / Delta vectors) because a wave stalls on issuing
-// more than a couple of wide loads at once. Stages rotate through a 4-deep LDS
-// ring (a stage's buffer is last read by group B's V one stage later). At the
-// end the two groups exchange partial sums through LDS: A stores dK, B dV.
+// Building blocks of the ping-pong dK/dV kernel (bf16, d = 64, 32 keys per
+// wave), split so the LDS reads of a block's operands can be issued a phase
+// before the MFMAs that use them.
 namespace pp {
 
 constexpr int kNbuf = 4;
@@ -545,6 +338,218 @@ __device__ __forceinline__ void softmax_block(f32x4 (&s)[2][2], f32x4 (&dp)[2][2
 }
 
 }  // namespace pp
+
+// One 64-query stage of the dK/dV pass for one wave (16*KT keys). vf holds -V
+// and the dP accumulators start at Delta, so they come out as Delta - dP and
+// accK accumulates -dK / scale (the epilogue multiplies by -scale).
+template <class Pol, int KT, bool CAUSAL, bool MASK>
+__device__ __forceinline__ void dkv_stage(f32x4 (&accK)[Pol::D / 16][KT], f32x4 (&accV)[Pol::D / 16][KT],
+                                          const typename Pol::Frag (&kf)[KT][Pol::NC],
+                                          const typename Pol::Frag (&vf)[KT][Pol::NC], const typename Pol::T *sq,
+                                          const typename Pol::T *sdo, const float *sl, const float *sd, int qs,
+                                          int kw0, int N, float scale_log2, int g, int l16) {
+    using Frag = typename Pol::Frag;
+    constexpr int NC = Pol::NC, XT = Pol::D / 16;
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+        f32x4 s[2][KT], dp[2][KT];  // [t][kt]
+        f32x4 L2[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            // block rows bidx(t, g, 0..3) are consecutive: one 16-byte LDS read
+            const int q4 = 32 * blk + Pol::bidx(t, g, 0);
+            L2[t] = *reinterpret_cast<const f32x4 *>(sl + q4) * kLog2e;
+            const f32x4 dl = *reinterpret_cast<const f32x4 *>(sd + q4);
+            Frag a[NC];
+            const int n = 32 * blk + Pol::arow(t, l16);
+            Pol::lds_row_frags(a, sq, n, g);
+#pragma unroll
+            for (int kt = 0; kt < KT; ++kt) {
+                f32x4 c = zero4();
+#pragma unroll
+                for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], kf[kt][kc], c);
+                s[t][kt] = c;
+            }
+            Pol::lds_row_frags(a, sdo, n, g);
+#pragma unroll
+            for (int kt = 0; kt < KT; ++kt) {
+                f32x4 c = dl;
+#pragma unroll
+                for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], vf[kt][kc], c);
+                dp[t][kt] = c;
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+#pragma unroll
+                for (int kt = 0; kt < KT; ++kt) {
+                    float x = s[t][kt][r] * scale_log2 - L2[t][r];
+                    if constexpr (MASK) {
+                        // causal: query qs + 32 blk + bidx(t, g, r) before key kw0 + 16 kt + l16
+                        const bool before = Pol::bidx(t, g, r) - l16 < kw0 - qs + 16 * kt - 32 * blk;
+                        x = before ? -INFINITY : x;
+                    }
+                    const float pv = fast_exp2(x);
+                    s[t][kt][r] = pv;
+                    dp[t][kt][r] = pv * dp[t][kt][r];  // -dS / scale
+                }
+            }
+        }
+        typename Pol::ChainB cp[KT], cds[KT];
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) {
+            cp[kt] = Pol::pack(s[0][kt], s[1][kt]);
+            cds[kt] = Pol::pack(dp[0][kt], dp[1][kt]);
+        }
+#pragma unroll
+        for (int xt = 0; xt < XT; ++xt) {
+#pragma unroll
+            for (int kt = 0; kt < KT; ++kt) {
+                accV[xt][kt] = Pol::chain(accV[xt][kt], cp[kt], sdo, 16 * xt, 32 * blk, g, l16);
+                accK[xt][kt] = Pol::chain(accK[xt][kt], cds[kt], sq, 16 * xt, 32 * blk, g, l16);
+            }
+        }
+    }
+}
+
+template <class Pol, int KT, bool CAUSAL, int NW>
+__global__ __launch_bounds__(64 * NW, Pol::kWavesDkv * 4 / NW) void dkv_kernel(Params p) {
+    using T = typename Pol::T;
+    using Frag = typename Pol::Frag;
+    constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
+    constexpr int NT = 64 * NW;       // threads per workgroup
+    constexpr int BKV = 16 * KT * NW; // keys per workgroup
+    constexpr int BQ = Pol::ROWS;     // queries per stage
+    static_assert(BKV % BQ == 0, "causal start must align to a stage");
+
+    // NBUF-deep ring of stages: loads are issued NBUF-1 stages ahead
+    constexpr int NBUF = Pol::kDkvBuffers;
+    __shared__ __attribute__((aligned(16))) T sQ[NBUF][BQ * D];
+    __shared__ __attribute__((aligned(16))) T sdO[NBUF][BQ * D];
+    __shared__ __attribute__((aligned(16))) float sL[NBUF][BQ];
+    __shared__ __attribute__((aligned(16))) float sD[NBUF][BQ];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, l16 = lane & 15;
+    const int N = p.N;
+    const int bkv = blockIdx.x;  // b * Hkv + kvh
+    const int kb = blockIdx.y;   // causal: block 0 (most queries) is dispatched first
+    const int b = bkv / p.Hkv, kvh = bkv % p.Hkv;
+    const size_t kvoff = (size_t)bkv * N * D;
+    const T *K = static_cast<const T *>(p.k) + kvoff;
+    const T *V = static_cast<const T *>(p.v) + kvoff;
+    const int kw0 = kb * BKV + wave * 16 * KT;  // first key of this wave
+
+    Frag kf[KT][NC], vf[KT][NC];
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+        const int key = kw0 + 16 * kt + l16;
+        Pol::gmem_row_frags(kf[kt], K + (size_t)key * D, g, key < N);
+        Pol::gmem_row_frags(vf[kt], V + (size_t)key * D, g, key < N);
+#pragma unroll
+        for (int kc = 0; kc < NC; ++kc) vf[kt][kc] = Pol::neg(vf[kt][kc]);
+    }
+    f32x4 accK[XT][KT], accV[XT][KT];
+#pragma unroll
+    for (int xt = 0; xt < XT; ++xt) {
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) accK[xt][kt] = accV[xt][kt] = zero4();
+    }
+
+    const int qstart = CAUSAL ? kb * BKV : 0;
+    const int nqs = (N - qstart + BQ - 1) / BQ;  // stages per query head
+    const int nsteps = nqs * p.group;
+    const size_t bh0 = (size_t)b * p.Hq + (size_t)kvh * p.group;
+
+    auto issue = [&](int st) __attribute__((always_inline)) {
+        const int bf = st % NBUF;
+        stage_qdo<Pol, NT>(sQ[bf], sdO[bf], sL[bf], sD[bf], p, bh0 + st / nqs, qstart + (st % nqs) * BQ, N, tid,
+                           wave, lane);
+    };
+    // loads of one stage per thread: the Q and dO tiles (+1 vector on waves
+    // 0-1, which the waits below may over-wait by one load)
+    constexpr int kLoads = 2 * tile_loads<Pol, NT>();
+#pragma unroll
+    for (int i = 0; i < NBUF - 1; ++i) {
+        if (i < nsteps) issue(i);
+    }
+    if (NBUF > 2 && nsteps > 1) {
+        wait_vmcnt<kLoads>();
+    } else {
+        wait_stage();
+    }
+    __syncthreads();
+
+    // One stage: prefetch stage st + NBUF - 1, compute stage st, then wait for
+    // stage st + 1 and barrier. Causal: the stages that straddle the diagonal
+    // are the first ceil(BKV / BQ) of each query head (queries from kb * BKV);
+    // they run in a loop of their own with the masked body, so neither loop
+    // carries the other's code (two bodies behind one branch make the register
+    // allocator spill).
+    auto run = [&](auto mask_tag, int st) __attribute__((always_inline)) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        const int cur = st % NBUF;
+        const bool ahead = st + NBUF - 1 < nsteps;
+        if (ahead) issue(st + NBUF - 1);
+        const int qs = qstart + (st % nqs) * BQ;
+        // a wave whose keys all follow the stage's queries has nothing to do
+        if (!CAUSAL || qs + BQ - 1 >= kw0) {
+            dkv_stage<Pol, KT, CAUSAL, MASK>(accK, accV, kf, vf, sQ[cur], sdO[cur], sL[cur], sD[cur], qs, kw0, N,
+                                             p.scale_log2, g, l16);
+        }
+        if (NBUF > 2 && ahead) {
+            wait_vmcnt<kLoads>();
+        } else {
+            wait_stage();
+        }
+        barrier_lds();
+    };
+    // rows past N get p = 0 from LSE = +inf, so only the causal diagonal masks
+    const int ndiag = CAUSAL ? min(nqs, BKV / BQ) : 0;
+    for (int hh = 0, st = 0; hh < p.group; ++hh) {
+        for (int i = 0; i < ndiag; ++i, ++st) run(std::true_type{}, st);
+        for (int i = ndiag; i < nqs; ++i, ++st) run(std::false_type{}, st);
+    }
+
+    T *dK = static_cast<T *>(p.dk) + kvoff;
+    T *dV = static_cast<T *>(p.dv) + kvoff;
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+        const int key = kw0 + 16 * kt + l16;
+        if (key < N) {
+#pragma unroll
+            for (int xt = 0; xt < XT; ++xt) {
+                store4<T>(dK + (size_t)key * D + 16 * xt + 4 * g, accK[xt][kt], -p.scale);
+                store4<T>(dV + (size_t)key * D + 16 * xt + 4 * g, accV[xt][kt], 1.0f);
+            }
+        }
+    }
+}
+
+// ------------------------------------------------- dK/dV pass, ping-pong form
+
+// The dK/dV pass for bf16, d = 64, with two wave groups per workgroup that
+// take turns on the matrix cores. A workgroup owns 128 keys; waves w and w + 4
+// (which the hardware places on the same SIMD) both own keys 32w..32w+31.
+// Group A (waves 0-3) takes query block 0 (rows 0-31) of every 64-query stage
+// and group B (waves 4-7) block 1, so each wave handles one block per stage in
+// two phases:
+//   M: the chained GEMMs of its previous block (dV += P^T dO, dK += dS^T Q,
+//      16 MFMAs, their LDS operands already in registers) and the scores and
+//      dP of the current block (16 MFMAs);
+//   V: the softmax recompute and dS of the current block (VALU and exp), the
+//      transposed LDS reads of that block's chain operands for the next M, and
+//      the group's share of the global->LDS loads of stage + 2.
+// Group B runs one phase behind group A and a barrier separates the phases,
+// so while one wave of a SIMD issues MFMAs the other issues VALU, LDS and
+// global-load work. The loads are split between the groups (B: Q tiles,
+// A: dO tiles and the LSE / Delta vectors) because a wave stalls on issuing
+// more than a couple of wide loads at once. Stages rotate through a 4-deep LDS
+// ring (a stage's buffer is last read by group B's V one stage later). At the
+// end the two groups exchange partial sums through LDS: A stores dK, B dV.
 
 template <bool CAUSAL>
 __global__ __launch_bounds__(512) void dkv_pp_kernel(Params p) {
@@ -760,10 +765,10 @@ hipError_t launch_preprocess(const Params &p, int dtype_bf16, int d, hipStream_t
     return hipGetLastError();
 }
 
-template <class Pol, bool CAUSAL>
+template <class Pol, bool CAUSAL, int NW = 4>
 static hipError_t launch_dq_t(const Params &p, hipStream_t stream) {
-    const dim3 grid(p.B * p.Hq, (p.N + 127) / 128);
-    hipLaunchKernelGGL((dq_kernel<Pol, CAUSAL>), grid, dim3(256), 0, stream, p);
+    const dim3 grid(p.B * p.Hq, (p.N + 32 * NW - 1) / (32 * NW));
+    hipLaunchKernelGGL((dq_kernel<Pol, CAUSAL, NW>), grid, dim3(64 * NW), 0, stream, p);
     return hipGetLastError();
 }
 
@@ -799,10 +804,10 @@ static hipError_t launch_dkv_pp(const Params &p, hipStream_t stream) {
     return hipGetLastError();
 }
 
-template <class Pol, int KT, bool CAUSAL>
+template <class Pol, int KT, bool CAUSAL, int NW = 4>
 static hipError_t launch_dkv_t(const Params &p, hipStream_t stream) {
-    const dim3 grid(p.B * p.Hkv, (p.N + 64 * KT - 1) / (64 * KT));
-    hipLaunchKernelGGL((dkv_kernel<Pol, KT, CAUSAL>), grid, dim3(256), 0, stream, p);
+    const dim3 grid(p.B * p.Hkv, (p.N + 16 * KT * NW - 1) / (16 * KT * NW));
+    hipLaunchKernelGGL((dkv_kernel<Pol, KT, CAUSAL, NW>), grid, dim3(64 * NW), 0, stream, p);
     return hipGetLastError();
 }
 

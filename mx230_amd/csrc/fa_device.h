@@ -340,11 +340,11 @@ __device__ __forceinline__ void stage_rows(typename Pol::T *tile, const typename
 }
 
 // One K/V stage: Pol::ROWS key rows from k0 of K and V into LDS buffers.
-template <class Pol>
+template <class Pol, int NT = 256>
 __device__ __forceinline__ void stage_kv(typename Pol::T *sk, typename Pol::T *sv, const typename Pol::T *K,
                                          const typename Pol::T *V, int k0, int N, int tid, int wave) {
-    stage_rows<Pol>(sk, K + (size_t)k0 * Pol::D, N - k0, tid, wave);
-    stage_rows<Pol>(sv, V + (size_t)k0 * Pol::D, N - k0, tid, wave);
+    stage_rows<Pol, NT>(sk, K + (size_t)k0 * Pol::D, N - k0, tid, wave);
+    stage_rows<Pol, NT>(sv, V + (size_t)k0 * Pol::D, N - k0, tid, wave);
 }
 
 // Read by lanes past the end of a staged vector (see stage_vec64).
@@ -376,10 +376,11 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Global->LDS loads one thread issues for one Pol::ROWS x D tile.
-template <class Pol>
+// Global->LDS loads one thread of an NT-thread workgroup issues for one
+// Pol::ROWS x D tile.
+template <class Pol, int NT = 256>
 constexpr int tile_loads() {
-    return Pol::ROWS * (Pol::D / Pol::EPC) / 256;
+    return Pol::ROWS * (Pol::D / Pol::EPC) / NT;
 }
 
 // Store four consecutive elements x0..x0+3 of one output row.
