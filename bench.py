@@ -7,13 +7,14 @@ reference (02-flash-attention/src/main.rs:599-611). One timed step = one full
 backward pass: Delta preprocess + dK/dV pass + dQ pass, inputs resident in HBM.
 
 Prints one JSON line. ``value`` is the algorithmic backward throughput
-(10 N^2 d per (batch, head), halved for causal) in TFLOP/s; ``roofline`` is the
-dominant kernel's achieved MFMA rate against MI355X's dense bf16 peak; and
-``cpu_baseline`` times the CPU oracle (a C restatement of the reference's CPU
-backward, main.rs:246-300) on a bounded sample of the same workload on this
-host.
+(10 N^2 d per (batch, head), halved for causal) in TFLOP/s. ``roofline`` is the
+dominant kernel's achieved MFMA rate against MI355X's dense bf16 peak, with the
+probe kernels' ceilings measured in the same run beside it (``measured_peak``,
+``hbm_measured_gbps``). ``cpu_baseline`` times the CPU oracle (a C restatement
+of the reference's CPU backward, main.rs:246-300) on a bounded sample of the
+same workload on this host.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-probe]
        [--B 4 --H 12 --Hkv 12 --N 4096 --d 64 --causal 1 --dtype bf16]
 """
 from __future__ import annotations
@@ -44,6 +45,8 @@ def parse():
     ap.add_argument("--causal", type=int, default=1)
     ap.add_argument("--dtype", choices=["bf16", "f32"], default="bf16")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--no-probe", action="store_true",
+                    help="skip the roofline probes (measured MFMA / HBM ceilings, after the timed region)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run a plain device-to-device copy of MIB "
                          "MiB three times (calibrates the FETCH_SIZE / WRITE_SIZE counters)")
@@ -205,6 +208,14 @@ def main():
         "fwd": {"ms": round(fwd_avg, 4),
                 "tflops": round(mx.fwd_flops(a.B, a.H, a.N, a.d, causal) / (fwd_avg * 1e-3) / 1e12, 2)},
     }
+    if not a.no_probe:
+        # measured ceilings (probe kernels, after the timed region): the same
+        # MFMA pipe at full occupancy with independent accumulators, and HBM
+        # streaming reads; `peak` stays AMD's published figure
+        mfma = mx.probe_mfma_tflops(bf16=a.dtype == "bf16", iters=256)
+        res["roofline"]["measured_peak"] = round(mfma, 1)
+        res["roofline"]["frac_of_measured"] = round(achieved / mfma, 4)
+        res["roofline"]["hbm_measured_gbps"] = round(mx.probe_hbm_gbps(mib=1024), 1)
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline(a, hkv)
     print(json.dumps(res), flush=True)

@@ -144,6 +144,25 @@ size_t mxfa_naive_scratch_bytes(const mxfa_shape *shape);
 int mxfa_run_naive_fwd(const mxfa_shape *shape, const void *q, const void *k, const void *v,
                        float *s, void *o, void *stream);
 
+/* ---- Roofline probes: measured ceilings next to the published peaks.
+ * Replace the reference's throughput audit, common/kernels/isa.cu:11-63
+ * (fma_f32 / dp4a_s32 / fma_h2 chains and the stream_f4 read) driven by
+ * common/examples/isa.rs:17-88, with the pipes this path runs on. The caller
+ * times the launches (e.g. with events on `stream`). */
+
+/* Floats in the probes' device sink (one per probe thread). */
+int mxfa_probe_sink_len(void);
+/* Launches `iters` x 8 independent MFMAs per wave over 2048 x 256 threads:
+ * v_mfma_f32_16x16x32_bf16 for MXFA_BF16, v_mfma_f32_16x16x4_f32 for
+ * MXFA_F32. Writes the flops the launch performs to *flops. `sink` is a device
+ * float[mxfa_probe_sink_len()] (written; the values are meaningless). */
+int mxfa_probe_mfma(int dtype, int iters, float *sink, double *flops, void *stream);
+/* Launches a grid-stride streaming read of `bytes` (a multiple of 16) at `x`,
+ * the stream_f4 shape (isa.cu:55-63). */
+int mxfa_probe_read(const void *x, size_t bytes, float *sink, void *stream);
+/* Launches a grid-stride copy of `bytes` (a multiple of 16) from x to y. */
+int mxfa_probe_copy(const void *x, void *y, size_t bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

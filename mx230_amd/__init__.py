@@ -44,7 +44,8 @@ EXPORTS = (
     "mxfa_version", "mxfa_strerror", "mxfa_init", "mxfa_shutdown", "mxfa_check_shape",
     "mxfa_run_flash", "mxfa_run_flash_lse", "mxfa_run_preprocess", "mxfa_run_bwd_dq",
     "mxfa_run_bwd_dkv", "mxfa_run_bwd_flash", "mxfa_bwd_workspace_bytes", "mxfa_run_bwd_naive",
-    "mxfa_naive_scratch_bytes", "mxfa_run_naive_fwd",
+    "mxfa_naive_scratch_bytes", "mxfa_run_naive_fwd", "mxfa_probe_sink_len", "mxfa_probe_mfma",
+    "mxfa_probe_read", "mxfa_probe_copy",
 )
 
 
@@ -100,6 +101,10 @@ def load_library(path: str | None = None):
     lib.mxfa_naive_scratch_bytes.argtypes = [sp]
     lib.mxfa_naive_scratch_bytes.restype = ctypes.c_size_t
     lib.mxfa_run_naive_fwd.argtypes = [sp, vp, vp, vp, fp, vp, vp]
+    lib.mxfa_probe_sink_len.argtypes = []
+    lib.mxfa_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_int, fp, ctypes.POINTER(ctypes.c_double), vp]
+    lib.mxfa_probe_read.argtypes = [vp, ctypes.c_size_t, fp, vp]
+    lib.mxfa_probe_copy.argtypes = [vp, vp, ctypes.c_size_t, vp]
     for name in EXPORTS:
         if name not in ("mxfa_version", "mxfa_strerror", "mxfa_bwd_workspace_bytes",
                         "mxfa_naive_scratch_bytes"):
@@ -309,6 +314,65 @@ def attention_bwd(q, k, v, o, lse, do, causal: bool, scale: float = 0.0, stream=
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     run_bwd_flash(q, k, v, do, lse, delta, dq, dk, dv, causal, scale, stream)
     return dq, dk, dv
+
+
+# ----------------------------------------------------------- roofline probes --
+
+def _time_ms(launch, reps: int) -> float:
+    """Mean event time (ms) of `reps` back-to-back launches, after one warm-up."""
+    torch = _torch()
+    launch()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        launch()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / reps
+
+
+def probe_mfma_tflops(bf16: bool = True, iters: int = 256, reps: int = 5) -> float:
+    """Measured MFMA throughput (TFLOP/s) of the whole device: every wave issues
+    independent v_mfma_f32_16x16x32_bf16 (bf16) or v_mfma_f32_16x16x4_f32 (fp32)."""
+    torch = _torch()
+    lib = load_library()
+    sink = torch.empty(lib.mxfa_probe_sink_len(), dtype=torch.float32, device="cuda")
+    flops = ctypes.c_double(0.0)
+    dt = MXFA_BF16 if bf16 else MXFA_F32
+    stream = _stream(None)
+
+    def launch():
+        _check("mxfa_probe_mfma", lib.mxfa_probe_mfma(dt, iters, _ptr(sink, "sink", torch.float32),
+                                                      ctypes.byref(flops), stream))
+    ms = _time_ms(launch, reps)
+    return flops.value / (ms * 1e-3) / 1e12
+
+
+def probe_hbm_gbps(mib: int = 1024, reps: int = 5, copy: bool = False) -> float:
+    """Measured HBM streaming bandwidth (GB/s): a grid-stride read of `mib` MiB
+    (or, with copy=True, a copy of that size, counting read + write bytes)."""
+    torch = _torch()
+    lib = load_library()
+    nbytes = mib * 2**20
+    x = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    stream = _stream(None)
+    if copy:
+        y = torch.empty_like(x)
+
+        def launch():
+            _check("mxfa_probe_copy", lib.mxfa_probe_copy(_ptr(x, "x", torch.float32), _ptr(y, "y", torch.float32),
+                                                          nbytes, stream))
+        moved = 2 * nbytes
+    else:
+        sink = torch.empty(lib.mxfa_probe_sink_len(), dtype=torch.float32, device="cuda")
+
+        def launch():
+            _check("mxfa_probe_read", lib.mxfa_probe_read(_ptr(x, "x", torch.float32), nbytes,
+                                                          _ptr(sink, "sink", torch.float32), stream))
+        moved = nbytes
+    ms = _time_ms(launch, reps)
+    return moved / (ms * 1e-3) / 1e9
 
 
 def init(device: int = 0):

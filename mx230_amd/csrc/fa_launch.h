@@ -16,4 +16,11 @@ hipError_t launch_bwd_dkv(const Params &p, int dtype_bf16, int d, int causal, hi
 hipError_t launch_bwd_naive(const Params &p, int d, int causal, hipStream_t stream);
 hipError_t launch_naive_fwd(const Params &p, float *s, int d, int causal, hipStream_t stream);
 
+// roofline probes (probe.hip)
+int probe_sink_len();
+double probe_mfma_flops(int bf16, int iters);
+hipError_t launch_probe_mfma(int bf16, int iters, float *sink, hipStream_t stream);
+hipError_t launch_probe_read(const void *x, size_t bytes, float *sink, hipStream_t stream);
+hipError_t launch_probe_copy(const void *x, void *y, size_t bytes, hipStream_t stream);
+
 }  // namespace mxfa

@@ -225,4 +225,29 @@ int mxfa_run_naive_fwd(const mxfa_shape *shape, const void *q, const void *k, co
     return from_hip(mxfa::launch_naive_fwd(p, s, shape->d, shape->causal, static_cast<hipStream_t>(stream)));
 }
 
+int mxfa_probe_sink_len(void) { return mxfa::probe_sink_len(); }
+
+int mxfa_probe_mfma(int dtype, int iters, float *sink, double *flops, void *stream) {
+    if (dtype != MXFA_F32 && dtype != MXFA_BF16) return MXFA_ERR_DTYPE;
+    if (iters < 1) return MXFA_ERR_SHAPE;
+    if (sink == nullptr || flops == nullptr) return MXFA_ERR_NULL;
+    if (!aligned16(sink)) return MXFA_ERR_ALIGN;
+    *flops = mxfa::probe_mfma_flops(dtype == MXFA_BF16, iters);
+    return from_hip(mxfa::launch_probe_mfma(dtype == MXFA_BF16, iters, sink, static_cast<hipStream_t>(stream)));
+}
+
+int mxfa_probe_read(const void *x, size_t bytes, float *sink, void *stream) {
+    int rc = check_ptrs({x, sink});
+    if (rc != MXFA_OK) return rc;
+    if (bytes == 0 || bytes % 16 != 0) return MXFA_ERR_SHAPE;
+    return from_hip(mxfa::launch_probe_read(x, bytes, sink, static_cast<hipStream_t>(stream)));
+}
+
+int mxfa_probe_copy(const void *x, void *y, size_t bytes, void *stream) {
+    int rc = check_ptrs({x, y});
+    if (rc != MXFA_OK) return rc;
+    if (bytes == 0 || bytes % 16 != 0) return MXFA_ERR_SHAPE;
+    return from_hip(mxfa::launch_probe_copy(x, y, bytes, static_cast<hipStream_t>(stream)));
+}
+
 }  // extern "C"

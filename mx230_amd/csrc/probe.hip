@@ -1,0 +1,115 @@
+// Roofline probes: the measured ceilings of the MI355X pipes the flash-attention
+// kernels run on, reported next to AMD's published peaks.
+//
+// They follow the idea of the reference's instruction-throughput audit
+// (common/kernels/isa.cu:11-63 and common/examples/isa.rs:17-88: every thread
+// runs several independent chains of the instruction under test, and the
+// accumulators are written out so nothing is eliminated), re-targeted at what
+// bounds this path on CDNA4: the bf16 and fp32 MFMA pipes and HBM streaming.
+#include "fa_device.h"
+#include "fa_launch.h"
+
+namespace mxfa {
+
+namespace {
+
+constexpr int kProbeBlocks = 2048;  // 8 per CU: up to 8 waves per SIMD
+constexpr int kProbeThreads = 256;
+constexpr int kChains = 8;          // independent accumulators per wave
+
+// Each wave issues iters x kChains MFMAs whose accumulators do not depend on
+// each other, so the matrix pipe, not the dependent-issue latency, is the limit.
+template <bool BF16>
+__global__ __launch_bounds__(kProbeThreads) void probe_mfma_kernel(float *sink, int iters) {
+    const int tid = threadIdx.x;
+    f32x4 acc[kChains];
+#pragma unroll
+    for (int j = 0; j < kChains; ++j) acc[j] = zero4();
+    // the loop body is kUnroll x kChains MFMAs and nothing else (checked in the
+    // ISA): the accumulators stay in place across iterations
+    constexpr int kUnroll = 4;
+    const int outer = (iters + kUnroll - 1) / kUnroll;
+    if constexpr (BF16) {
+        bf16x8 a, b;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            a[e] = (__bf16)(0.001f * (float)((tid + e) & 7));
+            b[e] = (__bf16)(0.002f * (float)((tid ^ e) & 7));
+        }
+        // (asm: with the builtin the compiler rotates the accumulators through
+        // AGPRs, 56 moves per 32 MFMAs; here they stay in their VGPRs. A and B
+        // are loop-invariant and each accumulator recurs every kChains MFMAs.)
+        for (int i = 0; i < outer; ++i) {
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+#pragma unroll
+                for (int j = 0; j < kChains; ++j)
+                    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(acc[j]) : "v"(a), "v"(b));
+            }
+        }
+        asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");  // results settle before the VALU reads them
+    } else {
+        const float a = 0.001f * (float)(tid & 7), b = 0.002f * (float)((tid >> 3) & 7);
+        for (int i = 0; i < outer; ++i) {
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+#pragma unroll
+                for (int j = 0; j < kChains; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[j], 0, 0, 0);
+            }
+        }
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < kChains; ++j) s += acc[j][0] + acc[j][1] + acc[j][2] + acc[j][3];
+    sink[blockIdx.x * kProbeThreads + tid] = s;
+}
+
+// Streaming read of n16 16-byte vectors, grid-stride (the stream_f4 shape).
+__global__ __launch_bounds__(kProbeThreads) void probe_read_kernel(const float4 *x, size_t n16, float *sink) {
+    float s = 0.f;
+    for (size_t i = (size_t)blockIdx.x * kProbeThreads + threadIdx.x; i < n16; i += (size_t)gridDim.x * kProbeThreads) {
+        const float4 v = x[i];
+        s += v.x + v.y + v.z + v.w;
+    }
+    sink[blockIdx.x * kProbeThreads + threadIdx.x] = s;
+}
+
+// Streaming copy of n16 16-byte vectors, grid-stride.
+__global__ __launch_bounds__(kProbeThreads) void probe_copy_kernel(const float4 *x, float4 *y, size_t n16) {
+    for (size_t i = (size_t)blockIdx.x * kProbeThreads + threadIdx.x; i < n16; i += (size_t)gridDim.x * kProbeThreads)
+        y[i] = x[i];
+}
+
+}  // namespace
+
+int probe_sink_len() { return kProbeBlocks * kProbeThreads; }
+
+double probe_mfma_flops(int bf16, int iters) {
+    const double per_mfma = bf16 ? 2.0 * 16 * 16 * 32 : 2.0 * 16 * 16 * 4;
+    const double waves = (double)kProbeBlocks * (kProbeThreads / 64);
+    const int rounded = (iters + 3) / 4 * 4;  // the kernel runs whole unrolled rounds of 4
+    return waves * (double)rounded * kChains * per_mfma;
+}
+
+hipError_t launch_probe_mfma(int bf16, int iters, float *sink, hipStream_t stream) {
+    if (bf16) {
+        hipLaunchKernelGGL((probe_mfma_kernel<true>), dim3(kProbeBlocks), dim3(kProbeThreads), 0, stream, sink, iters);
+    } else {
+        hipLaunchKernelGGL((probe_mfma_kernel<false>), dim3(kProbeBlocks), dim3(kProbeThreads), 0, stream, sink, iters);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_probe_read(const void *x, size_t bytes, float *sink, hipStream_t stream) {
+    hipLaunchKernelGGL(probe_read_kernel, dim3(kProbeBlocks), dim3(kProbeThreads), 0, stream,
+                       static_cast<const float4 *>(x), bytes / 16, sink);
+    return hipGetLastError();
+}
+
+hipError_t launch_probe_copy(const void *x, void *y, size_t bytes, hipStream_t stream) {
+    hipLaunchKernelGGL(probe_copy_kernel, dim3(kProbeBlocks), dim3(kProbeThreads), 0, stream,
+                       static_cast<const float4 *>(x), static_cast<float4 *>(y), bytes / 16);
+    return hipGetLastError();
+}
+
+}  // namespace mxfa

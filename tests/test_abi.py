@@ -109,6 +109,40 @@ def test_python_layer_rejects_host_tensors():
         mx.shape_of(torch.zeros(16, 64, dtype=torch.float16), torch.zeros(16, 64, dtype=torch.float16), False)
 
 
+def test_probe_argument_checks(lib):
+    """The probes validate before launching (no device needed for these)."""
+    import ctypes
+    flops = ctypes.c_double(0.0)
+    fake = ctypes.c_void_p(4096)  # aligned, never dereferenced on the host
+    assert lib.mxfa_probe_sink_len() == 2048 * 256
+    assert lib.mxfa_probe_mfma(7, 16, fake, ctypes.byref(flops), None) == mx_status("MXFA_ERR_DTYPE")
+    assert lib.mxfa_probe_mfma(1, 0, fake, ctypes.byref(flops), None) == mx_status("MXFA_ERR_SHAPE")
+    assert lib.mxfa_probe_mfma(1, 16, None, ctypes.byref(flops), None) == mx_status("MXFA_ERR_NULL")
+    assert lib.mxfa_probe_mfma(1, 16, ctypes.c_void_p(4100), ctypes.byref(flops), None) == mx_status("MXFA_ERR_ALIGN")
+    assert lib.mxfa_probe_read(fake, 24, fake, None) == mx_status("MXFA_ERR_SHAPE")
+    assert lib.mxfa_probe_read(None, 32, fake, None) == mx_status("MXFA_ERR_NULL")
+    assert lib.mxfa_probe_copy(fake, fake, 0, None) == mx_status("MXFA_ERR_SHAPE")
+    assert lib.mxfa_probe_copy(fake, ctypes.c_void_p(4104), 32, None) == mx_status("MXFA_ERR_ALIGN")
+
+
+def mx_status(name: str) -> int:
+    return {v: k for k, v in mx.STATUS.items()}[name]
+
+
+def test_autograd_wrapper_rejects_host_tensors():
+    """The training-step wrapper has no CPU path either."""
+    import torch
+    from mx230_amd.autograd import CausalSelfAttention, flash_attention
+    q = torch.zeros(1, 2, 16, 64, requires_grad=True)
+    with pytest.raises(ValueError, match="device tensor"):
+        flash_attention(q, q, q, causal=True)
+    blk = CausalSelfAttention(128, n_heads=2, n_kv_heads=1)
+    with pytest.raises(ValueError, match="device tensor"):
+        blk(torch.zeros(1, 16, 128))
+    with pytest.raises(ValueError, match="multiple"):
+        CausalSelfAttention(128, n_heads=3, n_kv_heads=2)
+
+
 def test_product_never_touches_the_oracle():
     """The checker (oracle/) is test infrastructure: the package must not
     import, load or call it."""
