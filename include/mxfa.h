@@ -144,6 +144,38 @@ size_t mxfa_naive_scratch_bytes(const mxfa_shape *shape);
 int mxfa_run_naive_fwd(const mxfa_shape *shape, const void *q, const void *k, const void *v,
                        float *s, void *o, void *stream);
 
+/* ---- Inference-side forward (prefill): token-major rows over a KV cache.
+ * Replaces `attn_prefill` (03-llm-engine/kernels/llm.cu:3806-3815, body
+ * :3674-3804; launched by gpu.rs:3235-3289): query row i of this chunk sits at
+ * absolute position pos0 + i and attends to cache rows 0 .. pos0 + i (causal
+ * with a diagonal offset). Q row i holds head h at elements
+ * [h * head_dim, (h + 1) * head_dim) of a row q_stride elements long (the
+ * fused QKV row in the reference); the K and V caches hold position j in rows
+ * kv_stride elements long, KV head h / (n_head / n_kv_head) at
+ * [kvh * head_dim, ...); the output row i likewise with out_stride. Rows
+ * 0 .. pos0 + n_tok - 1 of both caches must be filled (the reference copies
+ * the chunk's own K/V in first, copy_kv_batch at llm.cu:3635). Generalisations: bf16 as well
+ * as fp32, head_dim 128 (bf16), any scale; the reference is fp32, head_dim 64,
+ * scale 1/8. No LSE is written. */
+typedef struct {
+    int n_tok;      /* query rows of this chunk */
+    int n_head;     /* query heads */
+    int n_kv_head;  /* KV heads; n_head % n_kv_head == 0 */
+    int head_dim;   /* 64 (fp32, bf16) or 128 (bf16) */
+    int pos0;       /* absolute position of query row 0 */
+    int q_stride;   /* elements between query rows (>= n_head * head_dim) */
+    int kv_stride;  /* elements between cache rows (>= n_kv_head * head_dim) */
+    int out_stride; /* elements between output rows (>= n_head * head_dim) */
+    int dtype;      /* mxfa_dtype */
+    float scale;    /* 0 -> 1/sqrt(head_dim) */
+} mxfa_prefill_shape;
+
+/* MXFA_OK if the prefill shape is supported; strides whose rows would not start
+ * on 16-byte boundaries give MXFA_ERR_ALIGN. */
+int mxfa_check_prefill(const mxfa_prefill_shape *shape);
+int mxfa_run_prefill(const mxfa_prefill_shape *shape, const void *q, const void *kcache, const void *vcache,
+                     void *out, void *stream);
+
 /* ---- Roofline probes: measured ceilings next to the published peaks.
  * Replace the reference's throughput audit, common/kernels/isa.cu:11-63
  * (fma_f32 / dp4a_s32 / fma_h2 chains and the stream_f4 read) driven by

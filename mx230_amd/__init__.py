@@ -44,8 +44,8 @@ EXPORTS = (
     "mxfa_version", "mxfa_strerror", "mxfa_init", "mxfa_shutdown", "mxfa_check_shape",
     "mxfa_run_flash", "mxfa_run_flash_lse", "mxfa_run_preprocess", "mxfa_run_bwd_dq",
     "mxfa_run_bwd_dkv", "mxfa_run_bwd_flash", "mxfa_bwd_workspace_bytes", "mxfa_run_bwd_naive",
-    "mxfa_naive_scratch_bytes", "mxfa_run_naive_fwd", "mxfa_probe_sink_len", "mxfa_probe_mfma",
-    "mxfa_probe_read", "mxfa_probe_copy",
+    "mxfa_naive_scratch_bytes", "mxfa_run_naive_fwd", "mxfa_check_prefill", "mxfa_run_prefill",
+    "mxfa_probe_sink_len", "mxfa_probe_mfma", "mxfa_probe_read", "mxfa_probe_copy",
 )
 
 
@@ -60,6 +60,13 @@ class MxfaError(RuntimeError):
 class MxfaShape(ctypes.Structure):
     _fields_ = [("B", ctypes.c_int), ("Hq", ctypes.c_int), ("Hkv", ctypes.c_int), ("N", ctypes.c_int),
                 ("d", ctypes.c_int), ("causal", ctypes.c_int), ("dtype", ctypes.c_int),
+                ("scale", ctypes.c_float)]
+
+
+class MxfaPrefillShape(ctypes.Structure):
+    _fields_ = [("n_tok", ctypes.c_int), ("n_head", ctypes.c_int), ("n_kv_head", ctypes.c_int),
+                ("head_dim", ctypes.c_int), ("pos0", ctypes.c_int), ("q_stride", ctypes.c_int),
+                ("kv_stride", ctypes.c_int), ("out_stride", ctypes.c_int), ("dtype", ctypes.c_int),
                 ("scale", ctypes.c_float)]
 
 
@@ -101,6 +108,9 @@ def load_library(path: str | None = None):
     lib.mxfa_naive_scratch_bytes.argtypes = [sp]
     lib.mxfa_naive_scratch_bytes.restype = ctypes.c_size_t
     lib.mxfa_run_naive_fwd.argtypes = [sp, vp, vp, vp, fp, vp, vp]
+    pp = ctypes.POINTER(MxfaPrefillShape)
+    lib.mxfa_check_prefill.argtypes = [pp]
+    lib.mxfa_run_prefill.argtypes = [pp, vp, vp, vp, vp, vp]
     lib.mxfa_probe_sink_len.argtypes = []
     lib.mxfa_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_int, fp, ctypes.POINTER(ctypes.c_double), vp]
     lib.mxfa_probe_read.argtypes = [vp, ctypes.c_size_t, fp, vp]
@@ -291,6 +301,51 @@ def naive_run(q, k, v, s, o, causal: bool, scale: float = 0.0, stream=None):
             _ptr(s, "s", torch.float32), _expect(o, "o", qs, dt))
     _check("mxfa_run_naive_fwd",
            load_library().mxfa_run_naive_fwd(ctypes.byref(sh.c()), *args, _stream(stream)))
+
+
+# ------------------------------------------------------------------ prefill --
+
+def _rows(t, name, dtype, min_rows, min_cols):
+    """A 2-D device tensor whose rows are contiguous (any row stride): returns
+    (pointer, row stride in elements)."""
+    torch = _torch()
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: must be a device tensor (got {t.device}); there is no CPU path")
+    if t.dtype != dtype:
+        raise ValueError(f"{name}: dtype {t.dtype}, expected {dtype}")
+    if t.dim() != 2 or (t.shape[1] > 1 and t.stride(1) != 1):
+        raise ValueError(f"{name}: expected a 2-D tensor with contiguous rows, got shape {tuple(t.shape)} "
+                         f"strides {t.stride()}")
+    if t.shape[0] < min_rows or t.shape[1] < min_cols:
+        raise ValueError(f"{name}: needs at least {min_rows} rows x {min_cols} columns, got {tuple(t.shape)}")
+    return ctypes.c_void_p(t.data_ptr()), (t.stride(0) if t.shape[0] > 1 else max(t.shape[1], min_cols))
+
+
+def run_prefill(q, kcache, vcache, out, pos0: int, n_head: int, n_kv_head: int, head_dim: int = 64,
+                scale: float = 0.0, stream=None):
+    """mxfa_run_prefill, the flash forward over a KV cache with token-major rows
+    (attn_prefill, 03-llm-engine/kernels/llm.cu:3806-3815): query row i sits at
+    position pos0 + i and attends to cache rows 0..pos0 + i.
+
+    q: [n_tok, >= n_head*head_dim] (head h at columns h*head_dim..; may be a
+    view into a fused QKV buffer); kcache, vcache: [>= pos0 + n_tok,
+    >= n_kv_head*head_dim], same row stride, rows 0..pos0 + n_tok - 1 filled;
+    out: [n_tok, >= n_head*head_dim]. All bf16, or fp32 with head_dim 64."""
+    torch = _torch()
+    if q.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"q: dtype {q.dtype}; bf16 or float32 expected")
+    n_tok = q.shape[0] if q.dim() == 2 else -1
+    qp, qs = _rows(q, "q", q.dtype, 1, n_head * head_dim)
+    kp, ks = _rows(kcache, "kcache", q.dtype, pos0 + n_tok, n_kv_head * head_dim)
+    vp, vs = _rows(vcache, "vcache", q.dtype, pos0 + n_tok, n_kv_head * head_dim)
+    if ks != vs:
+        raise ValueError(f"kcache and vcache must share a row stride ({ks} != {vs})")
+    op, os_ = _rows(out, "out", q.dtype, n_tok, n_head * head_dim)
+    sh = MxfaPrefillShape(n_tok, n_head, n_kv_head, head_dim, pos0, qs, ks, os_,
+                          MXFA_BF16 if q.dtype == torch.bfloat16 else MXFA_F32, scale)
+    _check("mxfa_run_prefill", load_library().mxfa_run_prefill(ctypes.byref(sh), qp, kp, vp, op, _stream(stream)))
 
 
 # ------------------------------------------------------------ conveniences --

@@ -37,6 +37,13 @@ struct Params {
     void *dq, *dk, *dv;
     int B, Hq, Hkv, N, group;
     float scale, scale_log2;
+    // Forward layout, in elements: batch, head and row strides of Q and O and
+    // of K/V, the number of key rows, and the causal offset (query row i sits
+    // at position pos0 + i and sees keys 0..pos0 + i). The packed training
+    // layout [B][H][N][d] has Nk = N and pos0 = 0; the backward and naive
+    // kernels assume it.
+    long long q_bs, q_hs, kv_bs, kv_hs, o_bs, o_hs;
+    int q_rs, kv_rs, o_rs, Nk, pos0;
 };
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
@@ -324,7 +331,7 @@ __device__ __forceinline__ void lds_dma4(uint32_t base, const void *src) {
 // workgroup.
 template <class Pol, int NT = 256>
 __device__ __forceinline__ void stage_rows(typename Pol::T *tile, const typename Pol::T *src, int nvalid,
-                                           int tid, int wave) {
+                                           int tid, int wave, int row_stride = Pol::D) {
     constexpr int CPR = Pol::D / Pol::EPC;
     constexpr int NCH = Pol::ROWS * CPR;
     static_assert(NCH % NT == 0, "whole wave-wide loads");
@@ -335,16 +342,18 @@ __device__ __forceinline__ void stage_rows(typename Pol::T *tile, const typename
         int row, c;
         Pol::chunk_at(P, row, c);
         const int grow = min(row, nvalid - 1);
-        lds_dma16(base + k * NT * 16, src + (size_t)grow * Pol::D + c * Pol::EPC);
+        lds_dma16(base + k * NT * 16, src + (size_t)grow * row_stride + c * Pol::EPC);
     }
 }
 
-// One K/V stage: Pol::ROWS key rows from k0 of K and V into LDS buffers.
+// One K/V stage: Pol::ROWS key rows from k0 of K and V (rows row_stride
+// elements apart) into LDS buffers.
 template <class Pol, int NT = 256>
 __device__ __forceinline__ void stage_kv(typename Pol::T *sk, typename Pol::T *sv, const typename Pol::T *K,
-                                         const typename Pol::T *V, int k0, int N, int tid, int wave) {
-    stage_rows<Pol, NT>(sk, K + (size_t)k0 * Pol::D, N - k0, tid, wave);
-    stage_rows<Pol, NT>(sv, V + (size_t)k0 * Pol::D, N - k0, tid, wave);
+                                         const typename Pol::T *V, int k0, int N, int tid, int wave,
+                                         int row_stride = Pol::D) {
+    stage_rows<Pol, NT>(sk, K + (size_t)k0 * row_stride, N - k0, tid, wave, row_stride);
+    stage_rows<Pol, NT>(sv, V + (size_t)k0 * row_stride, N - k0, tid, wave, row_stride);
 }
 
 // Read by lanes past the end of a staged vector (see stage_vec64).

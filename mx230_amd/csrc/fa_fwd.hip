@@ -21,11 +21,12 @@
 namespace mxfa {
 
 // One 64-key stage for one wave: scores, online-softmax update, O^T += V^T P^T.
+// qpos0: position of the wave's first query row; Nk: key rows.
 template <class Pol, bool CAUSAL, bool MASK>
 __device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][2], float (&m)[2], float (&lsum)[2],
                                           const typename Pol::Frag (&qf)[2][Pol::NC],
-                                          const typename Pol::T *sk, const typename Pol::T *sv, int k0, int q0,
-                                          int N, float scale_log2, int g, int l16) {
+                                          const typename Pol::T *sk, const typename Pol::T *sv, int k0, int qpos0,
+                                          int Nk, float scale_log2, int g, int l16) {
     using Frag = typename Pol::Frag;
     constexpr int NC = Pol::NC, XT = Pol::D / 16;
     f32x4 s[2][2][2];  // [block][t][qt]
@@ -46,7 +47,7 @@ __device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][2], float (&
     }
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
-        const int qi = q0 + 16 * qt + l16;
+        const int qpos = qpos0 + 16 * qt + l16;
         float mx = -INFINITY;
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
@@ -57,7 +58,7 @@ __device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][2], float (&
                     float v = s[blk][t][qt][r] * scale_log2;
                     if constexpr (MASK) {
                         const int key = k0 + 32 * blk + Pol::bidx(t, g, r);
-                        v = (key >= N || (CAUSAL && key > qi)) ? -INFINITY : v;
+                        v = (key >= Nk || (CAUSAL && key > qpos)) ? -INFINITY : v;
                     }
                     s[blk][t][qt][r] = v;
                     mx = fmaxf(mx, v);
@@ -111,53 +112,55 @@ __global__ __launch_bounds__(256, Pol::kWaves) void fwd_kernel(Params p) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, l16 = lane & 15;
-    const int N = p.N;
+    const int N = p.N, Nk = p.Nk, pos0 = p.pos0;
     const int bh = blockIdx.x;
     const int nqb = (N + BQ - 1) / BQ;
     const int qb = CAUSAL ? (nqb - 1 - (int)blockIdx.y) : (int)blockIdx.y;  // heaviest first
     const int b = bh / p.Hq, h = bh % p.Hq, kvh = h / p.group;
-    const T *Q = static_cast<const T *>(p.q) + (size_t)bh * N * D;
-    const size_t kvoff = ((size_t)b * p.Hkv + kvh) * N * D;
+    const T *Q = static_cast<const T *>(p.q) + b * p.q_bs + h * p.q_hs;
+    const size_t kvoff = b * p.kv_bs + kvh * p.kv_hs;
     const T *K = static_cast<const T *>(p.k) + kvoff;
     const T *V = static_cast<const T *>(p.v) + kvoff;
     const int q0 = qb * BQ + wave * 32;
+    const int qpos0 = pos0 + q0;  // position of the wave's first query row
 
     Frag qf[2][NC];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
         const int qi = q0 + 16 * qt + l16;
-        Pol::gmem_row_frags(qf[qt], Q + (size_t)qi * D, g, qi < N);
+        Pol::gmem_row_frags(qf[qt], Q + (size_t)qi * p.q_rs, g, qi < N);
     }
     f32x4 acc[XT][2];
 #pragma unroll
     for (int xt = 0; xt < XT; ++xt) acc[xt][0] = acc[xt][1] = zero4();
     float m[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.f, 0.f};
 
-    const int kend = CAUSAL ? min(N, qb * BQ + BQ) : N;
+    const int kend = CAUSAL ? min(Nk, pos0 + qb * BQ + BQ) : Nk;
     const int nsteps = (kend + BK - 1) / BK;
 
-    stage_kv<Pol>(sK[0], sV[0], K, V, 0, N, tid, wave);
+    stage_kv<Pol>(sK[0], sV[0], K, V, 0, Nk, tid, wave, p.kv_rs);
     wait_stage();
     __syncthreads();
 
     for (int st = 0; st < nsteps; ++st) {
         const int cur = st & 1;
-        if (st + 1 < nsteps) stage_kv<Pol>(sK[cur ^ 1], sV[cur ^ 1], K, V, (st + 1) * BK, N, tid, wave);
+        if (st + 1 < nsteps) stage_kv<Pol>(sK[cur ^ 1], sV[cur ^ 1], K, V, (st + 1) * BK, Nk, tid, wave, p.kv_rs);
         const int k0 = st * BK;
         // a wave whose queries all precede the stage's keys has nothing to do
-        if (!CAUSAL || k0 <= q0 + 31) {
-            const bool need_mask = (k0 + BK > N) || (CAUSAL && k0 + BK - 1 > q0);
+        if (!CAUSAL || k0 <= qpos0 + 31) {
+            const bool need_mask = (k0 + BK > Nk) || (CAUSAL && k0 + BK - 1 > qpos0);
             if (need_mask) {
-                fwd_stage<Pol, CAUSAL, true>(acc, m, lsum, qf, sK[cur], sV[cur], k0, q0, N, p.scale_log2, g, l16);
+                fwd_stage<Pol, CAUSAL, true>(acc, m, lsum, qf, sK[cur], sV[cur], k0, qpos0, Nk, p.scale_log2, g, l16);
             } else {
-                fwd_stage<Pol, CAUSAL, false>(acc, m, lsum, qf, sK[cur], sV[cur], k0, q0, N, p.scale_log2, g, l16);
+                fwd_stage<Pol, CAUSAL, false>(acc, m, lsum, qf, sK[cur], sV[cur], k0, qpos0, Nk, p.scale_log2, g,
+                                              l16);
             }
         }
         wait_stage();
         __syncthreads();
     }
 
-    T *O = static_cast<T *>(p.o) + (size_t)bh * N * D;
+    T *O = static_cast<T *>(p.o) + b * p.o_bs + h * p.o_hs;
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
         const int qi = q0 + 16 * qt + l16;
@@ -165,7 +168,7 @@ __global__ __launch_bounds__(256, Pol::kWaves) void fwd_kernel(Params p) {
         const float inv = 1.0f / ltot;
         if (qi < N) {
 #pragma unroll
-            for (int xt = 0; xt < XT; ++xt) store4<T>(O + (size_t)qi * D + 16 * xt + 4 * g, acc[xt][qt], inv);
+            for (int xt = 0; xt < XT; ++xt) store4<T>(O + (size_t)qi * p.o_rs + 16 * xt + 4 * g, acc[xt][qt], inv);
             if (p.lse != nullptr && g == 0) p.lse[(size_t)bh * N + qi] = (m[qt] + fast_log2(ltot)) * kLn2;
         }
     }

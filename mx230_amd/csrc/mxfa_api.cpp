@@ -45,6 +45,14 @@ Params make_params(const mxfa_shape *s) {
     p.group = s->Hq / s->Hkv;
     p.scale = s->scale > 0.0f ? s->scale : 1.0f / std::sqrt((float)s->d);
     p.scale_log2 = p.scale * mxfa::kLog2e;
+    // packed [B][H][N][d] layout, keys = queries, no causal offset
+    const long long nd = (long long)s->N * s->d;
+    p.q_rs = p.kv_rs = p.o_rs = s->d;
+    p.q_hs = p.o_hs = p.kv_hs = nd;
+    p.q_bs = p.o_bs = nd * s->Hq;
+    p.kv_bs = nd * s->Hkv;
+    p.Nk = s->N;
+    p.pos0 = 0;
     return p;
 }
 
@@ -223,6 +231,51 @@ int mxfa_run_naive_fwd(const mxfa_shape *shape, const void *q, const void *k, co
     p.v = v;
     p.o = o;
     return from_hip(mxfa::launch_naive_fwd(p, s, shape->d, shape->causal, static_cast<hipStream_t>(stream)));
+}
+
+int mxfa_check_prefill(const mxfa_prefill_shape *s) {
+    if (s == nullptr) return MXFA_ERR_NULL;
+    if (s->dtype != MXFA_F32 && s->dtype != MXFA_BF16) return MXFA_ERR_DTYPE;
+    if (s->n_tok < 1 || s->n_head < 1 || s->n_kv_head < 1 || s->head_dim < 1 || s->pos0 < 0) return MXFA_ERR_SHAPE;
+    if (s->n_head % s->n_kv_head != 0) return MXFA_ERR_SHAPE;
+    if (!(s->scale >= 0.0f) || std::isinf(s->scale)) return MXFA_ERR_SHAPE;
+    if ((long long)s->pos0 + s->n_tok > 0x7fffffffLL - 128) return MXFA_ERR_SHAPE;
+    if (((long long)s->n_tok + 127) / 128 > kMaxGridY) return MXFA_ERR_SHAPE;
+    if (s->head_dim != 64 && s->head_dim != 128) return MXFA_ERR_UNSUPPORTED;
+    if (s->dtype == MXFA_F32 && s->head_dim != 64) return MXFA_ERR_UNSUPPORTED;
+    // every head of a row must fit inside the row
+    const long long qw = (long long)s->n_head * s->head_dim, kw = (long long)s->n_kv_head * s->head_dim;
+    if (s->q_stride < qw || s->out_stride < qw || s->kv_stride < kw) return MXFA_ERR_SHAPE;
+    // rows start on 16-byte boundaries (the kernels load and stage 16-byte chunks)
+    const int esz = s->dtype == MXFA_BF16 ? 2 : 4;
+    if (((long long)s->q_stride * esz) % 16 || ((long long)s->kv_stride * esz) % 16 ||
+        ((long long)s->out_stride * esz) % 16)
+        return MXFA_ERR_ALIGN;
+    return MXFA_OK;
+}
+
+int mxfa_run_prefill(const mxfa_prefill_shape *s, const void *q, const void *kcache, const void *vcache, void *out,
+                     void *stream) {
+    int rc = mxfa_check_prefill(s);
+    if (rc != MXFA_OK) return rc;
+    rc = check_ptrs({q, kcache, vcache, out});
+    if (rc != MXFA_OK) return rc;
+    mxfa_shape sh{1, s->n_head, s->n_kv_head, s->n_tok, s->head_dim, 1, s->dtype, s->scale};
+    Params p = make_params(&sh);
+    p.q = q;
+    p.k = kcache;
+    p.v = vcache;
+    p.o = out;
+    p.lse = nullptr;
+    // token-major rows: head h at column h * head_dim of every row
+    p.q_rs = s->q_stride;
+    p.kv_rs = s->kv_stride;
+    p.o_rs = s->out_stride;
+    p.q_hs = p.o_hs = p.kv_hs = s->head_dim;
+    p.q_bs = p.o_bs = p.kv_bs = 0;
+    p.Nk = s->pos0 + s->n_tok;
+    p.pos0 = s->pos0;
+    return from_hip(mxfa::launch_fwd(p, s->dtype == MXFA_BF16, s->head_dim, 1, static_cast<hipStream_t>(stream)));
 }
 
 int mxfa_probe_sink_len(void) { return mxfa::probe_sink_len(); }

@@ -109,6 +109,43 @@ def test_python_layer_rejects_host_tensors():
         mx.shape_of(torch.zeros(16, 64, dtype=torch.float16), torch.zeros(16, 64, dtype=torch.float16), False)
 
 
+def _prefill(**kw):
+    base = dict(n_tok=100, n_head=14, n_kv_head=2, head_dim=64, pos0=37, q_stride=18 * 64, kv_stride=2 * 64,
+                out_stride=14 * 64, dtype=mx.MXFA_BF16, scale=0.0)
+    base.update(kw)
+    return mx.MxfaPrefillShape(**base)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(), 0),
+    (dict(dtype=mx.MXFA_F32), 0),
+    (dict(dtype=3), -3),
+    (dict(n_tok=0), -2),
+    (dict(pos0=-1), -2),
+    (dict(n_head=13), -2),
+    (dict(q_stride=14 * 64 - 8), -2),
+    (dict(kv_stride=64), -2),
+    (dict(out_stride=100), -2),
+    (dict(q_stride=18 * 64 + 4), -5),      # bf16 row of 2312 bytes: not a multiple of 16
+    (dict(q_stride=18 * 64 + 8), 0),       # 2320 bytes: fine
+    (dict(out_stride=14 * 64 + 2, dtype=mx.MXFA_F32), -5),
+    (dict(head_dim=96), -4),
+    (dict(head_dim=128, dtype=mx.MXFA_F32, q_stride=18 * 128, kv_stride=256, out_stride=14 * 128), -4),
+    (dict(head_dim=128, q_stride=18 * 128, kv_stride=256, out_stride=14 * 128), 0),
+    (dict(scale=float("nan")), -2),
+])
+def test_check_prefill(lib, kw, code):
+    assert lib.mxfa_check_prefill(ctypes.byref(_prefill(**kw))) == code
+
+
+def test_prefill_null_and_alignment(lib):
+    sh = _prefill()
+    ok, bad = ctypes.c_void_p(4096), ctypes.c_void_p(4096 + 4)
+    assert lib.mxfa_check_prefill(None) == -1
+    assert lib.mxfa_run_prefill(ctypes.byref(sh), ok, None, ok, ok, None) == -1
+    assert lib.mxfa_run_prefill(ctypes.byref(sh), ok, ok, bad, ok, None) == -5
+
+
 def test_probe_argument_checks(lib):
     """The probes validate before launching (no device needed for these)."""
     import ctypes
