@@ -90,15 +90,16 @@ __device__ __forceinline__ void stage_qdo(typename Pol::T *sq, typename Pol::T *
 
 // ------------------------------------------------------------------ dQ pass
 
-// One 64-key stage of the dQ pass for one wave (32 queries). dof holds -dO and
-// the dP accumulators start at Delta, so they come out as Delta - dP and the
-// MFMAs accumulate -dQ / scale (the epilogue multiplies by -scale).
+// One 64-key stage of the dQ pass for one wave (32 queries). qf holds Q
+// scale log2(e) and the score accumulators start at -L log2(e), so they come
+// out as the exponents of P; dof holds -dO and the dP accumulators start at
+// Delta, so they come out as Delta - dP and the MFMAs accumulate -dQ / scale
+// (the epilogue multiplies by -scale).
 template <class Pol, bool CAUSAL, bool MASK>
 __device__ __forceinline__ void dq_stage(f32x4 (&acc)[Pol::D / 16][2], const typename Pol::Frag (&qf)[2][Pol::NC],
-                                         const typename Pol::Frag (&dof)[2][Pol::NC], const float (&L2)[2],
+                                         const typename Pol::Frag (&dof)[2][Pol::NC], const float (&nL2)[2],
                                          const float (&Dl)[2], const typename Pol::T *sk,
-                                         const typename Pol::T *sv, int k0, int q0, int N, float scale_log2,
-                                         int g, int l16) {
+                                         const typename Pol::T *sv, int k0, int q0, int N, int g, int l16) {
     using Frag = typename Pol::Frag;
     constexpr int NC = Pol::NC, XT = Pol::D / 16;
 #pragma unroll
@@ -111,7 +112,7 @@ __device__ __forceinline__ void dq_stage(f32x4 (&acc)[Pol::D / 16][2], const typ
             Pol::lds_row_frags(a, sk, n, g);
 #pragma unroll
             for (int qt = 0; qt < 2; ++qt) {
-                f32x4 c = zero4();
+                f32x4 c = f32x4{nL2[qt], nL2[qt], nL2[qt], nL2[qt]};
 #pragma unroll
                 for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], qf[qt][kc], c);
                 s[t][qt] = c;
@@ -132,7 +133,7 @@ __device__ __forceinline__ void dq_stage(f32x4 (&acc)[Pol::D / 16][2], const typ
             for (int t = 0; t < 2; ++t) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    float x = s[t][qt][r] * scale_log2 - L2[qt];
+                    float x = s[t][qt][r];
                     if constexpr (MASK) {
                         const int key = k0 + 32 * blk + Pol::bidx(t, g, r);
                         x = (key >= N || (CAUSAL && key > qi)) ? -INFINITY : x;
@@ -179,7 +180,7 @@ __global__ __launch_bounds__(64 * NW, Pol::kWaves * 4 / NW) void dq_kernel(Param
     const int q0 = qb * BQ + wave * 32;
 
     Frag qf[2][NC], dof[2][NC];
-    float L2[2], Dl[2];
+    float nL2[2], Dl[2];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
         const int qi = q0 + 16 * qt + l16;
@@ -187,8 +188,11 @@ __global__ __launch_bounds__(64 * NW, Pol::kWaves * 4 / NW) void dq_kernel(Param
         Pol::gmem_row_frags(qf[qt], Q + (size_t)qi * D, g, ok);
         Pol::gmem_row_frags(dof[qt], dO + (size_t)qi * D, g, ok);
 #pragma unroll
-        for (int kc = 0; kc < NC; ++kc) dof[qt][kc] = Pol::neg(dof[qt][kc]);
-        L2[qt] = ok ? p.lse[(size_t)bh * N + qi] * kLog2e : 0.f;
+        for (int kc = 0; kc < NC; ++kc) {
+            qf[qt][kc] = Pol::scaled(qf[qt][kc], p.scale_log2);
+            dof[qt][kc] = Pol::neg(dof[qt][kc]);
+        }
+        nL2[qt] = ok ? p.lse[(size_t)bh * N + qi] * -kLog2e : 0.f;
         Dl[qt] = ok ? p.delta[(size_t)bh * N + qi] : 0.f;
     }
     f32x4 acc[XT][2];
@@ -209,9 +213,9 @@ __global__ __launch_bounds__(64 * NW, Pol::kWaves * 4 / NW) void dq_kernel(Param
         if (!CAUSAL || k0 <= q0 + 31) {
             const bool need_mask = (k0 + BK > N) || (CAUSAL && k0 + BK - 1 > q0);
             if (need_mask) {
-                dq_stage<Pol, CAUSAL, true>(acc, qf, dof, L2, Dl, sK[cur], sV[cur], k0, q0, N, p.scale_log2, g, l16);
+                dq_stage<Pol, CAUSAL, true>(acc, qf, dof, nL2, Dl, sK[cur], sV[cur], k0, q0, N, g, l16);
             } else {
-                dq_stage<Pol, CAUSAL, false>(acc, qf, dof, L2, Dl, sK[cur], sV[cur], k0, q0, N, p.scale_log2, g, l16);
+                dq_stage<Pol, CAUSAL, false>(acc, qf, dof, nL2, Dl, sK[cur], sV[cur], k0, q0, N, g, l16);
             }
         }
         wait_stage();
@@ -272,21 +276,24 @@ __device__ __forceinline__ void chain_block(f32x4 (&accK)[4][2], f32x4 (&accV)[4
 // and Delta of rows bidx(t, g, 0..3).
 struct ScoreOps {
     bf16x8 q[2][2], d[2][2];  // [t][kc]
-    f32x4 dl[2];
+    f32x4 dl[2], nl[2];       // Delta and -LSE log2(e) of the rows
 };
 template <class Pol>
-__device__ __forceinline__ void score_operands(ScoreOps &o, const u16 *sq, const u16 *sdo, const float *sd, int blk,
-                                               int g, int l16) {
+__device__ __forceinline__ void score_operands(ScoreOps &o, const u16 *sq, const u16 *sdo, const float *sl,
+                                               const float *sd, int blk, int g, int l16) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
         const int n = blk + Pol::arow(t, l16);
         Pol::lds_row_frags(o.q[t], sq, n, g);
         Pol::lds_row_frags(o.d[t], sdo, n, g);
         o.dl[t] = *reinterpret_cast<const f32x4 *>(sd + blk + Pol::bidx(t, g, 0));
+        o.nl[t] = *reinterpret_cast<const f32x4 *>(sl + blk + Pol::bidx(t, g, 0)) * -kLog2e;
     }
 }
 
-// Scores S = K Q^T and Delta - dP = Delta + (-V) dO^T of one block.
+// Exponents S scale log2(e) - L log2(e) = (K scale log2(e)) Q^T + C, C = -L
+// log2(e) (kf holds the scaled K), and Delta - dP = Delta + (-V) dO^T of one
+// block.
 template <class Pol>
 __device__ __forceinline__ void score_block(f32x4 (&s)[2][2], f32x4 (&dp)[2][2], const bf16x8 (&kf)[2][2],
                                             const bf16x8 (&vf)[2][2], const ScoreOps &o) {
@@ -294,7 +301,7 @@ __device__ __forceinline__ void score_block(f32x4 (&s)[2][2], f32x4 (&dp)[2][2],
     for (int t = 0; t < 2; ++t) {
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
-            f32x4 c = zero4();
+            f32x4 c = o.nl[t];
 #pragma unroll
             for (int kc = 0; kc < 2; ++kc) c = Pol::mma(o.q[t][kc], kf[kt][kc], c);
             s[t][kt] = c;
@@ -306,23 +313,22 @@ __device__ __forceinline__ void score_block(f32x4 (&s)[2][2], f32x4 (&dp)[2][2],
     }
 }
 
-// P = exp2(S scale log2(e) - L log2(e)) and -dS / scale = P (Delta - dP),
-// packed as the chain operands. MASK (causal): query row bidx of the block
-// precedes key 16 kt + l16 of the wave iff bidx - l16 < moff + 16 kt, where
-// moff = first key of the wave - first query of the block (0 on the diagonal,
-// >= 32 for a block wholly before the keys, whose P is then all zero).
+// P = exp2(S scale log2(e) - L log2(e)) (s holds the exponents) and
+// -dS / scale = P (Delta - dP), packed as the chain operands. MASK (causal):
+// query row bidx of the block precedes key 16 kt + l16 of the wave iff
+// bidx - l16 < moff + 16 kt, where moff = first key of the wave - first query
+// of the block (0 on the diagonal, >= 32 for a block wholly before the keys,
+// whose P is then all zero).
 template <class Pol, bool MASK>
 __device__ __forceinline__ void softmax_block(f32x4 (&s)[2][2], f32x4 (&dp)[2][2], bf16x8 (&cp)[2],
-                                              bf16x8 (&cds)[2], const float *sl, int blk, int moff,
-                                              float scale_log2, int g, int l16) {
+                                              bf16x8 (&cds)[2], int moff, int g, int l16) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-        const f32x4 L2 = *reinterpret_cast<const f32x4 *>(sl + blk + Pol::bidx(t, g, 0)) * kLog2e;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt) {
-                float x = s[t][kt][r] * scale_log2 - L2[r];
+                float x = s[t][kt][r];
                 if constexpr (MASK) x = Pol::bidx(t, g, r) - l16 < moff + 16 * kt ? -INFINITY : x;
                 const float pv = fast_exp2(x);
                 s[t][kt][r] = pv;
@@ -339,33 +345,34 @@ __device__ __forceinline__ void softmax_block(f32x4 (&s)[2][2], f32x4 (&dp)[2][2
 
 }  // namespace pp
 
-// One 64-query stage of the dK/dV pass for one wave (16*KT keys). vf holds -V
-// and the dP accumulators start at Delta, so they come out as Delta - dP and
-// accK accumulates -dK / scale (the epilogue multiplies by -scale).
+// One 64-query stage of the dK/dV pass for one wave (16*KT keys). kf holds
+// K scale log2(e) and the score accumulators start at -L log2(e), so they come
+// out as the exponents of P; vf holds -V and the dP accumulators start at
+// Delta, so they come out as Delta - dP and accK accumulates -dK / scale (the
+// epilogue multiplies by -scale).
 template <class Pol, int KT, bool CAUSAL, bool MASK>
 __device__ __forceinline__ void dkv_stage(f32x4 (&accK)[Pol::D / 16][KT], f32x4 (&accV)[Pol::D / 16][KT],
                                           const typename Pol::Frag (&kf)[KT][Pol::NC],
                                           const typename Pol::Frag (&vf)[KT][Pol::NC], const typename Pol::T *sq,
                                           const typename Pol::T *sdo, const float *sl, const float *sd, int qs,
-                                          int kw0, int N, float scale_log2, int g, int l16) {
+                                          int kw0, int N, int g, int l16) {
     using Frag = typename Pol::Frag;
     constexpr int NC = Pol::NC, XT = Pol::D / 16;
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
         f32x4 s[2][KT], dp[2][KT];  // [t][kt]
-        f32x4 L2[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             // block rows bidx(t, g, 0..3) are consecutive: one 16-byte LDS read
             const int q4 = 32 * blk + Pol::bidx(t, g, 0);
-            L2[t] = *reinterpret_cast<const f32x4 *>(sl + q4) * kLog2e;
+            const f32x4 nl = *reinterpret_cast<const f32x4 *>(sl + q4) * -kLog2e;
             const f32x4 dl = *reinterpret_cast<const f32x4 *>(sd + q4);
             Frag a[NC];
             const int n = 32 * blk + Pol::arow(t, l16);
             Pol::lds_row_frags(a, sq, n, g);
 #pragma unroll
             for (int kt = 0; kt < KT; ++kt) {
-                f32x4 c = zero4();
+                f32x4 c = nl;
 #pragma unroll
                 for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], kf[kt][kc], c);
                 s[t][kt] = c;
@@ -385,7 +392,7 @@ __device__ __forceinline__ void dkv_stage(f32x4 (&accK)[Pol::D / 16][KT], f32x4 
             for (int r = 0; r < 4; ++r) {
 #pragma unroll
                 for (int kt = 0; kt < KT; ++kt) {
-                    float x = s[t][kt][r] * scale_log2 - L2[t][r];
+                    float x = s[t][kt][r];
                     if constexpr (MASK) {
                         // causal: query qs + 32 blk + bidx(t, g, r) before key kw0 + 16 kt + l16
                         const bool before = Pol::bidx(t, g, r) - l16 < kw0 - qs + 16 * kt - 32 * blk;
@@ -450,7 +457,10 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDkv * 4 / NW) void dkv_kernel(P
         Pol::gmem_row_frags(kf[kt], K + (size_t)key * D, g, key < N);
         Pol::gmem_row_frags(vf[kt], V + (size_t)key * D, g, key < N);
 #pragma unroll
-        for (int kc = 0; kc < NC; ++kc) vf[kt][kc] = Pol::neg(vf[kt][kc]);
+        for (int kc = 0; kc < NC; ++kc) {
+            kf[kt][kc] = Pol::scaled(kf[kt][kc], p.scale_log2);
+            vf[kt][kc] = Pol::neg(vf[kt][kc]);
+        }
     }
     f32x4 accK[XT][KT], accV[XT][KT];
 #pragma unroll
@@ -497,8 +507,8 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDkv * 4 / NW) void dkv_kernel(P
         const int qs = qstart + (st % nqs) * BQ;
         // a wave whose keys all follow the stage's queries has nothing to do
         if (!CAUSAL || qs + BQ - 1 >= kw0) {
-            dkv_stage<Pol, KT, CAUSAL, MASK>(accK, accV, kf, vf, sQ[cur], sdO[cur], sL[cur], sD[cur], qs, kw0, N,
-                                             p.scale_log2, g, l16);
+            dkv_stage<Pol, KT, CAUSAL, MASK>(accK, accV, kf, vf, sQ[cur], sdO[cur], sL[cur], sD[cur], qs, kw0, N, g,
+                                             l16);
         }
         if (NBUF > 2 && ahead) {
             wait_vmcnt<kLoads>();
@@ -585,7 +595,10 @@ __global__ __launch_bounds__(512) void dkv_pp_kernel(Params p) {
         Pol::gmem_row_frags(kf[kt], K + (size_t)key * D, g, key < N);
         Pol::gmem_row_frags(vf[kt], V + (size_t)key * D, g, key < N);
 #pragma unroll
-        for (int kc = 0; kc < 2; ++kc) vf[kt][kc] = Pol::neg(vf[kt][kc]);
+        for (int kc = 0; kc < 2; ++kc) {
+            kf[kt][kc] = Pol::scaled(kf[kt][kc], p.scale_log2);
+            vf[kt][kc] = Pol::neg(vf[kt][kc]);
+        }
     }
     f32x4 accK[XT][KT], accV[XT][KT];
 #pragma unroll
@@ -651,19 +664,19 @@ __global__ __launch_bounds__(512) void dkv_pp_kernel(Params p) {
         const int moff = kw0 - (qstart + i * BQ + blk);
         pp::chain_operands<Pol>(cdo, cq, tq(bf), tdo(bf), blk, g, l16);
         if (CAUSAL && moff >= 0) {
-            pp::softmax_block<Pol, true>(s, dp, cp, cds, vl(bf), blk, moff, p.scale_log2, g, l16);
+            pp::softmax_block<Pol, true>(s, dp, cp, cds, moff, g, l16);
         } else {
-            pp::softmax_block<Pol, false>(s, dp, cp, cds, vl(bf), blk, 0, p.scale_log2, g, l16);
+            pp::softmax_block<Pol, false>(s, dp, cp, cds, 0, g, l16);
         }
     };
     auto m_phase = [&](int st) __attribute__((always_inline)) {
         const int cb = st % NBUF;
-        pp::score_operands<Pol>(so, tq(cb), tdo(cb), vd(cb), blk, g, l16);
+        pp::score_operands<Pol>(so, tq(cb), tdo(cb), vl(cb), vd(cb), blk, g, l16);
         pp::chain_block<Pol>(accK, accV, cp, cds, cdo, cq);
         pp::score_block<Pol>(s, dp, kf, vf, so);
     };
     auto first_scores = [&]() __attribute__((always_inline)) {
-        pp::score_operands<Pol>(so, tq(0), tdo(0), vd(0), blk, g, l16);
+        pp::score_operands<Pol>(so, tq(0), tdo(0), vl(0), vd(0), blk, g, l16);
         pp::score_block<Pol>(s, dp, kf, vf, so);
     };
 

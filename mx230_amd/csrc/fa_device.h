@@ -160,6 +160,15 @@ struct PolBF16 {
             }
         }
     }
+    // every element times s, rounded to bf16 (nearest even), pinned in
+    // registers like neg()
+    __device__ static __forceinline__ Frag scaled(Frag f, float s) {
+        Frag r;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r[e] = (__bf16)((float)f[e] * s);
+        pin_regs(r);
+        return r;
+    }
     // flips the sign of every element (bf16 sign bits, two per dword). The
     // result is pinned (pin_regs) so the compiler keeps the negated fragment
     // live instead of recomputing it from the original inside the stage loop.
@@ -257,6 +266,7 @@ struct PolF32 {
         }
     }
     __device__ static __forceinline__ Frag neg(Frag f) { return -f; }
+    __device__ static __forceinline__ Frag scaled(Frag f, float s) { return f * s; }
     // The chain operand of one 32-row block: the two C tiles themselves.
     struct ChainB {
         f32x4 c0, c1;

@@ -20,13 +20,14 @@
 
 namespace mxfa {
 
-// One 64-key stage for one wave: scores, online-softmax update, O^T += V^T P^T.
+// One 64-key stage for one wave: scores (in log2 units: qf holds Q scale
+// log2(e)), online-softmax update, O^T += V^T P^T.
 // qpos0: position of the wave's first query row; Nk: key rows.
 template <class Pol, bool CAUSAL, bool MASK>
 __device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][2], float (&m)[2], float (&lsum)[2],
                                           const typename Pol::Frag (&qf)[2][Pol::NC],
                                           const typename Pol::T *sk, const typename Pol::T *sv, int k0, int qpos0,
-                                          int Nk, float scale_log2, int g, int l16) {
+                                          int Nk, int g, int l16) {
     using Frag = typename Pol::Frag;
     constexpr int NC = Pol::NC, XT = Pol::D / 16;
     f32x4 s[2][2][2];  // [block][t][qt]
@@ -55,7 +56,7 @@ __device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][2], float (&
             for (int t = 0; t < 2; ++t) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    float v = s[blk][t][qt][r] * scale_log2;
+                    float v = s[blk][t][qt][r];
                     if constexpr (MASK) {
                         const int key = k0 + 32 * blk + Pol::bidx(t, g, r);
                         v = (key >= Nk || (CAUSAL && key > qpos)) ? -INFINITY : v;
@@ -129,6 +130,9 @@ __global__ __launch_bounds__(256, Pol::kWaves) void fwd_kernel(Params p) {
     for (int qt = 0; qt < 2; ++qt) {
         const int qi = q0 + 16 * qt + l16;
         Pol::gmem_row_frags(qf[qt], Q + (size_t)qi * p.q_rs, g, qi < N);
+        // Q scale log2(e): the scores come out of the MFMAs in log2 units
+#pragma unroll
+        for (int kc = 0; kc < NC; ++kc) qf[qt][kc] = Pol::scaled(qf[qt][kc], p.scale_log2);
     }
     f32x4 acc[XT][2];
 #pragma unroll
@@ -150,10 +154,9 @@ __global__ __launch_bounds__(256, Pol::kWaves) void fwd_kernel(Params p) {
         if (!CAUSAL || k0 <= qpos0 + 31) {
             const bool need_mask = (k0 + BK > Nk) || (CAUSAL && k0 + BK - 1 > qpos0);
             if (need_mask) {
-                fwd_stage<Pol, CAUSAL, true>(acc, m, lsum, qf, sK[cur], sV[cur], k0, qpos0, Nk, p.scale_log2, g, l16);
+                fwd_stage<Pol, CAUSAL, true>(acc, m, lsum, qf, sK[cur], sV[cur], k0, qpos0, Nk, g, l16);
             } else {
-                fwd_stage<Pol, CAUSAL, false>(acc, m, lsum, qf, sK[cur], sV[cur], k0, qpos0, Nk, p.scale_log2, g,
-                                              l16);
+                fwd_stage<Pol, CAUSAL, false>(acc, m, lsum, qf, sK[cur], sV[cur], k0, qpos0, Nk, g, l16);
             }
         }
         wait_stage();
