@@ -206,7 +206,26 @@ __global__ __launch_bounds__(64 * NW, Pol::kWaves * 4 / NW) void dq_kernel(Param
     wait_stage();
     __syncthreads();
 
-    for (int st = 0; st < nsteps; ++st) {
+    // Every stage but the last two is unmasked for every wave (causal: its keys
+    // all precede the workgroup's first query; otherwise: only the last stage
+    // can be ragged). Those run in pairs with the LDS buffer a compile-time
+    // constant, so the tile addresses fold into the instructions' immediate
+    // offsets; the last two stages choose their buffer and masking at run time.
+    auto main_stage = [&](auto buf, int st) __attribute__((always_inline)) {
+        constexpr int B = decltype(buf)::value;
+        if (st + 1 < nsteps) stage_kv<Pol, NT>(sK[B ^ 1], sV[B ^ 1], K, V, (st + 1) * BK, N, tid, wave);
+        dq_stage<Pol, CAUSAL, false>(acc, qf, dof, nL2, Dl, sK[B], sV[B], st * BK, q0, N, g, l16);
+        wait_stage();
+        __syncthreads();
+    };
+    const int nmain = nsteps - min(nsteps, 2);
+    int st = 0;
+    for (; st + 1 < nmain; st += 2) {
+        main_stage(std::integral_constant<int, 0>{}, st);
+        main_stage(std::integral_constant<int, 1>{}, st + 1);
+    }
+    if (st < nmain) main_stage(std::integral_constant<int, 0>{}, st++);
+    for (; st < nsteps; ++st) {
         const int cur = st & 1;
         if (st + 1 < nsteps) stage_kv<Pol, NT>(sK[cur ^ 1], sV[cur ^ 1], K, V, (st + 1) * BK, N, tid, wave);
         const int k0 = st * BK;
