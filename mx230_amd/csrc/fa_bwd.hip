@@ -536,11 +536,34 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDkv * 4 / NW) void dkv_kernel(P
         }
         barrier_lds();
     };
+    // The unmasked stages with the LDS buffer a compile-time constant (two
+    // buffers), so the tile addresses fold into the instructions' immediate
+    // offsets. No wave skips them: their queries follow all the workgroup's keys.
+    auto run_fixed = [&](auto buf, int st) __attribute__((always_inline)) {
+        constexpr int B = decltype(buf)::value;
+        if (st + 1 < nsteps) issue(st + 1);
+        const int qs = qstart + (st % nqs) * BQ;
+        dkv_stage<Pol, KT, CAUSAL, false>(accK, accV, kf, vf, sQ[B], sdO[B], sL[B], sD[B], qs, kw0, N, g, l16);
+        wait_stage();
+        barrier_lds();
+    };
+    using Buf0 = std::integral_constant<int, 0>;
+    using Buf1 = std::integral_constant<int, 1>;
     // rows past N get p = 0 from LSE = +inf, so only the causal diagonal masks
     const int ndiag = CAUSAL ? min(nqs, BKV / BQ) : 0;
     for (int hh = 0, st = 0; hh < p.group; ++hh) {
         for (int i = 0; i < ndiag; ++i, ++st) run(std::true_type{}, st);
-        for (int i = ndiag; i < nqs; ++i, ++st) run(std::false_type{}, st);
+        if constexpr (NBUF == 2) {
+            int i = ndiag;
+            if (i < nqs && (st & 1)) run_fixed(Buf1{}, st++), ++i;
+            for (; i + 1 < nqs; i += 2, st += 2) {
+                run_fixed(Buf0{}, st);
+                run_fixed(Buf1{}, st + 1);
+            }
+            if (i < nqs) run_fixed(Buf0{}, st++);
+        } else {
+            for (int i = ndiag; i < nqs; ++i, ++st) run(std::false_type{}, st);
+        }
     }
 
     T *dK = static_cast<T *>(p.dk) + kvoff;
