@@ -15,6 +15,8 @@
 //   * exponentials are base 2 with log2(e) folded into the scale;
 //   * only stages that straddle the causal diagonal or the end of the sequence
 //     run the masking code (a separate instantiation of the stage body).
+#include <type_traits>
+
 #include "fa_device.h"
 #include "fa_launch.h"
 
@@ -146,7 +148,25 @@ __global__ __launch_bounds__(256, Pol::kWaves) void fwd_kernel(Params p) {
     wait_stage();
     __syncthreads();
 
-    for (int st = 0; st < nsteps; ++st) {
+    // Leading stages that no wave masks (all their keys exist and precede the
+    // workgroup's first query position) run in pairs with the LDS buffer a
+    // compile-time constant, so the tile addresses fold into the instructions'
+    // immediate offsets; the rest choose buffer and masking at run time.
+    auto main_stage = [&](auto buf, int st) __attribute__((always_inline)) {
+        constexpr int B = decltype(buf)::value;
+        if (st + 1 < nsteps) stage_kv<Pol>(sK[B ^ 1], sV[B ^ 1], K, V, (st + 1) * BK, Nk, tid, wave, p.kv_rs);
+        fwd_stage<Pol, CAUSAL, false>(acc, m, lsum, qf, sK[B], sV[B], st * BK, qpos0, Nk, g, l16);
+        wait_stage();
+        __syncthreads();
+    };
+    const int nmain = min(min(nsteps, Nk / BK), CAUSAL ? (pos0 + qb * BQ + 1) / BK : nsteps);
+    int st = 0;
+    for (; st + 1 < nmain; st += 2) {
+        main_stage(std::integral_constant<int, 0>{}, st);
+        main_stage(std::integral_constant<int, 1>{}, st + 1);
+    }
+    if (st < nmain) main_stage(std::integral_constant<int, 0>{}, st++);
+    for (; st < nsteps; ++st) {
         const int cur = st & 1;
         if (st + 1 < nsteps) stage_kv<Pol>(sK[cur ^ 1], sV[cur ^ 1], K, V, (st + 1) * BK, Nk, tid, wave, p.kv_rs);
         const int k0 = st * BK;
