@@ -110,6 +110,17 @@ def test_gqa_tinyllama_shape_reduced(d):
     _check(f"tinyllama-d{d}-n256", q, k, v, do, True, True)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("n", [576, 200])
+def test_gqa_odd_stage_count(causal, n):
+    """Query heads of a GQA group with an odd number of 64-query stages each
+    (N = 576: 9 - 2 kb stages per head; N = 200: 4 - 2 kb rounded up), so the
+    dK/dV stage ring enters every other head's unmasked run on its second
+    buffer, and the dQ / forward main loops end on an unpaired stage."""
+    q, k, v, do = make_inputs(1, 6, 2, n, 64, bf16=True, seeds=(31, 32, 33, 34))
+    _check(f"gqa-odd-n{n}", q, k, v, do, causal, True)
+
+
 def test_gqa_fp32_small():
     q, k, v, do = make_inputs(2, 6, 2, 96, 64)
     _check("gqa-f32", q, k, v, do, True, False)
