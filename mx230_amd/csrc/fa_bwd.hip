@@ -493,10 +493,16 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDkv * 4 / NW) void dkv_kernel(P
     const int nsteps = nqs * p.group;
     const size_t bh0 = (size_t)b * p.Hq + (size_t)kvh * p.group;
 
+    // Stages are loaded strictly in order; (ld_h, ld_i) = query head and stage
+    // within it of the next one (kept incrementally: no division per stage).
+    int ld_h = 0, ld_i = 0;
     auto issue = [&](int st) __attribute__((always_inline)) {
         const int bf = st % NBUF;
-        stage_qdo<Pol, NT>(sQ[bf], sdO[bf], sL[bf], sD[bf], p, bh0 + st / nqs, qstart + (st % nqs) * BQ, N, tid,
-                           wave, lane);
+        stage_qdo<Pol, NT>(sQ[bf], sdO[bf], sL[bf], sD[bf], p, bh0 + ld_h, qstart + ld_i * BQ, N, tid, wave, lane);
+        if (++ld_i == nqs) {
+            ld_i = 0;
+            ++ld_h;
+        }
     };
     // loads of one stage per thread: the Q and dO tiles (+1 vector on waves
     // 0-1, which the waits below may over-wait by one load)
@@ -518,12 +524,12 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDkv * 4 / NW) void dkv_kernel(P
     // they run in a loop of their own with the masked body, so neither loop
     // carries the other's code (two bodies behind one branch make the register
     // allocator spill).
-    auto run = [&](auto mask_tag, int st) __attribute__((always_inline)) {
+    auto run = [&](auto mask_tag, int st, int i) __attribute__((always_inline)) {
         constexpr bool MASK = decltype(mask_tag)::value;
         const int cur = st % NBUF;
         const bool ahead = st + NBUF - 1 < nsteps;
         if (ahead) issue(st + NBUF - 1);
-        const int qs = qstart + (st % nqs) * BQ;
+        const int qs = qstart + i * BQ;
         // a wave whose keys all follow the stage's queries has nothing to do
         if (!CAUSAL || qs + BQ - 1 >= kw0) {
             dkv_stage<Pol, KT, CAUSAL, MASK>(accK, accV, kf, vf, sQ[cur], sdO[cur], sL[cur], sD[cur], qs, kw0, N, g,
@@ -539,10 +545,10 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDkv * 4 / NW) void dkv_kernel(P
     // The unmasked stages with the LDS buffer a compile-time constant (two
     // buffers), so the tile addresses fold into the instructions' immediate
     // offsets. No wave skips them: their queries follow all the workgroup's keys.
-    auto run_fixed = [&](auto buf, int st) __attribute__((always_inline)) {
+    auto run_fixed = [&](auto buf, int st, int i) __attribute__((always_inline)) {
         constexpr int B = decltype(buf)::value;
         if (st + 1 < nsteps) issue(st + 1);
-        const int qs = qstart + (st % nqs) * BQ;
+        const int qs = qstart + i * BQ;
         dkv_stage<Pol, KT, CAUSAL, false>(accK, accV, kf, vf, sQ[B], sdO[B], sL[B], sD[B], qs, kw0, N, g, l16);
         wait_stage();
         barrier_lds();
@@ -552,17 +558,17 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDkv * 4 / NW) void dkv_kernel(P
     // rows past N get p = 0 from LSE = +inf, so only the causal diagonal masks
     const int ndiag = CAUSAL ? min(nqs, BKV / BQ) : 0;
     for (int hh = 0, st = 0; hh < p.group; ++hh) {
-        for (int i = 0; i < ndiag; ++i, ++st) run(std::true_type{}, st);
+        for (int i = 0; i < ndiag; ++i, ++st) run(std::true_type{}, st, i);
         if constexpr (NBUF == 2) {
             int i = ndiag;
-            if (i < nqs && (st & 1)) run_fixed(Buf1{}, st++), ++i;
+            if (i < nqs && (st & 1)) run_fixed(Buf1{}, st++, i++);
             for (; i + 1 < nqs; i += 2, st += 2) {
-                run_fixed(Buf0{}, st);
-                run_fixed(Buf1{}, st + 1);
+                run_fixed(Buf0{}, st, i);
+                run_fixed(Buf1{}, st + 1, i + 1);
             }
-            if (i < nqs) run_fixed(Buf0{}, st++);
+            if (i < nqs) run_fixed(Buf0{}, st++, i);
         } else {
-            for (int i = ndiag; i < nqs; ++i, ++st) run(std::false_type{}, st);
+            for (int i = ndiag; i < nqs; ++i, ++st) run(std::false_type{}, st, i);
         }
     }
 
