@@ -662,10 +662,17 @@ __global__ __launch_bounds__(512) void dkv_pp_kernel(Params p) {
 
     // Loads of stage st: group B stages the Q tile (2 loads per thread),
     // group A the dO tile and, on its waves 0 and 1, the LSE / Delta vectors.
+    // Every wave issues the stages in order; (ld_h, ld_i) = query head and
+    // stage within it of the next one (kept incrementally: no division).
+    int ld_h = 0, ld_i = 0;
     auto issue = [&](int st) __attribute__((always_inline)) {
         const int bf = st % NBUF;
-        const size_t bh = bh0 + st / nqs;
-        const int qs = qstart + (st % nqs) * BQ;
+        const size_t bh = bh0 + ld_h;
+        const int qs = qstart + ld_i * BQ;
+        if (++ld_i == nqs) {
+            ld_i = 0;
+            ++ld_h;
+        }
         const size_t off = (bh * N + qs) * D;
         if (grp == 1) {
             stage_rows<Pol>(tq(bf), static_cast<const T *>(p.q) + off, N - qs, gtid, pair);
@@ -698,7 +705,7 @@ __global__ __launch_bounds__(512) void dkv_pp_kernel(Params p) {
     issue(0);
     if (nsteps > 1) issue(1);
     wait_stage();
-    barrier_lds();
+    barrier_phase();
 
     // Per-wave pipeline state: scores awaiting their softmax (M -> V), chain
     // operands awaiting their GEMMs (V -> next M). Every block is computed:
@@ -737,41 +744,41 @@ __global__ __launch_bounds__(512) void dkv_pp_kernel(Params p) {
     // segment 2 st, A in 2 st + 1), once stage st - 2's buffer is free.
     if (grp == 0) {
         first_scores();
-        barrier_lds();
+        barrier_phase();
         if (nsteps > 2) issue(2);
         v_phase(0, 0);
         wait_next(0);
-        barrier_lds();
+        barrier_phase();
         for (int st = 1, i = 0; st < nsteps; ++st) {
             if (++i == nqs) i = 0;
             m_phase(st);
-            barrier_lds();
+            barrier_phase();
             if (st + 2 < nsteps) issue(st + 2);
             v_phase(st, i);
             wait_next(st);
-            barrier_lds();
+            barrier_phase();
         }
         pp::chain_block<Pol>(accK, accV, cp, cds, cdo, cq);
     } else {
         if (nsteps > 2) issue(2);
-        barrier_lds();
+        barrier_phase();
         first_scores();
         wait_next(0);
-        barrier_lds();
+        barrier_phase();
         int ip = 0;  // stage index within its query head, of stage st - 1
         for (int st = 1; st < nsteps; ++st) {
             if (st + 2 < nsteps) issue(st + 2);
             v_phase(st - 1, ip);
-            barrier_lds();
+            barrier_phase();
             m_phase(st);
             wait_next(st);
-            barrier_lds();
+            barrier_phase();
             if (++ip == nqs) ip = 0;
         }
         v_phase(nsteps - 1, ip);
         pp::chain_block<Pol>(accK, accV, cp, cds, cdo, cq);
     }
-    barrier_lds();
+    barrier_phase();
 
     // exchange: group A publishes its dV partials, group B its dK partials.
     // (Selected by value: a conditional between two array elements would take
@@ -792,7 +799,7 @@ __global__ __launch_bounds__(512) void dkv_pp_kernel(Params p) {
 #pragma unroll
         for (int kt = 0; kt < KT; ++kt) xch[(wave * 8 + xt * KT + kt) * 64 + lane] = give[xt][kt];
     }
-    barrier_lds();
+    barrier_phase();
     const int other = wave ^ 4;
     T *out = static_cast<T *>(grp == 0 ? p.dk : p.dv) + kvoff;
     const float mul = grp == 0 ? -p.scale : 1.0f;

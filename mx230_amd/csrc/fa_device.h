@@ -385,6 +385,16 @@ __device__ __forceinline__ void wait_stage() { __builtin_amdgcn_s_waitcnt(0); }
 // compiler memory barrier, so no LDS access moves across it.
 __device__ __forceinline__ void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// barrier_lds() that also fences the instruction scheduler: register-only
+// instructions (MFMAs above all) are not moved across it either. The asm alone
+// orders memory accesses only, and the scheduler otherwise sinks MFMAs past
+// the barrier into the next phase.
+__device__ __forceinline__ void barrier_phase() {
+    __builtin_amdgcn_sched_barrier(0);
+    barrier_lds();
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 // Waits until at most VM of this wave's vector-memory loads are outstanding
 // (s_waitcnt vmcnt(VM); expcnt and lgkmcnt left unconstrained): with loads
 // issued for two stages ahead, the older stage is complete while the newer
