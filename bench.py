@@ -4,7 +4,9 @@ Workload (BASELINE.json metric): B=4, H=12, N=4096, d=64, causal, bf16 inputs
 with fp32 accumulation. Synthetic seeded N(0,1) Q, K, V, dO generated on the
 GPU. The forward (O, LSE) runs once before the timed region, as in the
 reference (02-flash-attention/src/main.rs:599-611). One timed step = one full
-backward pass: Delta preprocess + dK/dV pass + dQ pass, inputs resident in HBM.
+backward pass from O (mxfa_run_bwd): the dQ pass with Delta = rowsum(dO * O)
+folded in, then the dK/dV pass, inputs resident in HBM (--separate-delta: the
+reference-shaped preprocess launch + dQ pass + dK/dV pass instead).
 
 Prints one JSON line. ``value`` is the algorithmic backward throughput
 (10 N^2 d per (batch, head), halved for causal) in TFLOP/s. ``roofline`` is the
@@ -45,6 +47,8 @@ def parse():
     ap.add_argument("--causal", type=int, default=1)
     ap.add_argument("--dtype", choices=["bf16", "f32"], default="bf16")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--separate-delta", action="store_true",
+                    help="run the reference-shaped sequence (preprocess launch, then the dQ pass reading Delta)")
     ap.add_argument("--no-probe", action="store_true",
                     help="skip the roofline probes (measured MFMA / HBM ceilings, after the timed region)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -145,36 +149,56 @@ def main():
     fwd_avg = sum(x.elapsed_time(y) for x, y in fwd_ms) / len(fwd_ms)
 
     def step(evs=None):
+        # the backward from O (mxfa_run_bwd): the dQ pass computes Delta
+        # itself and writes it for the dK/dV pass; with --separate-delta the
+        # reference-shaped preprocess launch runs first instead. evs: events
+        # recorded on the launch stream before each launch and after the last.
+        i = 0
+        if a.separate_delta:
+            if evs:
+                evs[i].record(stream)
+                i += 1
+            mx.run_preprocess(do, o, delta)
         if evs:
-            evs[0].record(stream)
-        mx.run_preprocess(do, o, delta)
+            evs[i].record(stream)
+            i += 1
+        if a.separate_delta:
+            mx.run_bwd_dq(q, k, v, do, lse, delta, dq, causal)
+        else:
+            mx.run_bwd_dq_delta(q, k, v, o, do, lse, delta, dq, causal)
         if evs:
-            evs[1].record(stream)
+            evs[i].record(stream)
+            i += 1
         mx.run_bwd_dkv(q, k, v, do, lse, delta, dk, dv, causal)
         if evs:
-            evs[2].record(stream)
-        mx.run_bwd_dq(q, k, v, do, lse, delta, dq, causal)
-        if evs:
-            evs[3].record(stream)
+            evs[i].record(stream)
 
     for _ in range(a.warmup):
         step()
     torch.cuda.synchronize()
 
-    # timed region: exactly K backward steps, synchronised on both sides; the
-    # events between the launches give each kernel's duration on the same stream
-    evsets = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(a.steps)]
+    # timed region: exactly K backward steps, synchronised on both sides, timed
+    # by one event pair around them on the launch stream (an event recorded
+    # between two launches costs a few microseconds of stream time, so the
+    # per-kernel events are kept out of this region)
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for _ in range(a.steps):
+        step()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms_per_step = t0.elapsed_time(t1) / a.steps
+
+    # second timed region of K steps with events between the launches: each
+    # kernel's average duration on the same stream (the roofline's basis)
+    names = (["preprocess"] if a.separate_delta else []) + ["dq", "dkv"]
+    evsets = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)] for _ in range(a.steps)]
     torch.cuda.synchronize()
     for evs in evsets:
         step(evs)
     torch.cuda.synchronize()
-    ms_per_step = evsets[0][0].elapsed_time(evsets[-1][3]) / a.steps
-    kern = {"preprocess": 0.0, "dkv": 0.0, "dq": 0.0}
-    for evs in evsets:
-        kern["preprocess"] += evs[0].elapsed_time(evs[1])
-        kern["dkv"] += evs[1].elapsed_time(evs[2])
-        kern["dq"] += evs[2].elapsed_time(evs[3])
-    kern = {n: t / a.steps for n, t in kern.items()}
+    kern = {n: sum(evs[j].elapsed_time(evs[j + 1]) for evs in evsets) / a.steps for j, n in enumerate(names)}
 
     half = 0.5 if causal else 1.0
     bwd_flops = mx.bwd_flops(a.B, a.H, a.N, a.d, causal)
@@ -198,7 +222,9 @@ def main():
         "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": a.dtype,
         "data": "synthetic (seeded N(0,1) on the GPU)",
-        "config": {"workload": "flash-attention backward (preprocess + dK/dV + dQ), fwd outside timing",
+        "config": {"workload": "flash-attention backward (dQ with Delta folded in + dK/dV), fwd outside timing"
+                   if not a.separate_delta else
+                   "flash-attention backward (preprocess + dQ + dK/dV), fwd outside timing",
                    "B": a.B, "Hq": a.H, "Hkv": hkv, "N": a.N, "d": a.d, "causal": causal,
                    "parallelism": "single GPU"},
         "pct_peak": round(100.0 * value / peak, 2),

@@ -120,6 +120,23 @@ int mxfa_run_bwd_flash(const mxfa_shape *shape, const void *q, const void *k, co
                        const void *dout, const float *lse, const float *delta, void *dq,
                        void *dk, void *dv, void *stream);
 
+/* dQ pass that also computes Delta = rowsum(dO * O) for its query rows and
+ * writes it to `delta` (the preprocess launch, attention_bwd.cu:32-44,
+ * folded into the attn_bwd_dq launch, :96-158). */
+int mxfa_run_bwd_dq_delta(const mxfa_shape *shape, const void *q, const void *k, const void *v, const void *o,
+                          const void *dout, const float *lse, float *delta, void *dq, void *stream);
+
+/* The whole backward from O in two launches: the dQ pass computes
+ * Delta = rowsum(dO * O) itself (writing it to `delta`, B*Hq*N fp32, which the
+ * caller owns as for mxfa_run_preprocess) and the dK/dV pass reads it.
+ * Replaces the sequence run_preprocess + run_bwd_flash (main.rs:126-143,
+ * :179-210; attention_bwd.cu:32-44, :96-243) with the preprocess launch folded
+ * into the dQ pass; results equal that sequence's up to the summation order of
+ * Delta. */
+int mxfa_run_bwd(const mxfa_shape *shape, const void *q, const void *k, const void *v, const void *o,
+                 const void *dout, const float *lse, float *delta, void *dq, void *dk, void *dv,
+                 void *stream);
+
 /* Bytes of device workspace the backward needs beyond its inputs and
  * outputs: always 0 (dQ is a separate atomic-free pass). */
 size_t mxfa_bwd_workspace_bytes(const mxfa_shape *shape);

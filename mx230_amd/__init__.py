@@ -43,7 +43,7 @@ STATUS = {
 EXPORTS = (
     "mxfa_version", "mxfa_strerror", "mxfa_init", "mxfa_shutdown", "mxfa_check_shape",
     "mxfa_run_flash", "mxfa_run_flash_lse", "mxfa_run_preprocess", "mxfa_run_bwd_dq",
-    "mxfa_run_bwd_dkv", "mxfa_run_bwd_flash", "mxfa_bwd_workspace_bytes", "mxfa_run_bwd_naive",
+    "mxfa_run_bwd_dkv", "mxfa_run_bwd_flash", "mxfa_run_bwd_dq_delta", "mxfa_run_bwd", "mxfa_bwd_workspace_bytes", "mxfa_run_bwd_naive",
     "mxfa_naive_scratch_bytes", "mxfa_run_naive_fwd", "mxfa_check_prefill", "mxfa_run_prefill",
     "mxfa_probe_sink_len", "mxfa_probe_mfma", "mxfa_probe_read", "mxfa_probe_copy",
 )
@@ -102,6 +102,8 @@ def load_library(path: str | None = None):
     lib.mxfa_run_bwd_dq.argtypes = [sp, vp, vp, vp, vp, fp, fp, vp, vp]
     lib.mxfa_run_bwd_dkv.argtypes = [sp, vp, vp, vp, vp, fp, fp, vp, vp, vp]
     lib.mxfa_run_bwd_flash.argtypes = [sp, vp, vp, vp, vp, fp, fp, vp, vp, vp, vp]
+    lib.mxfa_run_bwd.argtypes = [sp, vp, vp, vp, vp, vp, fp, fp, vp, vp, vp, vp]
+    lib.mxfa_run_bwd_dq_delta.argtypes = [sp, vp, vp, vp, vp, vp, fp, fp, vp, vp]
     lib.mxfa_run_bwd_naive.argtypes = [sp, vp, vp, vp, vp, fp, fp, vp, vp, vp, vp]
     lib.mxfa_bwd_workspace_bytes.argtypes = [sp]
     lib.mxfa_bwd_workspace_bytes.restype = ctypes.c_size_t
@@ -261,6 +263,30 @@ def run_bwd_flash(q, k, v, do, lse, delta, dq, dk, dv, causal: bool, scale: floa
            load_library().mxfa_run_bwd_flash(ctypes.byref(sh.c()), *args, _stream(stream)))
 
 
+def run_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, causal: bool, scale: float = 0.0, stream=None):
+    """The whole backward from O in two launches (mxfa_run_bwd): the dQ pass
+    computes Delta = rowsum(dO * O) itself and writes it to ``delta`` for the
+    dK/dV pass (run_preprocess + run_bwd_flash with the preprocess launch folded
+    in). Outputs are overwritten."""
+    sh = shape_of(q, k, causal, scale)
+    dt, qs, ks = _io(sh)
+    args = [_expect(q, "q", qs, dt), _expect(k, "k", ks, dt), _expect(v, "v", ks, dt), _expect(o, "o", qs, dt),
+            _expect(do, "do", qs, dt), _vec_ptr(lse, "lse", sh), _vec_ptr(delta, "delta", sh),
+            _expect(dq, "dq", qs, dt), _expect(dk, "dk", ks, dt), _expect(dv, "dv", ks, dt)]
+    _check("mxfa_run_bwd", load_library().mxfa_run_bwd(ctypes.byref(sh.c()), *args, _stream(stream)))
+
+
+def run_bwd_dq_delta(q, k, v, o, do, lse, delta, dq, causal: bool, scale: float = 0.0, stream=None):
+    """dQ pass that computes Delta from O itself and writes it to ``delta``."""
+    sh = shape_of(q, k, causal, scale)
+    dt, qs, ks = _io(sh)
+    args = [_expect(q, "q", qs, dt), _expect(k, "k", ks, dt), _expect(v, "v", ks, dt), _expect(o, "o", qs, dt),
+            _expect(do, "do", qs, dt), _vec_ptr(lse, "lse", sh), _vec_ptr(delta, "delta", sh),
+            _expect(dq, "dq", qs, dt)]
+    _check("mxfa_run_bwd_dq_delta", load_library().mxfa_run_bwd_dq_delta(ctypes.byref(sh.c()), *args,
+                                                                          _stream(stream)))
+
+
 def run_bwd_dq(q, k, v, do, lse, delta, dq, causal: bool, scale: float = 0.0, stream=None):
     """dQ pass alone (attention_bwd.cu:96-158)."""
     sh, dt, qs, ks, args = _bwd_args(q, k, v, do, lse, delta, causal, scale)
@@ -361,13 +387,13 @@ def attention_fwd(q, k, v, causal: bool, scale: float = 0.0, stream=None):
 
 
 def attention_bwd(q, k, v, o, lse, do, causal: bool, scale: float = 0.0, stream=None):
-    """Allocates Delta, dQ, dK, dV and runs preprocess + backward; returns (dQ, dK, dV)."""
+    """Allocates Delta, dQ, dK, dV and runs the backward (run_bwd: Delta folded
+    into the dQ pass); returns (dQ, dK, dV)."""
     torch = _torch()
     sh = shape_of(q, k, causal, scale)
     delta = torch.empty((sh.B, sh.Hq, sh.N), dtype=torch.float32, device=q.device)
-    run_preprocess(do, o, delta, stream)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    run_bwd_flash(q, k, v, do, lse, delta, dq, dk, dv, causal, scale, stream)
+    run_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, causal, scale, stream)
     return dq, dk, dv
 
 

@@ -154,7 +154,10 @@ __device__ __forceinline__ void dq_stage(f32x4 (&acc)[Pol::D / 16][2], const typ
     }
 }
 
-template <class Pol, bool CAUSAL, int NW>
+// DELTA: compute Delta_i = sum_x dO[i,x] O[i,x] here (O from p.o_in, the
+// same fp32 products as preprocess_kernel, summed in another order) and write
+// it to p.delta for the dK/dV pass, instead of reading it from there.
+template <class Pol, bool CAUSAL, int NW, bool DELTA>
 __global__ __launch_bounds__(64 * NW, Pol::kWaves * 4 / NW) void dq_kernel(Params p) {
     using T = typename Pol::T;
     using Frag = typename Pol::Frag;
@@ -187,13 +190,25 @@ __global__ __launch_bounds__(64 * NW, Pol::kWaves * 4 / NW) void dq_kernel(Param
         const bool ok = qi < N;
         Pol::gmem_row_frags(qf[qt], Q + (size_t)qi * D, g, ok);
         Pol::gmem_row_frags(dof[qt], dO + (size_t)qi * D, g, ok);
+        if constexpr (DELTA) {
+            // the lane holds 16 of the row's d elements; the 4 lane groups
+            // g = 0..3 together hold the row
+            Frag of[NC];
+            Pol::gmem_row_frags(of, static_cast<const T *>(p.o_in) + (size_t)bh * N * D + (size_t)qi * D, g, ok);
+            float dsum = 0.f;
+#pragma unroll
+            for (int kc = 0; kc < NC; ++kc) dsum += Pol::dot(dof[qt][kc], of[kc]);
+            Dl[qt] = xg_sum(dsum);
+            if (ok && g == 0) p.delta[(size_t)bh * N + qi] = Dl[qt];
+        } else {
+            Dl[qt] = ok ? p.delta[(size_t)bh * N + qi] : 0.f;
+        }
 #pragma unroll
         for (int kc = 0; kc < NC; ++kc) {
             qf[qt][kc] = Pol::scaled(qf[qt][kc], p.scale_log2);
             dof[qt][kc] = Pol::neg(dof[qt][kc]);
         }
         nL2[qt] = ok ? p.lse[(size_t)bh * N + qi] * -kLog2e : 0.f;
-        Dl[qt] = ok ? p.delta[(size_t)bh * N + qi] : 0.f;
     }
     f32x4 acc[XT][2];
 #pragma unroll
@@ -834,16 +849,20 @@ hipError_t launch_preprocess(const Params &p, int dtype_bf16, int d, hipStream_t
 }
 
 template <class Pol, bool CAUSAL, int NW = 4>
-static hipError_t launch_dq_t(const Params &p, hipStream_t stream) {
+static hipError_t launch_dq_t(const Params &p, int delta, hipStream_t stream) {
     const dim3 grid(p.B * p.Hq, (p.N + 32 * NW - 1) / (32 * NW));
-    hipLaunchKernelGGL((dq_kernel<Pol, CAUSAL, NW>), grid, dim3(64 * NW), 0, stream, p);
+    if (delta) {
+        hipLaunchKernelGGL((dq_kernel<Pol, CAUSAL, NW, true>), grid, dim3(64 * NW), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL((dq_kernel<Pol, CAUSAL, NW, false>), grid, dim3(64 * NW), 0, stream, p);
+    }
     return hipGetLastError();
 }
 
-hipError_t launch_bwd_dq(const Params &p, int dtype_bf16, int d, int causal, hipStream_t stream) {
+hipError_t launch_bwd_dq(const Params &p, int dtype_bf16, int d, int causal, int delta, hipStream_t stream) {
 #define MXFA_DQ(POL, DD)                                                        \
-    if (d == DD) return causal ? launch_dq_t<POL<DD>, true>(p, stream)         \
-                               : launch_dq_t<POL<DD>, false>(p, stream);
+    if (d == DD) return causal ? launch_dq_t<POL<DD>, true>(p, delta, stream)  \
+                               : launch_dq_t<POL<DD>, false>(p, delta, stream);
     if (dtype_bf16) {
         MXFA_DQ(PolBF16, 64)
         MXFA_DQ(PolBF16, 128)

@@ -160,6 +160,13 @@ struct PolBF16 {
             }
         }
     }
+    // sum of the element products, in fp32
+    __device__ static __forceinline__ float dot(Frag a, Frag b) {
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d += (float)a[e] * (float)b[e];
+        return d;
+    }
     // every element times s, rounded to bf16 (nearest even), pinned in
     // registers like neg()
     __device__ static __forceinline__ Frag scaled(Frag f, float s) {
@@ -267,6 +274,7 @@ struct PolF32 {
     }
     __device__ static __forceinline__ Frag neg(Frag f) { return -f; }
     __device__ static __forceinline__ Frag scaled(Frag f, float s) { return f * s; }
+    __device__ static __forceinline__ float dot(Frag a, Frag b) { return a * b; }
     // The chain operand of one 32-row block: the two C tiles themselves.
     struct ChainB {
         f32x4 c0, c1;

@@ -11,7 +11,8 @@ namespace mxfa {
 
 hipError_t launch_fwd(const Params &p, int dtype_bf16, int d, int causal, hipStream_t stream);
 hipError_t launch_preprocess(const Params &p, int dtype_bf16, int d, hipStream_t stream);
-hipError_t launch_bwd_dq(const Params &p, int dtype_bf16, int d, int causal, hipStream_t stream);
+// delta != 0: the dQ pass computes Delta from p.o_in and writes it to p.delta
+hipError_t launch_bwd_dq(const Params &p, int dtype_bf16, int d, int causal, int delta, hipStream_t stream);
 hipError_t launch_bwd_dkv(const Params &p, int dtype_bf16, int d, int causal, hipStream_t stream);
 hipError_t launch_bwd_naive(const Params &p, int d, int causal, hipStream_t stream);
 hipError_t launch_naive_fwd(const Params &p, float *s, int d, int causal, hipStream_t stream);

@@ -161,7 +161,7 @@ int mxfa_run_bwd_dq(const mxfa_shape *shape, const void *q, const void *k, const
     if (rc != MXFA_OK) return rc;
     Params p = bwd_params(shape, q, k, v, dout, lse, delta);
     p.dq = dq;
-    return from_hip(mxfa::launch_bwd_dq(p, shape->dtype == MXFA_BF16, shape->d, shape->causal,
+    return from_hip(mxfa::launch_bwd_dq(p, shape->dtype == MXFA_BF16, shape->d, shape->causal, 0,
                                         static_cast<hipStream_t>(stream)));
 }
 
@@ -188,6 +188,31 @@ int mxfa_run_bwd_flash(const mxfa_shape *shape, const void *q, const void *k, co
     rc = mxfa_run_bwd_dkv(shape, q, k, v, dout, lse, delta, dk, dv, stream);
     if (rc != MXFA_OK) return rc;
     return mxfa_run_bwd_dq(shape, q, k, v, dout, lse, delta, dq, stream);
+}
+
+int mxfa_run_bwd_dq_delta(const mxfa_shape *shape, const void *q, const void *k, const void *v, const void *o,
+                          const void *dout, const float *lse, float *delta, void *dq, void *stream) {
+    int rc = check_shape(shape);
+    if (rc != MXFA_OK) return rc;
+    rc = check_ptrs({q, k, v, o, dout, lse, delta, dq});
+    if (rc != MXFA_OK) return rc;
+    Params p = bwd_params(shape, q, k, v, dout, lse, delta);
+    p.o_in = o;
+    p.dq = dq;
+    return from_hip(mxfa::launch_bwd_dq(p, shape->dtype == MXFA_BF16, shape->d, shape->causal, 1,
+                                        static_cast<hipStream_t>(stream)));
+}
+
+int mxfa_run_bwd(const mxfa_shape *shape, const void *q, const void *k, const void *v, const void *o,
+                 const void *dout, const float *lse, float *delta, void *dq, void *dk, void *dv, void *stream) {
+    int rc = check_shape(shape);
+    if (rc != MXFA_OK) return rc;
+    rc = check_ptrs({q, k, v, o, dout, lse, delta, dq, dk, dv});
+    if (rc != MXFA_OK) return rc;
+    // dQ pass first: it computes Delta and writes it for the dK/dV pass
+    rc = mxfa_run_bwd_dq_delta(shape, q, k, v, o, dout, lse, delta, dq, stream);
+    if (rc != MXFA_OK) return rc;
+    return mxfa_run_bwd_dkv(shape, q, k, v, dout, lse, delta, dk, dv, stream);
 }
 
 size_t mxfa_bwd_workspace_bytes(const mxfa_shape *shape) {
