@@ -158,7 +158,7 @@ __device__ __forceinline__ void dq_stage(f32x4 (&acc)[Pol::D / 16][2], const typ
 // same fp32 products as preprocess_kernel, summed in another order) and write
 // it to p.delta for the dK/dV pass, instead of reading it from there.
 template <class Pol, bool CAUSAL, int NW, bool DELTA>
-__global__ __launch_bounds__(64 * NW, Pol::kWaves * 4 / NW) void dq_kernel(Params p) {
+__global__ __launch_bounds__(64 * NW, Pol::kWavesDq * 4 / NW) void dq_kernel(Params p) {
     using T = typename Pol::T;
     using Frag = typename Pol::Frag;
     constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
@@ -244,13 +244,10 @@ __global__ __launch_bounds__(64 * NW, Pol::kWaves * 4 / NW) void dq_kernel(Param
         const int cur = st & 1;
         if (st + 1 < nsteps) stage_kv<Pol, NT>(sK[cur ^ 1], sV[cur ^ 1], K, V, (st + 1) * BK, N, tid, wave);
         const int k0 = st * BK;
+        // one (masked) body for these stages: a second, unmasked body behind a
+        // branch makes the register allocator spill at three waves per SIMD
         if (!CAUSAL || k0 <= q0 + 31) {
-            const bool need_mask = (k0 + BK > N) || (CAUSAL && k0 + BK - 1 > q0);
-            if (need_mask) {
-                dq_stage<Pol, CAUSAL, true>(acc, qf, dof, nL2, Dl, sK[cur], sV[cur], k0, q0, N, g, l16);
-            } else {
-                dq_stage<Pol, CAUSAL, false>(acc, qf, dof, nL2, Dl, sK[cur], sV[cur], k0, q0, N, g, l16);
-            }
+            dq_stage<Pol, CAUSAL, true>(acc, qf, dof, nL2, Dl, sK[cur], sV[cur], k0, q0, N, g, l16);
         }
         wait_stage();
         __syncthreads();

@@ -109,10 +109,14 @@ struct PolBF16 {
     static constexpr int EPC = 8;      // elements per 16-byte chunk
     static constexpr int NC = D / 32;  // MFMAs over D per first-GEMM tile
     static constexpr int ROWS = 64;    // rows of every LDS tile
-    // waves per SIMD the forward / dQ kernels (kWaves) and the dK/dV kernel
-    // (kWavesDkv) are compiled for: the largest count that fits without spills
+    // waves per SIMD the forward (kWaves), dQ (kWavesDq) and dK/dV (kWavesDkv)
+    // kernels are compiled for: the largest count that fits without spills in
+    // their loops. Three work-groups per CU also balance the causal passes:
+    // their 128-row work-groups (64 - 2i stages of 64 for i = 0..31 at
+    // N = 4096) pair up into equal loads over 768 slots.
     static constexpr int kWaves = D == 64 ? 2 : 1;
-    static constexpr int kWavesDkv = 2;
+    static constexpr int kWavesDq = D == 64 ? 3 : 1;
+    static constexpr int kWavesDkv = D == 64 ? 3 : 2;
     // dK/dV stage ring depth (loads issued kDkvBuffers - 1 stages ahead); a
     // third buffer measured no faster at d = 64
     static constexpr int kDkvBuffers = 2;
@@ -231,6 +235,7 @@ struct PolF32 {
     static constexpr int NC = D / 4;
     static constexpr int ROWS = 64;
     static constexpr int kWaves = 1;
+    static constexpr int kWavesDq = 1;
     static constexpr int kWavesDkv = 1;
     static constexpr int kDkvBuffers = 2;
 
