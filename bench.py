@@ -18,6 +18,7 @@ same workload on this host.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-probe]
        [--B 4 --H 12 --Hkv 12 --N 4096 --d 64 --causal 1 --dtype bf16]
+       python bench.py --naive-table   (the reference's naive-vs-flash tables, one JSON line)
 """
 from __future__ import annotations
 
@@ -51,6 +52,9 @@ def parse():
                     help="run the reference-shaped sequence (preprocess launch, then the dQ pass reading Delta)")
     ap.add_argument("--no-probe", action="store_true",
                     help="skip the roofline probes (measured MFMA / HBM ceilings, after the timed region)")
+    ap.add_argument("--naive-table", action="store_true",
+                    help="instead of the benchmark, time the naive and flash paths on the reference's own "
+                         "tables (one fp32 head, d = 64) and print them as one JSON line")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run a plain device-to-device copy of MIB "
                          "MiB three times (calibrates the FETCH_SIZE / WRITE_SIZE counters)")
@@ -68,6 +72,120 @@ def copy_probe(mib):
         y.copy_(x)
     torch.cuda.synchronize()
     print(json.dumps({"copy_probe_bytes_per_launch": n * 4, "launches": 3}), flush=True)
+
+
+# The reference's published MX230 timings for the same rows (ms), for the table
+# mode: 02-flash-attention/README.md:16-21 (forward, non-causal) and :85-87
+# (backward, causal; flash = dQ pass + dK/dV pass, preprocess excluded).
+REF_FWD_MS = {1024: (17.0, 1.4), 2048: (64.7, 4.1), 4096: (275.9, 16.3), 8192: (1152.2, 60.8),
+              16384: (4762.1, 250.4), 32768: (None, 992.9)}
+REF_BWD_MS = {1024: (43.53, 3.90), 2048: (165.12, 14.43), 4096: (641.55, 54.50)}
+
+
+def naive_table():
+    """The reference's naive-vs-flash tables on one MI355X: one head, d = 64,
+    fp32, seeded N(0,1) inputs; each entry the median of 5 timed runs after
+    one warm-up (the reference's time_median_ms, common/src/lib.rs:22-43).
+    Forward: non-causal, naive = scores + softmax + S.V through the N x N
+    scratch (attention_naive.cu), flash = mxfa_run_flash. Backward: causal,
+    naive = the atomic kernel into zeroed outputs (zeroing inside the timed
+    launch sequence, as its caller must), flash = mxfa_run_bwd_flash (dQ pass +
+    dK/dV pass; the preprocess excluded, main.rs:603-611)."""
+    import torch
+    import mx230_amd as mx
+    dev = torch.device("cuda", 0)
+    mx.init(0)
+    stream = torch.cuda.current_stream()
+
+    def median_ms(fn):
+        fn()
+        times = []
+        for _ in range(5):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            fn()
+            e1.record(stream)
+            e1.synchronize()
+            times.append(e0.elapsed_time(e1))
+        return sorted(times)[2]
+
+    gen = torch.Generator(device=dev)
+    rows = []
+    for n in sorted(REF_FWD_MS):
+        gen.manual_seed(n)
+        q, k, v, do = (torch.randn((1, 1, n, 64), generator=gen, device=dev) for _ in range(4))
+        o = torch.empty_like(q)
+        flash = median_ms(lambda: mx.run_flash(q, k, v, o, False))
+        naive = None
+        if n <= 16384:
+            s = torch.empty(mx.naive_scratch_bytes(q, k, False) // 4, device=dev)
+            naive = median_ms(lambda: mx.naive_run(q, k, v, s, o, False))
+            del s
+        ref_naive, ref_flash = REF_FWD_MS[n]
+        rows.append({"pass": "fwd", "causal": False, "N": n, "naive_ms": naive and round(naive, 4),
+                     "flash_ms": round(flash, 4), "speedup": naive and round(naive / flash, 1),
+                     "flash_tflops": round(mx.fwd_flops(1, 1, n, 64, False) / (flash * 1e-3) / 1e12, 2),
+                     "mx230_naive_ms": ref_naive, "mx230_flash_ms": ref_flash})
+        if n in REF_BWD_MS:
+            lse = torch.empty((1, 1, n), device=dev)
+            delta = torch.empty_like(lse)
+            mx.run_flash_lse(q, k, v, o, lse, True)
+            mx.run_preprocess(do, o, delta)
+            dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+            flash = median_ms(lambda: mx.run_bwd_flash(q, k, v, do, lse, delta, dq, dk, dv, True))
+
+            def naive_bwd():
+                dq.zero_()
+                dk.zero_()
+                dv.zero_()
+                mx.run_bwd_naive(q, k, v, do, lse, delta, dq, dk, dv, True)
+            naive = median_ms(naive_bwd)
+            ref_naive, ref_flash = REF_BWD_MS[n]
+            rows.append({"pass": "bwd", "causal": True, "N": n, "naive_ms": round(naive, 4),
+                         "flash_ms": round(flash, 4), "speedup": round(naive / flash, 1),
+                         "flash_tflops": round(mx.bwd_flops(1, 1, n, 64, True) / (flash * 1e-3) / 1e12, 2),
+                         "mx230_naive_ms": ref_naive, "mx230_flash_ms": ref_flash})
+    print(json.dumps({"naive_table": rows, "dtype": "f32", "B": 1, "H": 1, "d": 64,
+                      "data": "synthetic (seeded N(0,1) on the GPU)",
+                      "timing": "median of 5 after 1 warm-up, HIP events on the launch stream"}), flush=True)
+
+
+def cpu_host():
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "cpu": model}
+
+
+def cpu_parallel(a, hkv):
+    """The oracle's multi-head backward over (batch, head) slices on a thread
+    per slice (the parallel CPU figure): 16 slices on up to 16 threads, the
+    host share of a one-GPU box."""
+    import numpy as np
+    import oracle  # the checker; used here only as the timed CPU baseline
+    lib = oracle.load()
+    threads = max(1, min(16, os.cpu_count() or 1))
+    nheads = min(16, a.B * a.H)
+    N, d = a.N, a.d
+    q = np.stack([oracle.normal(N * d, 5000 + i).reshape(N, d) for i in range(nheads)])[None]
+    k = np.stack([oracle.normal(N * d, 6000 + i).reshape(N, d) for i in range(nheads)])[None]
+    v = np.stack([oracle.normal(N * d, 7000 + i).reshape(N, d) for i in range(nheads)])[None]
+    do = np.stack([oracle.normal(N * d, 8000 + i).reshape(N, d) for i in range(nheads)])[None]
+    if a.dtype == "bf16":
+        q, k, v, do = (oracle.bf16_round(x) for x in (q, k, v, do))
+    t0 = time.perf_counter()
+    oracle.mha_bwd(q, k, v, do, 1, nheads, nheads, N, d, bool(a.causal), nthreads=threads, lib=lib)
+    dt = time.perf_counter() - t0
+    import mx230_amd as mx
+    flops = mx.bwd_flops(1, nheads, N, d, bool(a.causal))
+    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": threads,
+            "sample": f"backward of {nheads} (batch, head) slices at N={N}, d={d}, {threads} threads; {dt:.1f} s"}
 
 
 def cpu_baseline(a, hkv):
@@ -105,6 +223,9 @@ def main():
     a = parse()
     if a.copy_probe:
         copy_probe(a.copy_probe)
+        return
+    if a.naive_table:
+        naive_table()
         return
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {a.gpus}); the path shards "
@@ -244,6 +365,8 @@ def main():
         res["roofline"]["hbm_measured_gbps"] = round(mx.probe_hbm_gbps(mib=1024), 1)
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline(a, hkv)
+        res["cpu_baseline"]["parallel"] = cpu_parallel(a, hkv)
+        res["cpu_baseline"]["host"] = cpu_host()
     print(json.dumps(res), flush=True)
 
 
