@@ -77,12 +77,12 @@ __global__ __launch_bounds__(256) void preprocess_kernel(const T *dout, const T 
 // and their LSE and Delta, into LDS buffers.
 template <class Pol, int NT = 256>
 __device__ __forceinline__ void stage_qdo(typename Pol::T *sq, typename Pol::T *sdo, float *sl, float *sd,
-                                          const Params &p, size_t bh, int qs, int N, int tid, int wave,
-                                          int lane) {
+                                          const Params &p, size_t bh, int qs, int N, const RowPlan<Pol, NT> &pl,
+                                          int wave, int lane) {
     using T = typename Pol::T;
     const size_t off = (bh * N + qs) * Pol::D;
-    stage_rows<Pol, NT>(sq, static_cast<const T *>(p.q) + off, N - qs, tid, wave);
-    stage_rows<Pol, NT>(sdo, static_cast<const T *>(p.dout) + off, N - qs, tid, wave);
+    stage_rows<Pol, NT>(sq, static_cast<const T *>(p.q) + off, N - qs, pl, wave);
+    stage_rows<Pol, NT>(sdo, static_cast<const T *>(p.dout) + off, N - qs, pl, wave);
     // rows past N: LSE = +inf makes their p (and so dS) exactly 0
     if (wave == 0) stage_vec64(sl, p.lse + bh * N + qs, N - qs, lane, &kPosInf);
     if (wave == 1) stage_vec64(sd, p.delta + bh * N + qs, N - qs, lane, p.delta + bh * N + qs);
@@ -217,7 +217,8 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDq * 4 / NW) void dq_kernel(Par
     const int kend = CAUSAL ? min(N, qb * BQ + BQ) : N;
     const int nsteps = (kend + BK - 1) / BK;
 
-    stage_kv<Pol, NT>(sK[0], sV[0], K, V, 0, N, tid, wave);
+    const RowPlan<Pol, NT> plan(tid);
+    stage_kv<Pol, NT>(sK[0], sV[0], K, V, 0, N, plan, wave);
     wait_stage();
     __syncthreads();
 
@@ -228,7 +229,7 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDq * 4 / NW) void dq_kernel(Par
     // offsets; the last two stages choose their buffer and masking at run time.
     auto main_stage = [&](auto buf, int st) __attribute__((always_inline)) {
         constexpr int B = decltype(buf)::value;
-        if (st + 1 < nsteps) stage_kv<Pol, NT>(sK[B ^ 1], sV[B ^ 1], K, V, (st + 1) * BK, N, tid, wave);
+        if (st + 1 < nsteps) stage_kv<Pol, NT>(sK[B ^ 1], sV[B ^ 1], K, V, (st + 1) * BK, N, plan, wave);
         dq_stage<Pol, CAUSAL, false>(acc, qf, dof, nL2, Dl, sK[B], sV[B], st * BK, q0, N, g, l16);
         wait_stage();
         __syncthreads();
@@ -242,7 +243,7 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDq * 4 / NW) void dq_kernel(Par
     if (st < nmain) main_stage(std::integral_constant<int, 0>{}, st++);
     for (; st < nsteps; ++st) {
         const int cur = st & 1;
-        if (st + 1 < nsteps) stage_kv<Pol, NT>(sK[cur ^ 1], sV[cur ^ 1], K, V, (st + 1) * BK, N, tid, wave);
+        if (st + 1 < nsteps) stage_kv<Pol, NT>(sK[cur ^ 1], sV[cur ^ 1], K, V, (st + 1) * BK, N, plan, wave);
         const int k0 = st * BK;
         // one (masked) body for these stages: a second, unmasked body behind a
         // branch makes the register allocator spill at three waves per SIMD
@@ -507,10 +508,11 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDkv * 4 / NW) void dkv_kernel(P
 
     // Stages are loaded strictly in order; (ld_h, ld_i) = query head and stage
     // within it of the next one (kept incrementally: no division per stage).
+    const RowPlan<Pol, NT> plan(tid);
     int ld_h = 0, ld_i = 0;
     auto issue = [&](int st) __attribute__((always_inline)) {
         const int bf = st % NBUF;
-        stage_qdo<Pol, NT>(sQ[bf], sdO[bf], sL[bf], sD[bf], p, bh0 + ld_h, qstart + ld_i * BQ, N, tid, wave, lane);
+        stage_qdo<Pol, NT>(sQ[bf], sdO[bf], sL[bf], sD[bf], p, bh0 + ld_h, qstart + ld_i * BQ, N, plan, wave, lane);
         if (++ld_i == nqs) {
             ld_i = 0;
             ++ld_h;

@@ -369,6 +369,53 @@ __device__ __forceinline__ void stage_rows(typename Pol::T *tile, const typename
     }
 }
 
+// The same load with the global address split into a wave-uniform base (an
+// SGPR pair) and a 32-bit per-lane byte offset: the instruction's saddr form.
+__device__ __forceinline__ void lds_dma16_s(uint32_t base, const void *sbase, uint32_t voff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    uint32_t save;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+        : "=&s"(save)
+        : "v"(voff), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(base)));
+#endif
+}
+
+// Where each of a thread's staging loads of a tile reads from: load k fills
+// 16-byte position P = k NT + tid of the tile, which holds chunk c of row r
+// (Pol::chunk_at). Computed once per kernel and kept packed in one register
+// per load (r in bits 0-7, the chunk's byte offset within the row above), so
+// a stage's loads cost a few VALU operations each instead of the layout
+// arithmetic.
+template <class Pol, int NT = 256>
+struct RowPlan {
+    static constexpr int NK = Pol::ROWS * (Pol::D / Pol::EPC) / NT;
+    static_assert(NK * NT == Pol::ROWS * (Pol::D / Pol::EPC), "whole wave-wide loads");
+    uint32_t rc[NK];
+    __device__ explicit RowPlan(int tid) {
+#pragma unroll
+        for (int k = 0; k < NK; ++k) {
+            int row, c;
+            Pol::chunk_at(k * NT + tid, row, c);
+            rc[k] = (uint32_t)row | ((uint32_t)(c * 16) << 8);
+        }
+    }
+};
+
+// stage_rows with a RowPlan: rows >= nvalid re-read row nvalid - 1, as there.
+template <class Pol, int NT = 256>
+__device__ __forceinline__ void stage_rows(typename Pol::T *tile, const typename Pol::T *src, int nvalid,
+                                           const RowPlan<Pol, NT> &pl, int wave, int row_stride = Pol::D) {
+    const uint32_t base = lds_addr(tile) + wave * 64 * 16;
+    const uint32_t rs_bytes = (uint32_t)row_stride * sizeof(typename Pol::T);
+#pragma unroll
+    for (int k = 0; k < RowPlan<Pol, NT>::NK; ++k) {
+        const uint32_t grow = (uint32_t)min((int)(pl.rc[k] & 255u), nvalid - 1);
+        lds_dma16_s(base + k * NT * 16, src, grow * rs_bytes + (pl.rc[k] >> 8));
+    }
+}
+
 // One K/V stage: Pol::ROWS key rows from k0 of K and V (rows row_stride
 // elements apart) into LDS buffers.
 template <class Pol, int NT = 256>
@@ -377,6 +424,13 @@ __device__ __forceinline__ void stage_kv(typename Pol::T *sk, typename Pol::T *s
                                          int row_stride = Pol::D) {
     stage_rows<Pol, NT>(sk, K + (size_t)k0 * row_stride, N - k0, tid, wave, row_stride);
     stage_rows<Pol, NT>(sv, V + (size_t)k0 * row_stride, N - k0, tid, wave, row_stride);
+}
+template <class Pol, int NT = 256>
+__device__ __forceinline__ void stage_kv(typename Pol::T *sk, typename Pol::T *sv, const typename Pol::T *K,
+                                         const typename Pol::T *V, int k0, int N, const RowPlan<Pol, NT> &pl,
+                                         int wave, int row_stride = Pol::D) {
+    stage_rows<Pol, NT>(sk, K + (size_t)k0 * row_stride, N - k0, pl, wave, row_stride);
+    stage_rows<Pol, NT>(sv, V + (size_t)k0 * row_stride, N - k0, pl, wave, row_stride);
 }
 
 // Read by lanes past the end of a staged vector (see stage_vec64).

@@ -144,7 +144,8 @@ __global__ __launch_bounds__(256, Pol::kWaves) void fwd_kernel(Params p) {
     const int kend = CAUSAL ? min(Nk, pos0 + qb * BQ + BQ) : Nk;
     const int nsteps = (kend + BK - 1) / BK;
 
-    stage_kv<Pol>(sK[0], sV[0], K, V, 0, Nk, tid, wave, p.kv_rs);
+    const RowPlan<Pol> plan(tid);
+    stage_kv<Pol>(sK[0], sV[0], K, V, 0, Nk, plan, wave, p.kv_rs);
     wait_stage();
     __syncthreads();
 
@@ -154,7 +155,7 @@ __global__ __launch_bounds__(256, Pol::kWaves) void fwd_kernel(Params p) {
     // immediate offsets; the rest choose buffer and masking at run time.
     auto main_stage = [&](auto buf, int st) __attribute__((always_inline)) {
         constexpr int B = decltype(buf)::value;
-        if (st + 1 < nsteps) stage_kv<Pol>(sK[B ^ 1], sV[B ^ 1], K, V, (st + 1) * BK, Nk, tid, wave, p.kv_rs);
+        if (st + 1 < nsteps) stage_kv<Pol>(sK[B ^ 1], sV[B ^ 1], K, V, (st + 1) * BK, Nk, plan, wave, p.kv_rs);
         fwd_stage<Pol, CAUSAL, false>(acc, m, lsum, qf, sK[B], sV[B], st * BK, qpos0, Nk, g, l16);
         wait_stage();
         __syncthreads();
@@ -168,7 +169,7 @@ __global__ __launch_bounds__(256, Pol::kWaves) void fwd_kernel(Params p) {
     if (st < nmain) main_stage(std::integral_constant<int, 0>{}, st++);
     for (; st < nsteps; ++st) {
         const int cur = st & 1;
-        if (st + 1 < nsteps) stage_kv<Pol>(sK[cur ^ 1], sV[cur ^ 1], K, V, (st + 1) * BK, Nk, tid, wave, p.kv_rs);
+        if (st + 1 < nsteps) stage_kv<Pol>(sK[cur ^ 1], sV[cur ^ 1], K, V, (st + 1) * BK, Nk, plan, wave, p.kv_rs);
         const int k0 = st * BK;
         // a wave whose queries all precede the stage's keys has nothing to do
         if (!CAUSAL || k0 <= qpos0 + 31) {
