@@ -11,9 +11,9 @@
 // Two atomic-free passes, as in attention_bwd.cu:96-243, re-tiled for CDNA4:
 //   * dkv_kernel: a workgroup owns 64*KT keys of one (batch, KV head); each of
 //     its 4 waves owns 16*KT keys whose K/V rows sit in registers and whose
-//     dK/dV accumulate in registers. Q/dO/LSE/Delta stream through
-//     double-buffered LDS (direct global->LDS loads issued one stage ahead),
-//     64 queries per stage, for every query head of the
+//     dK/dV accumulate in registers (bf16, d = 64: three work-groups per CU).
+//     Q/dO/LSE/Delta stream through double-buffered LDS (direct global->LDS
+//     loads issued one stage ahead), 64 queries per stage, for every query head of the
 //     KV head's group in turn, so the grouped-query reduction of dK/dV happens
 //     inside the kernel with no atomics and no extra memory.
 //   * dq_kernel: a workgroup owns 128 queries of one (batch, query head) (32
@@ -873,11 +873,11 @@ hipError_t launch_bwd_dq(const Params &p, int dtype_bf16, int d, int causal, int
 }
 
 // The ping-pong dK/dV kernel is opt-in (MXFA_DKV_KERNEL=pingpong, read on
-// every call): at B=4, H=12, N=4096, d=64 causal it runs 0.29-0.30 ms against
-// 0.24 ms for the 4-wave kernel, because its softmax-phase waves stall on
-// issuing the global->LDS loads (which the 4-wave kernel hides behind the
-// second workgroup on each SIMD); its MFMA phase alone runs near the
-// matrix-core rate.
+// every call): at B=4, H=12, N=4096, d=64 causal it ran 0.29-0.30 ms against
+// 0.24 ms for the 4-wave kernel of the time (now ~0.19 ms at three waves per
+// SIMD), because its softmax-phase waves stall on issuing the global->LDS
+// loads (which the 4-wave kernel hides behind the other work-groups on each
+// SIMD); its MFMA phase alone runs near the matrix-core rate.
 static bool dkv_pingpong_selected() {
     const char *e = std::getenv("MXFA_DKV_KERNEL");
     return e != nullptr && std::strcmp(e, "pingpong") == 0;
