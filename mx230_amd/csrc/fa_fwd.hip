@@ -13,6 +13,8 @@
 //   * the output is accumulated transposed, O^T = V^T P^T, so the per-query
 //     rescale factor is a per-lane scalar as well;
 //   * exponentials are base 2 with log2(e) folded into the scale;
+//   * after the first stage the running max is only raised (and O and the sum
+//     rescaled) when a score exceeds it by a factor above 2^8 (fwd_stage_lazy);
 //   * only stages that straddle the causal diagonal or the end of the sequence
 //     run the masking code (a separate instantiation of the stage body).
 #include <type_traits>
@@ -102,6 +104,122 @@ __device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][2], float (&
     }
 }
 
+// fwd_stage for every stage after the first, with lazy rescaling. Key 0 is
+// visible to every query (pos0 >= 0), so after the first stage m is finite for
+// every row. The scores come out of the MFMAs relative to the running max (the
+// accumulators start at -m), and m, O and the sum are only rescaled when some
+// score of the wave exceeds its row's m by more than kLazy (log2 units).
+// Otherwise p = 2^(s - m) with the old m, so p <= 2^kLazy: m never exceeds the
+// row's true running max and never falls more than kLazy below it, so the
+// largest p of each row lies in [1, 2^kLazy] and neither it nor the fp32 sum
+// can overflow or underflow. The result is the online softmax's up to
+// rounding, since LSE = m + log2(l) holds for any m used consistently.
+constexpr float kLazy = 8.0f;
+
+template <class Pol, bool CAUSAL, bool MASK>
+__device__ __forceinline__ void fwd_stage_lazy(f32x4 (&acc)[Pol::D / 16][2], float (&m)[2], float (&lsum)[2],
+                                               const typename Pol::Frag (&qf)[2][Pol::NC],
+                                               const typename Pol::T *sk, const typename Pol::T *sv, int k0,
+                                               int qpos0, int Nk, int g, int l16) {
+    using Frag = typename Pol::Frag;
+    constexpr int NC = Pol::NC, XT = Pol::D / 16;
+    f32x4 s[2][2][2];  // [block][t][qt]
+    const f32x4 nm[2] = {f32x4{-m[0], -m[0], -m[0], -m[0]}, f32x4{-m[1], -m[1], -m[1], -m[1]}};
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            Frag a[NC];
+            Pol::lds_row_frags(a, sk, 32 * blk + Pol::arow(t, l16), g);
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) {
+                f32x4 c = nm[qt];
+#pragma unroll
+                for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], qf[qt][kc], c);
+                s[blk][t][qt] = c;
+            }
+        }
+    }
+    float mx[2];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        const int qpos = qpos0 + 16 * qt + l16;
+        float v = -INFINITY;
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float x = s[blk][t][qt][r];
+                    if constexpr (MASK) {
+                        const int key = k0 + 32 * blk + Pol::bidx(t, g, r);
+                        x = (key >= Nk || (CAUSAL && key > qpos)) ? -INFINITY : x;
+                        s[blk][t][qt][r] = x;
+                    }
+                    v = fmaxf(v, x);
+                }
+            }
+        }
+        mx[qt] = xg_max(v);
+    }
+    if (__builtin_amdgcn_ballot_w64(mx[0] > kLazy || mx[1] > kLazy) != 0) {
+        // some row of the wave moved up by more than kLazy: rescale (rows whose
+        // max did not rise keep shift 0)
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+            const float shift = fmaxf(mx[qt], 0.f);
+            const float corr = fast_exp2(-shift);
+            m[qt] += shift;
+#pragma unroll
+            for (int xt = 0; xt < XT; ++xt) acc[xt][qt] *= corr;
+            float ls = lsum[qt] * corr;
+#pragma unroll
+            for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float pv = fast_exp2(s[blk][t][qt][r] - shift);
+                        s[blk][t][qt][r] = pv;
+                        ls += pv;
+                    }
+                }
+            }
+            lsum[qt] = ls;
+        }
+    } else {
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+            float ls = lsum[qt];
+#pragma unroll
+            for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float pv = fast_exp2(s[blk][t][qt][r]);
+                        s[blk][t][qt][r] = pv;
+                        ls += pv;
+                    }
+                }
+            }
+            lsum[qt] = ls;
+        }
+    }
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+        typename Pol::ChainB cb[2];
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) cb[qt] = Pol::pack(s[blk][0][qt], s[blk][1][qt]);
+#pragma unroll
+        for (int xt = 0; xt < XT; ++xt) {
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) acc[xt][qt] = Pol::chain(acc[xt][qt], cb[qt], sv, 16 * xt, 32 * blk, g, l16);
+        }
+    }
+}
+
 template <class Pol, bool CAUSAL>
 __global__ __launch_bounds__(256, Pol::kWaves) void fwd_kernel(Params p) {
     using T = typename Pol::T;
@@ -153,31 +271,41 @@ __global__ __launch_bounds__(256, Pol::kWaves) void fwd_kernel(Params p) {
     // workgroup's first query position) run in pairs with the LDS buffer a
     // compile-time constant, so the tile addresses fold into the instructions'
     // immediate offsets; the rest choose buffer and masking at run time.
-    auto main_stage = [&](auto buf, int st) __attribute__((always_inline)) {
+    // The first stage runs the plain online-softmax body (the running max
+    // starts at -inf); later ones the lazy-rescaling body.
+    auto main_stage = [&](auto buf, auto first, int st) __attribute__((always_inline)) {
         constexpr int B = decltype(buf)::value;
         if (st + 1 < nsteps) stage_kv<Pol>(sK[B ^ 1], sV[B ^ 1], K, V, (st + 1) * BK, Nk, plan, wave, p.kv_rs);
-        fwd_stage<Pol, CAUSAL, false>(acc, m, lsum, qf, sK[B], sV[B], st * BK, qpos0, Nk, g, l16);
+        if constexpr (decltype(first)::value) {
+            fwd_stage<Pol, CAUSAL, false>(acc, m, lsum, qf, sK[B], sV[B], st * BK, qpos0, Nk, g, l16);
+        } else {
+            fwd_stage_lazy<Pol, CAUSAL, false>(acc, m, lsum, qf, sK[B], sV[B], st * BK, qpos0, Nk, g, l16);
+        }
         wait_stage();
         __syncthreads();
     };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
     const int nmain = min(min(nsteps, Nk / BK), CAUSAL ? (pos0 + qb * BQ + 1) / BK : nsteps);
     int st = 0;
+    if (nmain > 0) main_stage(B0{}, std::true_type{}, st++);
     for (; st + 1 < nmain; st += 2) {
-        main_stage(std::integral_constant<int, 0>{}, st);
-        main_stage(std::integral_constant<int, 1>{}, st + 1);
+        main_stage(B1{}, std::false_type{}, st);
+        main_stage(B0{}, std::false_type{}, st + 1);
     }
-    if (st < nmain) main_stage(std::integral_constant<int, 0>{}, st++);
+    if (st < nmain) main_stage(B1{}, std::false_type{}, st++);
+    // the remaining stages may straddle the diagonal or the end of the keys:
+    // one masked body each for the first stage and the later ones
     for (; st < nsteps; ++st) {
         const int cur = st & 1;
         if (st + 1 < nsteps) stage_kv<Pol>(sK[cur ^ 1], sV[cur ^ 1], K, V, (st + 1) * BK, Nk, plan, wave, p.kv_rs);
         const int k0 = st * BK;
         // a wave whose queries all precede the stage's keys has nothing to do
         if (!CAUSAL || k0 <= qpos0 + 31) {
-            const bool need_mask = (k0 + BK > Nk) || (CAUSAL && k0 + BK - 1 > qpos0);
-            if (need_mask) {
+            if (st == 0) {
                 fwd_stage<Pol, CAUSAL, true>(acc, m, lsum, qf, sK[cur], sV[cur], k0, qpos0, Nk, g, l16);
             } else {
-                fwd_stage<Pol, CAUSAL, false>(acc, m, lsum, qf, sK[cur], sV[cur], k0, qpos0, Nk, g, l16);
+                fwd_stage_lazy<Pol, CAUSAL, true>(acc, m, lsum, qf, sK[cur], sV[cur], k0, qpos0, Nk, g, l16);
             }
         }
         wait_stage();
