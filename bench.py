@@ -55,6 +55,8 @@ def parse():
     ap.add_argument("--naive-table", action="store_true",
                     help="instead of the benchmark, time the naive and flash paths on the reference's own "
                          "tables (one fp32 head, d = 64) and print them as one JSON line")
+    ap.add_argument("--config-table", action="store_true",
+                    help="forward and backward timings at every BASELINE config (one JSON line)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run a plain device-to-device copy of MIB "
                          "MiB three times (calibrates the FETCH_SIZE / WRITE_SIZE counters)")
@@ -150,6 +152,74 @@ def naive_table():
                       "timing": "median of 5 after 1 warm-up, HIP events on the launch stream"}), flush=True)
 
 
+# (name, B, Hq, Hkv, N, d, causal, dtype, Q/K/V scale)
+CONFIGS = [
+    ("cfg1 reference CPU case", 1, 1, 1, 256, 64, False, "f32", 1.0),
+    ("cfg2 GPT-2", 4, 12, 12, 1024, 64, True, "f32", 0.5),
+    ("cfg3 long sequence", 1, 12, 12, 32768, 64, False, "f32", 1.0),
+    ("cfg3 long sequence", 1, 12, 12, 32768, 64, False, "bf16", 1.0),
+    ("cfg4 Qwen2.5 GQA 7:1", 2, 14, 2, 4096, 64, True, "bf16", 1.0),
+    ("cfg5 TinyLlama GQA 8:1", 1, 32, 4, 2048, 64, True, "bf16", 0.5),
+    ("cfg5 TinyLlama GQA 8:1", 1, 32, 4, 2048, 128, True, "bf16", 0.5),
+    ("north star", 4, 12, 12, 4096, 64, True, "bf16", 1.0),
+]
+
+
+def config_table():
+    """Forward (mxfa_run_flash_lse) and backward from O (mxfa_run_bwd_ws: the
+    dQ pass with Delta, then dK/dV, split over the query heads of a GQA group
+    through its workspace where that applies) at every BASELINE config, each the median of
+    20 event-timed runs after 3 warm-ups, inputs resident. TFLOP/s are the
+    algorithmic 4 N^2 d (forward) and 10 N^2 d (backward) per (batch, query
+    head), halved when causal; % peak against the dense MFMA peak of the dtype."""
+    import torch
+    import mx230_amd as mx
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    mx.init(0)
+    stream = torch.cuda.current_stream()
+
+    def median_ms(fn, reps=20):
+        for _ in range(3):
+            fn()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for e0, e1 in evs:
+            e0.record(stream)
+            fn()
+            e1.record(stream)
+        torch.cuda.synchronize()
+        return sorted(e0.elapsed_time(e1) for e0, e1 in evs)[reps // 2]
+
+    rows = []
+    for name, B, H, Hkv, N, d, causal, dtype, sc in CONFIGS:
+        dt = torch.bfloat16 if dtype == "bf16" else torch.float32
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(N + H + d)
+        qs, ks = (B, H, N, d), (B, Hkv, N, d)
+        q, k, v = (torch.randn(s, generator=gen, device=dev).mul_(sc).to(dt) for s in (qs, ks, ks))
+        do = torch.randn(qs, generator=gen, device=dev).to(dt)
+        o = torch.empty_like(q)
+        lse = torch.empty((B, H, N), device=dev)
+        delta = torch.empty_like(lse)
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        fwd = median_ms(lambda: mx.run_flash_lse(q, k, v, o, lse, causal))
+        nws = mx.bwd_workspace_bytes(q, k, causal)
+        ws = torch.empty(nws, dtype=torch.uint8, device=dev) if nws else None
+        bwd = median_ms(lambda: mx.run_bwd_ws(q, k, v, o, do, lse, delta, dq, dk, dv, ws, causal))
+        peak = PEAK_TFLOPS[dtype]
+        ftf = mx.fwd_flops(B, H, N, d, causal) / (fwd * 1e-3) / 1e12
+        btf = mx.bwd_flops(B, H, N, d, causal) / (bwd * 1e-3) / 1e12
+        rows.append({"config": name, "B": B, "Hq": H, "Hkv": Hkv, "N": N, "d": d, "causal": causal,
+                     "dtype": dtype, "workspace_mb": round(nws / 1e6, 1), "fwd_ms": round(fwd, 4), "fwd_tflops": round(ftf, 2),
+                     "fwd_pct_peak": round(100 * ftf / peak, 1), "bwd_ms": round(bwd, 4),
+                     "bwd_tflops": round(btf, 2), "bwd_pct_peak": round(100 * btf / peak, 1)})
+        print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+        del q, k, v, do, o, lse, delta, dq, dk, dv, ws
+    print(json.dumps({"config_table": rows, "peak_tflops": PEAK_TFLOPS,
+                      "data": "synthetic (seeded N(0,1) on the GPU; Q/K/V x0.5 where BASELINE says so)",
+                      "timing": "median of 20 after 3 warm-ups, HIP events on the launch stream"}), flush=True)
+
+
 def cpu_host():
     model = "unknown"
     try:
@@ -226,6 +296,9 @@ def main():
         return
     if a.naive_table:
         naive_table()
+        return
+    if a.config_table:
+        config_table()
         return
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {a.gpus}); the path shards "

@@ -46,7 +46,8 @@ typedef enum {
     MXFA_ERR_UNSUPPORTED = -4, /* valid shape, but no kernel (e.g. d not in {64, 128}) */
     MXFA_ERR_ALIGN = -5,       /* a device pointer is not 16-byte aligned */
     MXFA_ERR_LAUNCH = -6,      /* the HIP runtime rejected a launch */
-    MXFA_ERR_DEVICE = -7       /* no usable gfx950 device */
+    MXFA_ERR_DEVICE = -7,      /* no usable gfx950 device */
+    MXFA_ERR_WORKSPACE = -8    /* a workspace smaller than mxfa_bwd_workspace_bytes(shape) */
 } mxfa_status;
 
 typedef enum { MXFA_F32 = 0, MXFA_BF16 = 1 } mxfa_dtype;
@@ -137,9 +138,37 @@ int mxfa_run_bwd(const mxfa_shape *shape, const void *q, const void *k, const vo
                  const void *dout, const float *lse, float *delta, void *dq, void *dk, void *dv,
                  void *stream);
 
-/* Bytes of device workspace the backward needs beyond its inputs and
- * outputs: always 0 (dQ is a separate atomic-free pass). */
+/* Bytes of device workspace the _ws entry points below can use (0 for an
+ * invalid shape). dQ is a separate atomic-free pass and needs none. With GQA
+ * (Hq > Hkv), when the key blocks alone would leave the GPU underfilled, the
+ * dK/dV pass splits each group's query heads over several work-groups per key
+ * block: each writes fp32 partial dK/dV sums to the workspace and a second
+ * launch adds them in a fixed order (deterministic, atomic-free). The size is
+ * 2 * split * B * Hkv * N * d * 4 bytes, where split divides Hq / Hkv; 0 when
+ * no split helps (always without GQA).
+ * The reference has no GQA (d = 64, one head, attention_bwd.cu:165-243); this
+ * sizes the scratch of its dK/dV pass generalised to GQA groups. */
 size_t mxfa_bwd_workspace_bytes(const mxfa_shape *shape);
+
+/* mxfa_run_bwd_dkv with a caller-owned workspace (16-byte aligned, at least
+ * mxfa_bwd_workspace_bytes(shape) bytes, else MXFA_ERR_ALIGN or
+ * MXFA_ERR_WORKSPACE). workspace == NULL is allowed and runs the unsplit pass
+ * (= mxfa_run_bwd_dkv). Results equal the unsplit pass's up to the summation
+ * order over the query heads of a group; the workspace holds nothing the
+ * caller needs afterwards.
+ * Replaces the attn_bwd_dkv launch (attention_bwd.cu:165-243, main.rs:206-209)
+ * for GQA shapes. */
+int mxfa_run_bwd_dkv_ws(const mxfa_shape *shape, const void *q, const void *k, const void *v,
+                        const void *dout, const float *lse, const float *delta, void *dk,
+                        void *dv, void *workspace, size_t workspace_bytes, void *stream);
+
+/* mxfa_run_bwd with a caller-owned workspace for its dK/dV pass (as
+ * mxfa_run_bwd_dkv_ws; NULL = mxfa_run_bwd).
+ * Replaces run_preprocess + run_bwd_flash (main.rs:126-143, :179-210) as
+ * mxfa_run_bwd does. */
+int mxfa_run_bwd_ws(const mxfa_shape *shape, const void *q, const void *k, const void *v, const void *o,
+                    const void *dout, const float *lse, float *delta, void *dq, void *dk, void *dv,
+                    void *workspace, size_t workspace_bytes, void *stream);
 
 /* Naive backward baseline: one thread per query row, dK/dV scattered with
  * atomic adds. fp32 only. dQ, dK, dV MUST be zeroed by the caller.

@@ -37,13 +37,15 @@ STATUS = {
     -5: "MXFA_ERR_ALIGN",
     -6: "MXFA_ERR_LAUNCH",
     -7: "MXFA_ERR_DEVICE",
+    -8: "MXFA_ERR_WORKSPACE",
 }
 
 # Every symbol include/mxfa.h declares (the tests check the library exports them).
 EXPORTS = (
     "mxfa_version", "mxfa_strerror", "mxfa_init", "mxfa_shutdown", "mxfa_check_shape",
     "mxfa_run_flash", "mxfa_run_flash_lse", "mxfa_run_preprocess", "mxfa_run_bwd_dq",
-    "mxfa_run_bwd_dkv", "mxfa_run_bwd_flash", "mxfa_run_bwd_dq_delta", "mxfa_run_bwd", "mxfa_bwd_workspace_bytes", "mxfa_run_bwd_naive",
+    "mxfa_run_bwd_dkv", "mxfa_run_bwd_flash", "mxfa_run_bwd_dq_delta", "mxfa_run_bwd", "mxfa_bwd_workspace_bytes",
+    "mxfa_run_bwd_dkv_ws", "mxfa_run_bwd_ws", "mxfa_run_bwd_naive",
     "mxfa_naive_scratch_bytes", "mxfa_run_naive_fwd", "mxfa_check_prefill", "mxfa_run_prefill",
     "mxfa_probe_sink_len", "mxfa_probe_mfma", "mxfa_probe_read", "mxfa_probe_copy",
 )
@@ -107,6 +109,8 @@ def load_library(path: str | None = None):
     lib.mxfa_run_bwd_naive.argtypes = [sp, vp, vp, vp, vp, fp, fp, vp, vp, vp, vp]
     lib.mxfa_bwd_workspace_bytes.argtypes = [sp]
     lib.mxfa_bwd_workspace_bytes.restype = ctypes.c_size_t
+    lib.mxfa_run_bwd_dkv_ws.argtypes = [sp, vp, vp, vp, vp, fp, fp, vp, vp, vp, ctypes.c_size_t, vp]
+    lib.mxfa_run_bwd_ws.argtypes = [sp, vp, vp, vp, vp, vp, fp, fp, vp, vp, vp, vp, ctypes.c_size_t, vp]
     lib.mxfa_naive_scratch_bytes.argtypes = [sp]
     lib.mxfa_naive_scratch_bytes.restype = ctypes.c_size_t
     lib.mxfa_run_naive_fwd.argtypes = [sp, vp, vp, vp, fp, vp, vp]
@@ -276,6 +280,37 @@ def run_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, causal: bool, scale: float =
     _check("mxfa_run_bwd", load_library().mxfa_run_bwd(ctypes.byref(sh.c()), *args, _stream(stream)))
 
 
+def bwd_workspace_bytes(q, k, causal: bool) -> int:
+    """Bytes of workspace run_bwd_ws / run_bwd_dkv_ws can use for this shape
+    (mxfa_bwd_workspace_bytes): nonzero only for GQA shapes whose dK/dV pass
+    splits each group's query heads over several work-groups."""
+    sh = shape_of(q, k, causal)
+    return int(load_library().mxfa_bwd_workspace_bytes(ctypes.byref(sh.c())))
+
+
+def _ws_args(workspace):
+    if workspace is None:
+        return [None, 0]
+    torch = _torch()
+    if workspace.device.type != "cuda" or not workspace.is_contiguous():
+        raise ValueError("workspace: must be a contiguous device tensor")
+    return [ctypes.c_void_p(workspace.data_ptr()), workspace.numel() * workspace.element_size()]
+
+
+def run_bwd_ws(q, k, v, o, do, lse, delta, dq, dk, dv, workspace, causal: bool, scale: float = 0.0,
+               stream=None):
+    """run_bwd with a workspace (a device tensor of at least
+    bwd_workspace_bytes(q, k, causal) bytes, or None) for the split dK/dV pass
+    of GQA shapes (mxfa_run_bwd_ws)."""
+    sh = shape_of(q, k, causal, scale)
+    dt, qs, ks = _io(sh)
+    args = [_expect(q, "q", qs, dt), _expect(k, "k", ks, dt), _expect(v, "v", ks, dt), _expect(o, "o", qs, dt),
+            _expect(do, "do", qs, dt), _vec_ptr(lse, "lse", sh), _vec_ptr(delta, "delta", sh),
+            _expect(dq, "dq", qs, dt), _expect(dk, "dk", ks, dt), _expect(dv, "dv", ks, dt)]
+    args += _ws_args(workspace)
+    _check("mxfa_run_bwd_ws", load_library().mxfa_run_bwd_ws(ctypes.byref(sh.c()), *args, _stream(stream)))
+
+
 def run_bwd_dq_delta(q, k, v, o, do, lse, delta, dq, causal: bool, scale: float = 0.0, stream=None):
     """dQ pass that computes Delta from O itself and writes it to ``delta``."""
     sh = shape_of(q, k, causal, scale)
@@ -300,6 +335,15 @@ def run_bwd_dkv(q, k, v, do, lse, delta, dk, dv, causal: bool, scale: float = 0.
     args += [_expect(dk, "dk", ks, dt), _expect(dv, "dv", ks, dt)]
     _check("mxfa_run_bwd_dkv",
            load_library().mxfa_run_bwd_dkv(ctypes.byref(sh.c()), *args, _stream(stream)))
+
+
+def run_bwd_dkv_ws(q, k, v, do, lse, delta, dk, dv, workspace, causal: bool, scale: float = 0.0,
+                   stream=None):
+    """dK/dV pass with a workspace for the split GQA form (mxfa_run_bwd_dkv_ws)."""
+    sh, dt, qs, ks, args = _bwd_args(q, k, v, do, lse, delta, causal, scale)
+    args += [_expect(dk, "dk", ks, dt), _expect(dv, "dv", ks, dt)] + _ws_args(workspace)
+    _check("mxfa_run_bwd_dkv_ws",
+           load_library().mxfa_run_bwd_dkv_ws(ctypes.byref(sh.c()), *args, _stream(stream)))
 
 
 def run_bwd_naive(q, k, v, do, lse, delta, dq, dk, dv, causal: bool, scale: float = 0.0,
@@ -387,13 +431,16 @@ def attention_fwd(q, k, v, causal: bool, scale: float = 0.0, stream=None):
 
 
 def attention_bwd(q, k, v, o, lse, do, causal: bool, scale: float = 0.0, stream=None):
-    """Allocates Delta, dQ, dK, dV and runs the backward (run_bwd: Delta folded
-    into the dQ pass); returns (dQ, dK, dV)."""
+    """Allocates Delta, dQ, dK, dV (and, for GQA shapes that use one, the dK/dV
+    workspace) and runs the backward (run_bwd_ws: Delta folded into the dQ
+    pass); returns (dQ, dK, dV)."""
     torch = _torch()
     sh = shape_of(q, k, causal, scale)
     delta = torch.empty((sh.B, sh.Hq, sh.N), dtype=torch.float32, device=q.device)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    run_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, causal, scale, stream)
+    nws = bwd_workspace_bytes(q, k, causal)
+    ws = torch.empty(nws, dtype=torch.uint8, device=q.device) if nws else None
+    run_bwd_ws(q, k, v, o, do, lse, delta, dq, dk, dv, ws, causal, scale, stream)
     return dq, dk, dv
 
 

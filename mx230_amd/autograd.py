@@ -1,10 +1,11 @@
 """Training-step wrapper: the flash-attention path as a ``torch.autograd.Function``.
 
 The forward calls ``mxfa_run_flash_lse`` and saves Q, K, V, O and LSE; the
-backward calls ``mxfa_run_preprocess`` (Delta = rowsum(dO * O)) and
-``mxfa_run_bwd_flash`` (dQ, dK, dV). This is the sequence the reference drives
-by hand around its kernels (02-flash-attention/src/main.rs:470-511: flash
-forward with LSE, then preprocess, then ``run_bwd_flash``), packaged so a
+backward calls ``mxfa_run_bwd_ws`` (the dQ pass with Delta = rowsum(dO * O)
+folded in, then the dK/dV pass, split over the query heads of a GQA group
+through a workspace where that fills the GPU better). This is the sequence the
+reference drives by hand around its kernels (02-flash-attention/src/main.rs:470-511:
+flash forward with LSE, then preprocess, then ``run_bwd_flash``), packaged so a
 PyTorch-ROCm training step can put it between its QKV and output projections.
 
 Layouts as in the package: Q ``[B, Hq, N, d]``, K/V ``[B, Hkv, N, d]`` (grouped

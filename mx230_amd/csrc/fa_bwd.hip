@@ -20,6 +20,7 @@
 //     per wave, Q/dO rows in registers); K/V stream through LDS 64 keys per
 //     stage. It recomputes S and dP (the price of staying atomic-free and O(N)
 //     in memory).
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 #include <type_traits>
@@ -474,9 +475,12 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDkv * 4 / NW) void dkv_kernel(P
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, l16 = lane & 15;
     const int N = p.N;
-    const int bkv = blockIdx.x;  // b * Hkv + kvh
+    const int nsplit = p.dkv_split;
+    const int bkv = blockIdx.x / nsplit;       // b * Hkv + kvh
+    const int sp = blockIdx.x - bkv * nsplit;  // which share of the group's query heads
     const int kb = blockIdx.y;   // causal: block 0 (most queries) is dispatched first
     const int b = bkv / p.Hkv, kvh = bkv % p.Hkv;
+    const int h0 = sp * p.group / nsplit, nh = (sp + 1) * p.group / nsplit - h0;
     const size_t kvoff = (size_t)bkv * N * D;
     const T *K = static_cast<const T *>(p.k) + kvoff;
     const T *V = static_cast<const T *>(p.v) + kvoff;
@@ -503,8 +507,8 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDkv * 4 / NW) void dkv_kernel(P
 
     const int qstart = CAUSAL ? kb * BKV : 0;
     const int nqs = (N - qstart + BQ - 1) / BQ;  // stages per query head
-    const int nsteps = nqs * p.group;
-    const size_t bh0 = (size_t)b * p.Hq + (size_t)kvh * p.group;
+    const int nsteps = nqs * nh;
+    const size_t bh0 = (size_t)b * p.Hq + (size_t)kvh * p.group + h0;
 
     // Stages are loaded strictly in order; (ld_h, ld_i) = query head and stage
     // within it of the next one (kept incrementally: no division per stage).
@@ -571,7 +575,7 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDkv * 4 / NW) void dkv_kernel(P
     using Buf1 = std::integral_constant<int, 1>;
     // rows past N get p = 0 from LSE = +inf, so only the causal diagonal masks
     const int ndiag = CAUSAL ? min(nqs, BKV / BQ) : 0;
-    for (int hh = 0, st = 0; hh < p.group; ++hh) {
+    for (int hh = 0, st = 0; hh < nh; ++hh) {
         for (int i = 0; i < ndiag; ++i, ++st) run(std::true_type{}, st, i);
         if constexpr (NBUF == 2) {
             int i = ndiag;
@@ -586,6 +590,25 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDkv * 4 / NW) void dkv_kernel(P
         }
     }
 
+    if (nsplit > 1) {
+        // this share's fp32 partial sums (unscaled); dkv_reduce_kernel adds
+        // the shares and applies the scale
+        const size_t plane = (size_t)p.B * p.Hkv * N * D;
+        float *wK = p.dkv_ws + (size_t)sp * plane + kvoff;
+        float *wV = wK + (size_t)nsplit * plane;
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) {
+            const int key = kw0 + 16 * kt + l16;
+            if (key < N) {
+#pragma unroll
+                for (int xt = 0; xt < XT; ++xt) {
+                    store4<float>(wK + (size_t)key * D + 16 * xt + 4 * g, accK[xt][kt], 1.0f);
+                    store4<float>(wV + (size_t)key * D + 16 * xt + 4 * g, accV[xt][kt], 1.0f);
+                }
+            }
+        }
+        return;
+    }
     T *dK = static_cast<T *>(p.dk) + kvoff;
     T *dV = static_cast<T *>(p.dv) + kvoff;
 #pragma unroll
@@ -597,6 +620,28 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDkv * 4 / NW) void dkv_kernel(P
                 store4<T>(dK + (size_t)key * D + 16 * xt + 4 * g, accK[xt][kt], -p.scale);
                 store4<T>(dV + (size_t)key * D + 16 * xt + 4 * g, accV[xt][kt], 1.0f);
             }
+        }
+    }
+}
+
+// dK / dV of a split dK/dV pass: the sum of the nsplit fp32 partial planes in
+// split order (so the result is deterministic), times -scale for dK. n4 =
+// float4 groups per plane; the dV planes follow the dK planes.
+template <class T>
+__global__ __launch_bounds__(256) void dkv_reduce_kernel(const float *ws, T *dk, T *dv, size_t n4, int nsplit,
+                                                         float kscale) {
+    const f32x4 *w = reinterpret_cast<const f32x4 *>(ws);
+    const size_t stride = (size_t)gridDim.x * 256;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < 2 * n4; i += stride) {
+        const bool isv = i >= n4;
+        const size_t j = isv ? i - n4 : i;
+        const f32x4 *src = w + (isv ? (size_t)nsplit * n4 : 0) + j;
+        f32x4 a = src[0];
+        for (int s = 1; s < nsplit; ++s) a += src[(size_t)s * n4];
+        if (isv) {
+            store4<T>(dv + 4 * j, a, 1.0f);
+        } else {
+            store4<T>(dk + 4 * j, a, kscale);
         }
     }
 }
@@ -892,26 +937,69 @@ static hipError_t launch_dkv_pp(const Params &p, hipStream_t stream) {
 
 template <class Pol, int KT, bool CAUSAL, int NW = 4>
 static hipError_t launch_dkv_t(const Params &p, hipStream_t stream) {
-    const dim3 grid(p.B * p.Hkv, (p.N + 16 * KT * NW - 1) / (16 * KT * NW));
+    const dim3 grid(p.B * p.Hkv * p.dkv_split, (p.N + 16 * KT * NW - 1) / (16 * KT * NW));
     hipLaunchKernelGGL((dkv_kernel<Pol, KT, CAUSAL, NW>), grid, dim3(64 * NW), 0, stream, p);
     return hipGetLastError();
 }
 
-hipError_t launch_bwd_dkv(const Params &p, int dtype_bf16, int d, int causal, hipStream_t stream) {
-#define MXFA_DKV(POL, DD, KT)                                                          \
-    if (d == DD) return causal ? launch_dkv_t<POL<DD>, KT, true>(p, stream)           \
-                               : launch_dkv_t<POL<DD>, KT, false>(p, stream);
+// How many work-groups share the query heads of a key block's GQA group: the
+// smallest divisor of the group that gives the launch at least one work-group
+// per resident slot (256 CUs x the kernel's work-groups per CU), else the
+// whole group (one query head per work-group). 1 without GQA or when the key
+// blocks alone fill the GPU.
+template <class Pol, int KT, int NW = 4>
+static int dkv_split_t(const Params &p) {
+    if (p.group <= 1) return 1;
+    constexpr int BKV = 16 * KT * NW;
+    constexpr long long kSlots = 256LL * (Pol::kWavesDkv * 4 / NW);
+    const long long base = (long long)p.B * p.Hkv * ((p.N + BKV - 1) / BKV);
+    for (int s = 1; s < p.group; ++s) {
+        if (p.group % s == 0 && base * s >= kSlots) return s;
+    }
+    return p.group;
+}
+
+int dkv_split(const Params &p, int dtype_bf16, int d) {
     if (dtype_bf16) {
-        if (d == 64 && dkv_pingpong_selected()) {
+        if (d == 64) return dkv_split_t<PolBF16<64>, 2>(p);
+        if (d == 128) return dkv_split_t<PolBF16<128>, 1>(p);
+    } else if (d == 64) {
+        return dkv_split_t<PolF32<64>, 2>(p);
+    }
+    return 1;
+}
+
+template <class T>
+static hipError_t launch_dkv_reduce(const Params &p, int d, hipStream_t stream) {
+    const size_t n4 = (size_t)p.B * p.Hkv * p.N * (d / 4);
+    const size_t blocks = std::min<size_t>((2 * n4 + 255) / 256, 4096);
+    hipLaunchKernelGGL((dkv_reduce_kernel<T>), dim3((unsigned)blocks), dim3(256), 0, stream, p.dkv_ws,
+                       static_cast<T *>(p.dk), static_cast<T *>(p.dv), n4, p.dkv_split, -p.scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_bwd_dkv(const Params &pin, int dtype_bf16, int d, int causal, hipStream_t stream) {
+    // with a workspace, GQA shapes whose key blocks alone underfill the GPU
+    // split each group's query heads over several work-groups
+    Params p = pin;
+    p.dkv_split = p.dkv_ws != nullptr ? dkv_split(p, dtype_bf16, d) : 1;
+    if (p.dkv_split == 1) p.dkv_ws = nullptr;
+    hipError_t e = hipErrorInvalidValue;
+#define MXFA_DKV(POL, DD, KT)                                                                    \
+    if (d == DD) e = causal ? launch_dkv_t<POL<DD>, KT, true>(p, stream)                         \
+                            : launch_dkv_t<POL<DD>, KT, false>(p, stream);
+    if (dtype_bf16) {
+        if (d == 64 && p.dkv_split == 1 && dkv_pingpong_selected()) {
             return causal ? launch_dkv_pp<true>(p, stream) : launch_dkv_pp<false>(p, stream);
         }
         MXFA_DKV(PolBF16, 64, 2)
-        MXFA_DKV(PolBF16, 128, 1)
+        else MXFA_DKV(PolBF16, 128, 1)
     } else {
         MXFA_DKV(PolF32, 64, 2)
     }
 #undef MXFA_DKV
-    return hipErrorInvalidValue;
+    if (e != hipSuccess || p.dkv_split == 1) return e;
+    return dtype_bf16 ? launch_dkv_reduce<u16>(p, d, stream) : launch_dkv_reduce<float>(p, d, stream);
 }
 
 }  // namespace mxfa

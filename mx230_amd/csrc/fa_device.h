@@ -44,6 +44,12 @@ struct Params {
     // kernels assume it.
     long long q_bs, q_hs, kv_bs, kv_hs, o_bs, o_hs;
     int q_rs, kv_rs, o_rs, Nk, pos0;
+    // dK/dV pass: the query heads of a GQA group split over dkv_split
+    // work-groups per key block; with dkv_split > 1 each writes fp32 partial
+    // sums to dkv_ws ([split][B*Hkv][N][d] for dK, then the same for dV) and a
+    // reduce launch adds them in split order.
+    float *dkv_ws;
+    int dkv_split;
 };
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }

@@ -53,6 +53,8 @@ Params make_params(const mxfa_shape *s) {
     p.kv_bs = nd * s->Hkv;
     p.Nk = s->N;
     p.pos0 = 0;
+    p.dkv_ws = nullptr;
+    p.dkv_split = 1;
     return p;
 }
 
@@ -84,6 +86,15 @@ int fwd_impl(const mxfa_shape *shape, const void *q, const void *k, const void *
                                      static_cast<hipStream_t>(stream)));
 }
 
+// A workspace is optional (NULL: the dK/dV pass reduces each GQA group in one
+// work-group per key block); a given one must be 16-byte aligned and hold
+// mxfa_bwd_workspace_bytes(shape).
+int check_workspace(const mxfa_shape *shape, const void *ws, size_t bytes) {
+    if (ws == nullptr) return MXFA_OK;
+    if (!aligned16(ws)) return MXFA_ERR_ALIGN;
+    return bytes < mxfa_bwd_workspace_bytes(shape) ? MXFA_ERR_WORKSPACE : MXFA_OK;
+}
+
 Params bwd_params(const mxfa_shape *shape, const void *q, const void *k, const void *v, const void *dout,
                   const float *lse, const float *delta) {
     Params p = make_params(shape);
@@ -112,6 +123,7 @@ const char *mxfa_strerror(int status) {
         case MXFA_ERR_ALIGN: return "a device pointer is not 16-byte aligned";
         case MXFA_ERR_LAUNCH: return "the HIP runtime rejected a kernel launch";
         case MXFA_ERR_DEVICE: return "no usable gfx950 device";
+        case MXFA_ERR_WORKSPACE: return "the workspace is smaller than mxfa_bwd_workspace_bytes(shape)";
         default: return "unknown status";
     }
 }
@@ -167,13 +179,22 @@ int mxfa_run_bwd_dq(const mxfa_shape *shape, const void *q, const void *k, const
 
 int mxfa_run_bwd_dkv(const mxfa_shape *shape, const void *q, const void *k, const void *v, const void *dout,
                      const float *lse, const float *delta, void *dk, void *dv, void *stream) {
+    return mxfa_run_bwd_dkv_ws(shape, q, k, v, dout, lse, delta, dk, dv, nullptr, 0, stream);
+}
+
+int mxfa_run_bwd_dkv_ws(const mxfa_shape *shape, const void *q, const void *k, const void *v, const void *dout,
+                        const float *lse, const float *delta, void *dk, void *dv, void *workspace,
+                        size_t workspace_bytes, void *stream) {
     int rc = check_shape(shape);
     if (rc != MXFA_OK) return rc;
     rc = check_ptrs({q, k, v, dout, lse, delta, dk, dv});
     if (rc != MXFA_OK) return rc;
+    rc = check_workspace(shape, workspace, workspace_bytes);
+    if (rc != MXFA_OK) return rc;
     Params p = bwd_params(shape, q, k, v, dout, lse, delta);
     p.dk = dk;
     p.dv = dv;
+    p.dkv_ws = static_cast<float *>(workspace);
     return from_hip(mxfa::launch_bwd_dkv(p, shape->dtype == MXFA_BF16, shape->d, shape->causal,
                                          static_cast<hipStream_t>(stream)));
 }
@@ -205,19 +226,31 @@ int mxfa_run_bwd_dq_delta(const mxfa_shape *shape, const void *q, const void *k,
 
 int mxfa_run_bwd(const mxfa_shape *shape, const void *q, const void *k, const void *v, const void *o,
                  const void *dout, const float *lse, float *delta, void *dq, void *dk, void *dv, void *stream) {
+    return mxfa_run_bwd_ws(shape, q, k, v, o, dout, lse, delta, dq, dk, dv, nullptr, 0, stream);
+}
+
+int mxfa_run_bwd_ws(const mxfa_shape *shape, const void *q, const void *k, const void *v, const void *o,
+                    const void *dout, const float *lse, float *delta, void *dq, void *dk, void *dv,
+                    void *workspace, size_t workspace_bytes, void *stream) {
     int rc = check_shape(shape);
     if (rc != MXFA_OK) return rc;
     rc = check_ptrs({q, k, v, o, dout, lse, delta, dq, dk, dv});
     if (rc != MXFA_OK) return rc;
+    rc = check_workspace(shape, workspace, workspace_bytes);
+    if (rc != MXFA_OK) return rc;
     // dQ pass first: it computes Delta and writes it for the dK/dV pass
     rc = mxfa_run_bwd_dq_delta(shape, q, k, v, o, dout, lse, delta, dq, stream);
     if (rc != MXFA_OK) return rc;
-    return mxfa_run_bwd_dkv(shape, q, k, v, dout, lse, delta, dk, dv, stream);
+    return mxfa_run_bwd_dkv_ws(shape, q, k, v, dout, lse, delta, dk, dv, workspace, workspace_bytes, stream);
 }
 
 size_t mxfa_bwd_workspace_bytes(const mxfa_shape *shape) {
-    (void)shape;
-    return 0;
+    if (check_shape(shape) != MXFA_OK) return 0;
+    const Params p = make_params(shape);
+    const int split = mxfa::dkv_split(p, shape->dtype == MXFA_BF16, shape->d);
+    if (split <= 1) return 0;
+    // fp32 partial dK and dV planes, one pair per share of the query heads
+    return 2 * (size_t)split * shape->B * shape->Hkv * shape->N * shape->d * sizeof(float);
 }
 
 int mxfa_run_bwd_naive(const mxfa_shape *shape, const void *q, const void *k, const void *v,

@@ -100,6 +100,42 @@ def test_sizes_and_strings(lib):
     assert lib.mxfa_shutdown() == 0
 
 
+@pytest.mark.parametrize("kw,nbytes", [
+    # no GQA: nothing to split
+    (dict(B=4, Hq=12, Hkv=12, N=4096, d=64), 0),
+    # cfg4 (Qwen2.5, 7:1): 2*2 (b, kv head) x 32 key blocks = 128 work-groups
+    # for 768 slots; 7 is prime, so one query head per work-group
+    (dict(B=2, Hq=14, Hkv=2, N=4096, d=64), 2 * 7 * 2 * 2 * 4096 * 64 * 4),
+    # cfg5 d=64 (TinyLlama, 8:1): 64 work-groups; 4 shares give 256 < 768, so 8
+    (dict(B=1, Hq=32, Hkv=4, N=2048, d=64), 2 * 8 * 1 * 4 * 2048 * 64 * 4),
+    # cfg5 d=128: 64-key blocks, 128 work-groups for 512 slots: 4 shares
+    (dict(B=1, Hq=32, Hkv=4, N=2048, d=128), 2 * 4 * 1 * 4 * 2048 * 128 * 4),
+    # GQA whose key blocks already fill the GPU: no split
+    (dict(B=8, Hq=16, Hkv=8, N=4096, d=64), 0),
+    # fp32 parity path, tiny GQA shape: whole group split
+    (dict(B=1, Hq=2, Hkv=1, N=128, d=64, dtype=mx.MXFA_F32), 2 * 2 * 1 * 1 * 128 * 64 * 4),
+    # invalid shape
+    (dict(Hq=3, Hkv=2), 0),
+])
+def test_bwd_workspace_bytes(lib, kw, nbytes):
+    assert lib.mxfa_bwd_workspace_bytes(ctypes.byref(_shape(**kw))) == nbytes
+
+
+def test_workspace_checks(lib):
+    sh = _shape(B=2, Hq=14, Hkv=2, N=4096, d=64)
+    need = lib.mxfa_bwd_workspace_bytes(ctypes.byref(sh))
+    p = ctypes.c_void_p(4096)
+    bad = ctypes.c_void_p(4096 + 4)
+    assert lib.mxfa_run_bwd_ws(ctypes.byref(sh), p, p, p, p, p, p, p, p, p, p, p, need - 1, None) == \
+        mx_status("MXFA_ERR_WORKSPACE")
+    assert lib.mxfa_run_bwd_dkv_ws(ctypes.byref(sh), p, p, p, p, p, p, p, p, p, need - 16, None) == \
+        mx_status("MXFA_ERR_WORKSPACE")
+    assert lib.mxfa_run_bwd_dkv_ws(ctypes.byref(sh), p, p, p, p, p, p, p, p, bad, need, None) == \
+        mx_status("MXFA_ERR_ALIGN")
+    assert lib.mxfa_run_bwd_ws(ctypes.byref(sh), p, p, p, p, p, p, p, p, p, None, p, need, None) == \
+        mx_status("MXFA_ERR_NULL")
+
+
 def test_python_layer_rejects_host_tensors():
     import torch
     q = torch.zeros(1, 1, 16, 64)

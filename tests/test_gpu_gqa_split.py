@@ -1,0 +1,115 @@
+"""GPU checks of the split dK/dV pass for GQA shapes (mxfa_run_bwd_ws /
+mxfa_run_bwd_dkv_ws): the query heads of a KV-head group are shared among
+several work-groups per key block, which write fp32 partial sums into the
+caller's workspace, and a second launch adds them in a fixed order.
+
+Each case compares the split backward
+- with the CPU oracle on one KV-head group (bf16 2e-2, fp32 1e-4 of each
+  output's max magnitude),
+- with the unsplit backward (mxfa_run_bwd) on every head: the two differ only
+  in the order of the fp32 sums over a group's query heads, so dK/dV agree to
+  about one bf16 rounding (3e-3 of the max; 1e-5 in fp32) and dQ is bitwise
+  equal (the dQ pass is the same launch),
+- with itself on a second run (bitwise: the reduction order is fixed).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from gpu_helpers import TOL_BF16, TOL_F32, make_inputs, oracle_fwd_bwd, parity, rel_err, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(q, k, v, do, causal, bf16, use_ws, ws=None):
+    """Forward, then the backward from O (run_bwd_ws with a workspace sized
+    for the shape, or run_bwd). Returns numpy (O, LSE, Delta, dQ, dK, dV) and
+    the workspace tensor used."""
+    import torch
+    import mx230_amd as mx
+    tq, tk, tv, tdo = (to_dev(x, bf16) for x in (q, k, v, do))
+    B, Hq, N, d = q.shape
+    o = torch.empty_like(tq)
+    lse = torch.empty((B, Hq, N), dtype=torch.float32, device="cuda")
+    delta = torch.empty_like(lse)
+    mx.run_flash_lse(tq, tk, tv, o, lse, causal)
+    dq, dk, dv = torch.empty_like(tq), torch.empty_like(tk), torch.empty_like(tv)
+    if use_ws:
+        need = mx.bwd_workspace_bytes(tq, tk, causal)
+        assert need > 0, "shape expected to split"
+        if ws is None or ws.numel() < need:
+            ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+        mx.run_bwd_ws(tq, tk, tv, o, tdo, lse, delta, dq, dk, dv, ws, causal)
+    else:
+        mx.run_bwd(tq, tk, tv, o, tdo, lse, delta, dq, dk, dv, causal)
+    torch.cuda.synchronize()
+    return tuple(to_np(t) for t in (o, lse, delta, dq, dk, dv)), ws
+
+
+def _check(name, q, k, v, do, causal, bf16, b=0, kvh=0):
+    B, Hq, N, d = q.shape
+    Hkv = k.shape[1]
+    grp = Hq // Hkv
+    tol = TOL_BF16 if bf16 else TOL_F32
+    print(f"\n[{name}] B{B} Hq{Hq} Hkv{Hkv} N{N} d{d} causal={causal} bf16={bf16}", flush=True)
+    split, ws = _run(q, k, v, do, causal, bf16, True)
+    again, _ = _run(q, k, v, do, causal, bf16, True, ws)
+    unsplit, _ = _run(q, k, v, do, causal, bf16, False)
+    for a, c in zip(split, again):
+        assert np.array_equal(a, c), f"{name}: split backward not deterministic"
+    assert np.array_equal(split[3], unsplit[3]), f"{name}: dQ differs from the unsplit run"
+    near = 3e-3 if bf16 else 1e-5
+    for i, n in ((4, "dK"), (5, "dV")):
+        e = rel_err(split[i], unsplit[i])
+        print(f"[{name}] split vs unsplit {n}: {e:.2e}", flush=True)
+        assert e <= near, (name, n, e)
+    hs = slice(kvh * grp, (kvh + 1) * grp)
+    ref = oracle_fwd_bwd(q[b:b + 1, hs], k[b:b + 1, kvh:kvh + 1], v[b:b + 1, kvh:kvh + 1],
+                         do[b:b + 1, hs], causal)
+    sub = (split[0][b:b + 1, hs], split[1][b:b + 1, hs], split[2][b:b + 1, hs], split[3][b:b + 1, hs],
+           split[4][b:b + 1, kvh:kvh + 1], split[5][b:b + 1, kvh:kvh + 1])
+    errs, bad = parity(sub, ref, tol)
+    print(f"[{name}] oracle, group (b={b}, kvh={kvh}): " + " ".join(f"{n}={e:.2e}" for n, e in errs.items()),
+          flush=True)
+    assert not bad, (name, errs)
+
+
+def test_split_cfg4_qwen_full():
+    """cfg4, B2 Hq14 Hkv2 N4096 d64 causal bf16: one query head per work-group."""
+    q, k, v, do = make_inputs(2, 14, 2, 4096, 64, bf16=True)
+    _check("split-cfg4", q, k, v, do, True, True, b=1, kvh=1)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_split_cfg5_tinyllama_full(d):
+    """cfg5, B1 Hq32 Hkv4 N2048 causal bf16, Q/K/V x0.5 (d=64: 8 shares, d=128: 4)."""
+    q, k, v, do = make_inputs(1, 32, 4, 2048, d, mult_qkv=0.5, bf16=True)
+    _check(f"split-cfg5-d{d}", q, k, v, do, True, True, b=0, kvh=3)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("n", [1, 77, 200, 576])
+def test_split_ragged(causal, n):
+    """Ragged and tiny N (key blocks past N, a single row) with a 4:1 group."""
+    q, k, v, do = make_inputs(1, 8, 2, n, 64, bf16=True, seeds=(31, 32, 33, 34))
+    _check(f"split-n{n}", q, k, v, do, causal, True, kvh=1)
+
+
+def test_split_fp32():
+    """The fp32 parity path, 2:1 group, causal."""
+    q, k, v, do = make_inputs(1, 4, 2, 300, 64, seeds=(41, 42, 43, 44))
+    _check("split-f32", q, k, v, do, True, False, kvh=1)
+
+
+def test_workspace_reused_for_a_smaller_shape():
+    """A workspace left over from a larger call holds stale partials; a
+    smaller call into it must overwrite every element it reads."""
+    q, k, v, do = make_inputs(1, 8, 2, 1000, 64, bf16=True, seeds=(51, 52, 53, 54))
+    _, ws = _run(q, k, v, do, True, True, True)
+    q2, k2, v2, do2 = make_inputs(1, 8, 2, 333, 64, bf16=True, seeds=(55, 56, 57, 58))
+    got, ws2 = _run(q2, k2, v2, do2, True, True, True, ws)
+    assert ws2 is ws
+    want, _ = _run(q2, k2, v2, do2, True, True, False)
+    for i in (4, 5):
+        assert rel_err(got[i], want[i]) <= 3e-3
