@@ -55,6 +55,9 @@ def parse():
     ap.add_argument("--naive-table", action="store_true",
                     help="instead of the benchmark, time the naive and flash paths on the reference's own "
                          "tables (one fp32 head, d = 64) and print them as one JSON line")
+    ap.add_argument("--atomic-probe", action="store_true",
+                    help="time the writes a dQ pass fused into the dK/dV pass would make (fp32 atomics "
+                         "vs plain stores) at the bench shape, next to the separate dQ pass")
     ap.add_argument("--config-table", action="store_true",
                     help="forward and backward timings at every BASELINE config (one JSON line)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -220,6 +223,37 @@ def config_table():
                       "timing": "median of 20 after 3 warm-ups, HIP events on the launch stream"}), flush=True)
 
 
+def atomic_probe(a):
+    """The alternative to the separate dQ pass, measured: the fp32 atomic adds
+    a dQ pass fused into the dK/dV pass would issue at the bench shape (one
+    64 x 64 partial tile per (128-key block, 64-query stage), causal, d = 64),
+    and plain stores of the same bytes, beside the separate dQ pass's own time
+    (with Delta folded in, mean of 20 launches)."""
+    import torch
+    import mx230_amd as mx
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    mx.init(0)
+    bh = a.B * a.H
+    at = mx.probe_dq_atomic(bh, a.N, atomic=True)
+    st = mx.probe_dq_atomic(bh, a.N, atomic=False)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+    qs = (a.B, a.H, a.N, 64)
+    q, k, v, do = (torch.randn(qs, generator=gen, device=dev).to(torch.bfloat16) for _ in range(4))
+    o = torch.empty_like(q)
+    lse = torch.empty((a.B, a.H, a.N), device=dev)
+    delta = torch.empty_like(lse)
+    dq = torch.empty_like(q)
+    mx.run_flash_lse(q, k, v, o, lse, True)
+    dq_ms = mx._time_ms(lambda: mx.run_bwd_dq_delta(q, k, v, o, do, lse, delta, dq, True), 20)
+    print(json.dumps({"atomic_probe": {"B*H": bh, "N": a.N, "d": 64, "causal": True,
+                                       "payload_mb": round(at["payload_bytes"] / 1e6, 1),
+                                       "atomic_us": round(at["us"], 1), "atomic_tbps": round(at["tbps"], 3),
+                                       "store_us": round(st["us"], 1), "store_tbps": round(st["tbps"], 3),
+                                       "separate_dq_pass_us": round(dq_ms * 1e3, 1)}}), flush=True)
+
+
 def cpu_host():
     model = "unknown"
     try:
@@ -299,6 +333,9 @@ def main():
         return
     if a.config_table:
         config_table()
+        return
+    if a.atomic_probe:
+        atomic_probe(a)
         return
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {a.gpus}); the path shards "

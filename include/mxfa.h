@@ -240,6 +240,16 @@ int mxfa_probe_mfma(int dtype, int iters, float *sink, double *flops, void *stre
 int mxfa_probe_read(const void *x, size_t bytes, float *sink, void *stream);
 /* Launches a grid-stride copy of `bytes` (a multiple of 16) from x to y. */
 int mxfa_probe_copy(const void *x, void *y, size_t bytes, void *stream);
+/* Replays the global writes a dQ pass fused into the dK/dV pass would make at a
+ * causal shape with `bh` (batch, head) pairs, N = n (a multiple of 128) and
+ * d = 64: the work-group of each 128-key block adds one 64 x 64 fp32 partial
+ * tile per 64-query stage from its diagonal stage on. atomic = 1: fp32 atomic
+ * adds of 1.0 (on a zeroed `acc`, element (h, row, x) ends at row / 128 + 1);
+ * atomic = 0: plain stores of the same bytes. `acc` is a device
+ * float[bh * n * 64]; the payload bytes are written to *bytes. No counterpart
+ * in the reference: it measures the alternative that the reference's separate
+ * dQ pass (attention_bwd.cu:96-158) avoids. */
+int mxfa_probe_dq_atomic(float *acc, int bh, int n, int atomic, double *bytes, void *stream);
 
 #ifdef __cplusplus
 }

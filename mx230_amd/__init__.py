@@ -47,7 +47,7 @@ EXPORTS = (
     "mxfa_run_bwd_dkv", "mxfa_run_bwd_flash", "mxfa_run_bwd_dq_delta", "mxfa_run_bwd", "mxfa_bwd_workspace_bytes",
     "mxfa_run_bwd_dkv_ws", "mxfa_run_bwd_ws", "mxfa_run_bwd_naive",
     "mxfa_naive_scratch_bytes", "mxfa_run_naive_fwd", "mxfa_check_prefill", "mxfa_run_prefill",
-    "mxfa_probe_sink_len", "mxfa_probe_mfma", "mxfa_probe_read", "mxfa_probe_copy",
+    "mxfa_probe_sink_len", "mxfa_probe_mfma", "mxfa_probe_read", "mxfa_probe_copy", "mxfa_probe_dq_atomic",
 )
 
 
@@ -121,6 +121,8 @@ def load_library(path: str | None = None):
     lib.mxfa_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_int, fp, ctypes.POINTER(ctypes.c_double), vp]
     lib.mxfa_probe_read.argtypes = [vp, ctypes.c_size_t, fp, vp]
     lib.mxfa_probe_copy.argtypes = [vp, vp, ctypes.c_size_t, vp]
+    lib.mxfa_probe_dq_atomic.argtypes = [fp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                         ctypes.POINTER(ctypes.c_double), vp]
     for name in EXPORTS:
         if name not in ("mxfa_version", "mxfa_strerror", "mxfa_bwd_workspace_bytes",
                         "mxfa_naive_scratch_bytes"):
@@ -475,6 +477,24 @@ def probe_mfma_tflops(bf16: bool = True, iters: int = 256, reps: int = 5) -> flo
                                                       ctypes.byref(flops), stream))
     ms = _time_ms(launch, reps)
     return flops.value / (ms * 1e-3) / 1e12
+
+
+def probe_dq_atomic(bh: int = 48, n: int = 4096, atomic: bool = True, reps: int = 5) -> dict:
+    """Time of the global writes a dQ pass fused into the dK/dV pass would make
+    at a causal (bh heads, N = n, d = 64) shape (mxfa_probe_dq_atomic): fp32
+    atomic adds, or with atomic=False plain stores of the same bytes. Returns
+    {"us", "payload_bytes", "tbps"} (mean of reps launches after one warm-up)."""
+    torch = _torch()
+    lib = load_library()
+    acc = torch.zeros(bh * n * 64, dtype=torch.float32, device="cuda")
+    nbytes = ctypes.c_double(0.0)
+    stream = _stream(None)
+
+    def launch():
+        _check("mxfa_probe_dq_atomic", lib.mxfa_probe_dq_atomic(_ptr(acc, "acc", torch.float32), bh, n,
+                                                                  int(atomic), ctypes.byref(nbytes), stream))
+    ms = _time_ms(launch, reps)
+    return {"us": ms * 1e3, "payload_bytes": nbytes.value, "tbps": nbytes.value / (ms * 1e-3) / 1e12}
 
 
 def probe_hbm_gbps(mib: int = 1024, reps: int = 5, copy: bool = False) -> float:

@@ -27,5 +27,7 @@ double probe_mfma_flops(int bf16, int iters);
 hipError_t launch_probe_mfma(int bf16, int iters, float *sink, hipStream_t stream);
 hipError_t launch_probe_read(const void *x, size_t bytes, float *sink, hipStream_t stream);
 hipError_t launch_probe_copy(const void *x, void *y, size_t bytes, hipStream_t stream);
+double probe_dq_atomic_bytes(int bh, int n);
+hipError_t launch_probe_dq_atomic(float *acc, int bh, int n, int atomic, hipStream_t stream);
 
 }  // namespace mxfa

@@ -361,4 +361,13 @@ int mxfa_probe_copy(const void *x, void *y, size_t bytes, void *stream) {
     return from_hip(mxfa::launch_probe_copy(x, y, bytes, static_cast<hipStream_t>(stream)));
 }
 
+int mxfa_probe_dq_atomic(float *acc, int bh, int n, int atomic, double *bytes, void *stream) {
+    int rc = check_ptrs({acc, bytes});
+    if (rc != MXFA_OK) return rc;
+    if (bh < 1 || n < 128 || n % 128 != 0 || n / 128 > kMaxGridY) return MXFA_ERR_SHAPE;
+    if (atomic != 0 && atomic != 1) return MXFA_ERR_SHAPE;
+    *bytes = mxfa::probe_dq_atomic_bytes(bh, n);
+    return from_hip(mxfa::launch_probe_dq_atomic(acc, bh, n, atomic, static_cast<hipStream_t>(stream)));
+}
+
 }  // extern "C"

@@ -80,9 +80,51 @@ __global__ __launch_bounds__(kProbeThreads) void probe_copy_kernel(const float4 
         y[i] = x[i];
 }
 
+// The global writes of a dQ pass fused into the dK/dV pass, causal, d = 64:
+// work-group (head, key block kb of 128 keys) adds one 64 x 64 fp32 partial
+// tile per 64-query stage from its diagonal stage 2 kb to the last, each wave
+// a quarter of the tile (16 lane-contiguous rows of 64 floats). ATOMIC: fp32
+// atomic adds of 1 (no return); else plain stores of the same bytes.
+// Key block 0 (the most stages) is dispatched first, as in the dK/dV pass.
+template <bool ATOMIC>
+__global__ __launch_bounds__(kProbeThreads) void probe_dq_atomic_kernel(float *acc, int n) {
+    const int h = blockIdx.x, kb = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nqs = n / 64;
+    float *base = acc + (size_t)h * n * 64 + wave * 1024 + lane;
+    for (int i = 2 * kb; i < nqs; ++i) {
+        float *tile = base + (size_t)i * 64 * 64;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            if constexpr (ATOMIC) {
+                atomicAdd(tile + j * 64, 1.0f);
+            } else {
+                tile[j * 64] = (float)i;
+            }
+        }
+    }
+}
+
 }  // namespace
 
 int probe_sink_len() { return kProbeBlocks * kProbeThreads; }
+
+double probe_dq_atomic_bytes(int bh, int n) {
+    const long long nqs = n / 64, nkb = n / 128;
+    long long tiles = 0;
+    for (long long kb = 0; kb < nkb; ++kb) tiles += nqs - 2 * kb;
+    return (double)bh * (double)tiles * 64.0 * 64.0 * 4.0;
+}
+
+hipError_t launch_probe_dq_atomic(float *acc, int bh, int n, int atomic, hipStream_t stream) {
+    const dim3 grid(bh, n / 128);
+    if (atomic) {
+        hipLaunchKernelGGL((probe_dq_atomic_kernel<true>), grid, dim3(kProbeThreads), 0, stream, acc, n);
+    } else {
+        hipLaunchKernelGGL((probe_dq_atomic_kernel<false>), grid, dim3(kProbeThreads), 0, stream, acc, n);
+    }
+    return hipGetLastError();
+}
 
 double probe_mfma_flops(int bf16, int iters) {
     const double per_mfma = bf16 ? 2.0 * 16 * 16 * 32 : 2.0 * 16 * 16 * 4;

@@ -196,6 +196,11 @@ def test_probe_argument_checks(lib):
     assert lib.mxfa_probe_read(None, 32, fake, None) == mx_status("MXFA_ERR_NULL")
     assert lib.mxfa_probe_copy(fake, fake, 0, None) == mx_status("MXFA_ERR_SHAPE")
     assert lib.mxfa_probe_copy(fake, ctypes.c_void_p(4104), 32, None) == mx_status("MXFA_ERR_ALIGN")
+    nb = ctypes.c_double(0.0)
+    assert lib.mxfa_probe_dq_atomic(None, 1, 128, 1, ctypes.byref(nb), None) == mx_status("MXFA_ERR_NULL")
+    assert lib.mxfa_probe_dq_atomic(fake, 1, 192, 1, ctypes.byref(nb), None) == mx_status("MXFA_ERR_SHAPE")
+    assert lib.mxfa_probe_dq_atomic(fake, 0, 128, 1, ctypes.byref(nb), None) == mx_status("MXFA_ERR_SHAPE")
+    assert lib.mxfa_probe_dq_atomic(fake, 1, 128, 2, ctypes.byref(nb), None) == mx_status("MXFA_ERR_SHAPE")
 
 
 def mx_status(name: str) -> int:

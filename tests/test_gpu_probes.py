@@ -29,3 +29,30 @@ def test_probe_hbm(copy):
     g = mx.probe_hbm_gbps(mib=1024, copy=copy)
     print(f"\n[probe] HBM {'copy' if copy else 'read'} {g:.0f} GB/s", flush=True)
     assert 2000.0 < g < 8200.0
+
+
+def test_probe_dq_atomic_counts_and_rates():
+    """The fused-dQ write replay: on a zeroed buffer one atomic launch leaves
+    row // 128 + 1 in every element of row `row` (the key blocks at or before
+    its diagonal); the store variant moves the same payload."""
+    import torch
+    import mx230_amd as mx
+    import ctypes
+    lib = mx.load_library()
+    bh, n = 3, 1024
+    acc = torch.zeros(bh * n * 64, dtype=torch.float32, device="cuda")
+    nbytes = ctypes.c_double(0.0)
+    rc = lib.mxfa_probe_dq_atomic(ctypes.c_void_p(acc.data_ptr()), bh, n, 1, ctypes.byref(nbytes), None)
+    assert rc == 0
+    torch.cuda.synchronize()
+    want = (torch.arange(n, device="cuda") // 128 + 1).float().view(1, n, 1).expand(bh, n, 64)
+    assert torch.equal(acc.view(bh, n, 64), want)
+    assert nbytes.value == bh * sum(n // 64 - 2 * kb for kb in range(n // 128)) * 64 * 64 * 4
+    a = mx.probe_dq_atomic(48, 4096, atomic=True)
+    st = mx.probe_dq_atomic(48, 4096, atomic=False)
+    print(f"\n[probe] fused-dQ writes at B*H=48 N=4096: {a['payload_bytes'] / 1e6:.0f} MB, "
+          f"atomic {a['us']:.0f} us ({a['tbps']:.2f} TB/s), store {st['us']:.0f} us ({st['tbps']:.2f} TB/s)",
+          flush=True)
+    # the 830 MB payload lands on 50 MB of addresses: repeated stores to a line
+    # merge in the write-back caches, so the store rate has no HBM bound
+    assert 0.05 < a["tbps"] < 10.0 and st["tbps"] > 0.05
