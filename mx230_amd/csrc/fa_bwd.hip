@@ -91,28 +91,28 @@ __device__ __forceinline__ void stage_qdo(typename Pol::T *sq, typename Pol::T *
 
 // ------------------------------------------------------------------ dQ pass
 
-// One 64-key stage of the dQ pass for one wave (32 queries). qf holds Q
+// One 64-key stage of the dQ pass for one wave (16 QT queries). qf holds Q
 // scale log2(e) and the score accumulators start at -L log2(e), so they come
 // out as the exponents of P; dof holds -dO and the dP accumulators start at
 // Delta, so they come out as Delta - dP and the MFMAs accumulate -dQ / scale
 // (the epilogue multiplies by -scale).
-template <class Pol, bool CAUSAL, bool MASK>
-__device__ __forceinline__ void dq_stage(f32x4 (&acc)[Pol::D / 16][2], const typename Pol::Frag (&qf)[2][Pol::NC],
-                                         const typename Pol::Frag (&dof)[2][Pol::NC], const float (&nL2)[2],
-                                         const float (&Dl)[2], const typename Pol::T *sk,
+template <class Pol, int QT, bool CAUSAL, bool MASK>
+__device__ __forceinline__ void dq_stage(f32x4 (&acc)[Pol::D / 16][QT], const typename Pol::Frag (&qf)[QT][Pol::NC],
+                                         const typename Pol::Frag (&dof)[QT][Pol::NC], const float (&nL2)[QT],
+                                         const float (&Dl)[QT], const typename Pol::T *sk,
                                          const typename Pol::T *sv, int k0, int q0, int N, int g, int l16) {
     using Frag = typename Pol::Frag;
     constexpr int NC = Pol::NC, XT = Pol::D / 16;
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
-        f32x4 s[2][2], dp[2][2];  // [t][qt]
+        f32x4 s[2][QT], dp[2][QT];  // [t][qt]
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             Frag a[NC];
             const int n = 32 * blk + Pol::arow(t, l16);
             Pol::lds_row_frags(a, sk, n, g);
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt) {
+            for (int qt = 0; qt < QT; ++qt) {
                 f32x4 c = f32x4{nL2[qt], nL2[qt], nL2[qt], nL2[qt]};
 #pragma unroll
                 for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], qf[qt][kc], c);
@@ -120,7 +120,7 @@ __device__ __forceinline__ void dq_stage(f32x4 (&acc)[Pol::D / 16][2], const typ
             }
             Pol::lds_row_frags(a, sv, n, g);
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt) {
+            for (int qt = 0; qt < QT; ++qt) {
                 f32x4 c = f32x4{Dl[qt], Dl[qt], Dl[qt], Dl[qt]};
 #pragma unroll
                 for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], dof[qt][kc], c);
@@ -128,7 +128,7 @@ __device__ __forceinline__ void dq_stage(f32x4 (&acc)[Pol::D / 16][2], const typ
             }
         }
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
+        for (int qt = 0; qt < QT; ++qt) {
             const int qi = q0 + 16 * qt + l16;
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
@@ -144,13 +144,13 @@ __device__ __forceinline__ void dq_stage(f32x4 (&acc)[Pol::D / 16][2], const typ
                 }
             }
         }
-        typename Pol::ChainB cb[2];
+        typename Pol::ChainB cb[QT];
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) cb[qt] = Pol::pack(s[0][qt], s[1][qt]);
+        for (int qt = 0; qt < QT; ++qt) cb[qt] = Pol::pack(s[0][qt], s[1][qt]);
 #pragma unroll
         for (int xt = 0; xt < XT; ++xt) {
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt) acc[xt][qt] = Pol::chain(acc[xt][qt], cb[qt], sk, 16 * xt, 32 * blk, g, l16);
+            for (int qt = 0; qt < QT; ++qt) acc[xt][qt] = Pol::chain(acc[xt][qt], cb[qt], sk, 16 * xt, 32 * blk, g, l16);
         }
     }
 }
@@ -158,12 +158,14 @@ __device__ __forceinline__ void dq_stage(f32x4 (&acc)[Pol::D / 16][2], const typ
 // DELTA: compute Delta_i = sum_x dO[i,x] O[i,x] here (O from p.o_in, the
 // same fp32 products as preprocess_kernel, summed in another order) and write
 // it to p.delta for the dK/dV pass, instead of reading it from there.
-template <class Pol, bool CAUSAL, int NW, bool DELTA>
-__global__ __launch_bounds__(64 * NW, Pol::kWavesDq * 4 / NW) void dq_kernel(Params p) {
+// QT: 16-query tiles per wave; NW: waves per work-group.
+template <class Pol, bool CAUSAL, int NW, bool DELTA, int QT>
+__global__ __launch_bounds__(64 * NW, Pol::kWavesDq) void dq_kernel(Params p) {
     using T = typename Pol::T;
     using Frag = typename Pol::Frag;
     constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
-    constexpr int BQ = 32 * NW, BK = Pol::ROWS, NT = 64 * NW;
+    constexpr int BQ = 16 * QT * NW, BK = Pol::ROWS, NT = 64 * NW;
+    static_assert(BQ % BK == 0, "causal: the masked tail is the work-group's BQ / BK diagonal stages");
 
     __shared__ __attribute__((aligned(16))) T sK[2][BK * D];
     __shared__ __attribute__((aligned(16))) T sV[2][BK * D];
@@ -181,12 +183,12 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDq * 4 / NW) void dq_kernel(Par
     const size_t kvoff = ((size_t)b * p.Hkv + kvh) * N * D;
     const T *K = static_cast<const T *>(p.k) + kvoff;
     const T *V = static_cast<const T *>(p.v) + kvoff;
-    const int q0 = qb * BQ + wave * 32;
+    const int q0 = qb * BQ + wave * 16 * QT;
 
-    Frag qf[2][NC], dof[2][NC];
-    float nL2[2], Dl[2];
+    Frag qf[QT][NC], dof[QT][NC];
+    float nL2[QT], Dl[QT];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < QT; ++qt) {
         const int qi = q0 + 16 * qt + l16;
         const bool ok = qi < N;
         Pol::gmem_row_frags(qf[qt], Q + (size_t)qi * D, g, ok);
@@ -211,9 +213,12 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDq * 4 / NW) void dq_kernel(Par
         }
         nL2[qt] = ok ? p.lse[(size_t)bh * N + qi] * -kLog2e : 0.f;
     }
-    f32x4 acc[XT][2];
+    f32x4 acc[XT][QT];
 #pragma unroll
-    for (int xt = 0; xt < XT; ++xt) acc[xt][0] = acc[xt][1] = zero4();
+    for (int xt = 0; xt < XT; ++xt) {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) acc[xt][qt] = zero4();
+    }
 
     const int kend = CAUSAL ? min(N, qb * BQ + BQ) : N;
     const int nsteps = (kend + BK - 1) / BK;
@@ -223,19 +228,21 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDq * 4 / NW) void dq_kernel(Par
     wait_stage();
     __syncthreads();
 
-    // Every stage but the last two is unmasked for every wave (causal: its keys
-    // all precede the workgroup's first query; otherwise: only the last stage
-    // can be ragged). Those run in pairs with the LDS buffer a compile-time
-    // constant, so the tile addresses fold into the instructions' immediate
-    // offsets; the last two stages choose their buffer and masking at run time.
+    // Every stage but the last kTail is unmasked for every wave (causal: its
+    // keys all precede the workgroup's first query; otherwise: only the last
+    // stage can be ragged). Those run in pairs with the LDS buffer a
+    // compile-time constant, so the tile addresses fold into the instructions'
+    // immediate offsets; the last kTail stages choose their buffer and masking
+    // at run time.
     auto main_stage = [&](auto buf, int st) __attribute__((always_inline)) {
         constexpr int B = decltype(buf)::value;
         if (st + 1 < nsteps) stage_kv<Pol, NT>(sK[B ^ 1], sV[B ^ 1], K, V, (st + 1) * BK, N, plan, wave);
-        dq_stage<Pol, CAUSAL, false>(acc, qf, dof, nL2, Dl, sK[B], sV[B], st * BK, q0, N, g, l16);
+        dq_stage<Pol, QT, CAUSAL, false>(acc, qf, dof, nL2, Dl, sK[B], sV[B], st * BK, q0, N, g, l16);
         wait_stage();
         __syncthreads();
     };
-    const int nmain = nsteps - min(nsteps, 2);
+    constexpr int kTail = BQ / BK > 2 ? BQ / BK : 2;
+    const int nmain = nsteps - min(nsteps, kTail);
     int st = 0;
     for (; st + 1 < nmain; st += 2) {
         main_stage(std::integral_constant<int, 0>{}, st);
@@ -248,8 +255,8 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDq * 4 / NW) void dq_kernel(Par
         const int k0 = st * BK;
         // one (masked) body for these stages: a second, unmasked body behind a
         // branch makes the register allocator spill at three waves per SIMD
-        if (!CAUSAL || k0 <= q0 + 31) {
-            dq_stage<Pol, CAUSAL, true>(acc, qf, dof, nL2, Dl, sK[cur], sV[cur], k0, q0, N, g, l16);
+        if (!CAUSAL || k0 <= q0 + 16 * QT - 1) {
+            dq_stage<Pol, QT, CAUSAL, true>(acc, qf, dof, nL2, Dl, sK[cur], sV[cur], k0, q0, N, g, l16);
         }
         wait_stage();
         __syncthreads();
@@ -257,7 +264,7 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDq * 4 / NW) void dq_kernel(Par
 
     T *dQ = static_cast<T *>(p.dq) + (size_t)bh * N * D;
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < QT; ++qt) {
         const int qi = q0 + 16 * qt + l16;
         if (qi < N) {
 #pragma unroll
@@ -455,7 +462,7 @@ __device__ __forceinline__ void dkv_stage(f32x4 (&accK)[Pol::D / 16][KT], f32x4 
 }
 
 template <class Pol, int KT, bool CAUSAL, int NW>
-__global__ __launch_bounds__(64 * NW, Pol::kWavesDkv * 4 / NW) void dkv_kernel(Params p) {
+__global__ __launch_bounds__(64 * NW, Pol::kWavesDkv) void dkv_kernel(Params p) {
     using T = typename Pol::T;
     using Frag = typename Pol::Frag;
     constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
@@ -892,13 +899,14 @@ hipError_t launch_preprocess(const Params &p, int dtype_bf16, int d, hipStream_t
     return hipGetLastError();
 }
 
-template <class Pol, bool CAUSAL, int NW = 4>
+template <class Pol, bool CAUSAL>
 static hipError_t launch_dq_t(const Params &p, int delta, hipStream_t stream) {
-    const dim3 grid(p.B * p.Hq, (p.N + 32 * NW - 1) / (32 * NW));
+    constexpr int QT = Pol::kDqTiles, NW = Pol::kDqWavesPerGroup, BQ = 16 * QT * NW;
+    const dim3 grid(p.B * p.Hq, (p.N + BQ - 1) / BQ);
     if (delta) {
-        hipLaunchKernelGGL((dq_kernel<Pol, CAUSAL, NW, true>), grid, dim3(64 * NW), 0, stream, p);
+        hipLaunchKernelGGL((dq_kernel<Pol, CAUSAL, NW, true, QT>), grid, dim3(64 * NW), 0, stream, p);
     } else {
-        hipLaunchKernelGGL((dq_kernel<Pol, CAUSAL, NW, false>), grid, dim3(64 * NW), 0, stream, p);
+        hipLaunchKernelGGL((dq_kernel<Pol, CAUSAL, NW, false, QT>), grid, dim3(64 * NW), 0, stream, p);
     }
     return hipGetLastError();
 }

@@ -122,6 +122,11 @@ struct PolBF16 {
     // N = 4096) pair up into equal loads over 768 slots.
     static constexpr int kWaves = D == 64 ? 2 : 1;
     static constexpr int kWavesDq = D == 64 ? 3 : 1;
+    // dQ pass: 16-query tiles per wave and waves per work-group. 64 queries
+    // per wave halve the LDS reads per MFMA but need two waves per SIMD, and
+    // ran 9-10% slower (48 queries: 8%)
+    static constexpr int kDqTiles = 2;
+    static constexpr int kDqWavesPerGroup = 4;
     static constexpr int kWavesDkv = D == 64 ? 3 : 2;
     // dK/dV stage ring depth (loads issued kDkvBuffers - 1 stages ahead); a
     // third buffer measured no faster at d = 64
@@ -242,6 +247,8 @@ struct PolF32 {
     static constexpr int ROWS = 64;
     static constexpr int kWaves = 1;
     static constexpr int kWavesDq = 1;
+    static constexpr int kDqTiles = 2;
+    static constexpr int kDqWavesPerGroup = 4;
     static constexpr int kWavesDkv = 1;
     static constexpr int kDkvBuffers = 2;
 
