@@ -124,7 +124,8 @@ struct PolBF16 {
     static constexpr int kWavesDq = D == 64 ? 3 : 1;
     // dQ pass: 16-query tiles per wave and waves per work-group. 64 queries
     // per wave halve the LDS reads per MFMA but need two waves per SIMD, and
-    // ran 9-10% slower (48 queries: 8%)
+    // ran 9-10% slower (48 queries: 8%); 16 queries at five waves per SIMD
+    // double them and ran 13% slower
     static constexpr int kDqTiles = 2;
     static constexpr int kDqWavesPerGroup = 4;
     static constexpr int kWavesDkv = D == 64 ? 3 : 2;
