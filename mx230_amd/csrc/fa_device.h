@@ -119,8 +119,12 @@ struct PolBF16 {
     // kernels are compiled for: the largest count that fits without spills in
     // their loops. Three work-groups per CU also balance the causal passes:
     // their 128-row work-groups (64 - 2i stages of 64 for i = 0..31 at
-    // N = 4096) pair up into equal loads over 768 slots.
+    // N = 4096) pair up into equal loads over 768 slots. The forward also has
+    // a three-wave form (kWavesFwdCausal, 60 bytes of spills outside its main
+    // loop) for causal launches of at least 768 work-groups; it was 4-16%
+    // slower on smaller causal grids and on non-causal ones.
     static constexpr int kWaves = D == 64 ? 2 : 1;
+    static constexpr int kWavesFwdCausal = D == 64 ? 3 : 1;
     static constexpr int kWavesDq = D == 64 ? 3 : 1;
     // dQ pass: 16-query tiles per wave and waves per work-group. 64 queries
     // per wave halve the LDS reads per MFMA but need two waves per SIMD, and
@@ -247,6 +251,7 @@ struct PolF32 {
     static constexpr int NC = D / 4;
     static constexpr int ROWS = 64;
     static constexpr int kWaves = 1;
+    static constexpr int kWavesFwdCausal = 1;
     static constexpr int kWavesDq = 1;
     static constexpr int kDqTiles = 2;
     static constexpr int kDqWavesPerGroup = 4;

@@ -220,8 +220,9 @@ __device__ __forceinline__ void fwd_stage_lazy(f32x4 (&acc)[Pol::D / 16][2], flo
     }
 }
 
-template <class Pol, bool CAUSAL>
-__global__ __launch_bounds__(256, Pol::kWaves) void fwd_kernel(Params p) {
+// WPS: waves per SIMD the kernel is compiled for.
+template <class Pol, bool CAUSAL, int WPS>
+__global__ __launch_bounds__(256, WPS) void fwd_kernel(Params p) {
     using T = typename Pol::T;
     using Frag = typename Pol::Frag;
     constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
@@ -329,7 +330,15 @@ __global__ __launch_bounds__(256, Pol::kWaves) void fwd_kernel(Params p) {
 template <class Pol, bool CAUSAL>
 static hipError_t launch_fwd_t(const Params &p, hipStream_t stream) {
     const dim3 grid(p.B * p.Hq, (p.N + 127) / 128);
-    hipLaunchKernelGGL((fwd_kernel<Pol, CAUSAL>), grid, dim3(256), 0, stream, p);
+    constexpr int kHi = Pol::kWavesFwdCausal;
+    if constexpr (CAUSAL && kHi > Pol::kWaves) {
+        // enough causal work-groups to fill kHi per CU (256 CUs)
+        if ((long long)grid.x * grid.y >= 256LL * kHi) {
+            hipLaunchKernelGGL((fwd_kernel<Pol, CAUSAL, kHi>), grid, dim3(256), 0, stream, p);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((fwd_kernel<Pol, CAUSAL, Pol::kWaves>), grid, dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 
