@@ -120,9 +120,9 @@ struct PolBF16 {
     // their loops. Three work-groups per CU also balance the causal passes:
     // their 128-row work-groups (64 - 2i stages of 64 for i = 0..31 at
     // N = 4096) pair up into equal loads over 768 slots. The forward also has
-    // a three-wave form (kWavesFwdCausal, 60 bytes of spills outside its main
-    // loop) for causal launches of at least 768 work-groups; it was 4-16%
-    // slower on smaller causal grids and on non-causal ones.
+    // a three-wave form (kWavesFwdCausal) for causal launches of at least 768
+    // work-groups; on smaller causal grids and non-causal launches it is no
+    // faster than two.
     static constexpr int kWaves = D == 64 ? 2 : 1;
     static constexpr int kWavesFwdCausal = D == 64 ? 3 : 1;
     static constexpr int kWavesDq = D == 64 ? 3 : 1;

@@ -165,7 +165,8 @@ __device__ __forceinline__ void fwd_stage_lazy(f32x4 (&acc)[Pol::D / 16][2], flo
     }
     if (__builtin_amdgcn_ballot_w64(mx[0] > kLazy || mx[1] > kLazy) != 0) {
         // some row of the wave moved up by more than kLazy: rescale (rows whose
-        // max did not rise keep shift 0)
+        // max did not rise keep shift 0) and shift its scores in place, so the
+        // exponentials below serve both cases from the same registers
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt) {
             const float shift = fmaxf(mx[qt], 0.f);
@@ -173,39 +174,33 @@ __device__ __forceinline__ void fwd_stage_lazy(f32x4 (&acc)[Pol::D / 16][2], flo
             m[qt] += shift;
 #pragma unroll
             for (int xt = 0; xt < XT; ++xt) acc[xt][qt] *= corr;
-            float ls = lsum[qt] * corr;
+            lsum[qt] *= corr;
 #pragma unroll
             for (int blk = 0; blk < 2; ++blk) {
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float pv = fast_exp2(s[blk][t][qt][r] - shift);
-                        s[blk][t][qt][r] = pv;
-                        ls += pv;
-                    }
+                    for (int r = 0; r < 4; ++r) s[blk][t][qt][r] -= shift;
                 }
             }
-            lsum[qt] = ls;
         }
-    } else {
+    }
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
-            float ls = lsum[qt];
+    for (int qt = 0; qt < 2; ++qt) {
+        float ls = lsum[qt];
 #pragma unroll
-            for (int blk = 0; blk < 2; ++blk) {
+        for (int blk = 0; blk < 2; ++blk) {
 #pragma unroll
-                for (int t = 0; t < 2; ++t) {
+            for (int t = 0; t < 2; ++t) {
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float pv = fast_exp2(s[blk][t][qt][r]);
-                        s[blk][t][qt][r] = pv;
-                        ls += pv;
-                    }
+                for (int r = 0; r < 4; ++r) {
+                    const float pv = fast_exp2(s[blk][t][qt][r]);
+                    s[blk][t][qt][r] = pv;
+                    ls += pv;
                 }
             }
-            lsum[qt] = ls;
         }
+        lsum[qt] = ls;
     }
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
