@@ -122,10 +122,12 @@ struct PolBF16 {
     // N = 4096) pair up into equal loads over 768 slots. The forward also has
     // a three-wave form (kWavesFwdCausal) for causal launches of at least 768
     // work-groups; on smaller causal grids and non-causal launches it is no
-    // faster than two.
-    static constexpr int kWaves = D == 64 ? 2 : 1;
-    static constexpr int kWavesFwdCausal = D == 64 ? 3 : 1;
-    static constexpr int kWavesDq = D == 64 ? 3 : 1;
+    // faster than two. At d = 128 all three kernels run two waves per SIMD
+    // (dK/dV is held there by its 66 KB of LDS; the non-causal forward spills
+    // 64 bytes per lane at two and still ran 22% faster than at one).
+    static constexpr int kWaves = 2;
+    static constexpr int kWavesFwdCausal = D == 64 ? 3 : 2;
+    static constexpr int kWavesDq = D == 64 ? 3 : 2;
     // dQ pass: 16-query tiles per wave and waves per work-group. 64 queries
     // per wave halve the LDS reads per MFMA but need two waves per SIMD, and
     // ran 9-10% slower (48 queries: 8%); 16 queries at five waves per SIMD
