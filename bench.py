@@ -459,6 +459,9 @@ def main():
                    "B": a.B, "Hq": a.H, "Hkv": hkv, "N": a.N, "d": a.d, "causal": causal,
                    "parallelism": "single GPU"},
         "pct_peak": round(100.0 * value / peak, 2),
+        # MFMA work the two passes execute per step (the dQ pass recomputes S
+        # and dP: 14 N^2 d per (batch, head), halved when causal) over the step
+        "executed_tflops": round((kflops["dkv"] + kflops["dq"]) / (ms_per_step * 1e-3) / 1e12, 2),
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2), "peak": peak,
                      "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic},
         "kernels_ms": {n: round(t, 4) for n, t in kern.items()},
