@@ -91,16 +91,19 @@ __device__ __forceinline__ void stage_qdo(typename Pol::T *sq, typename Pol::T *
 
 // ------------------------------------------------------------------ dQ pass
 
-// One 64-key stage of the dQ pass for one wave (16 QT queries). qf holds Q
-// scale log2(e) and the score accumulators start at -L log2(e), so they come
-// out as the exponents of P; dof holds -dO and the dP accumulators start at
-// Delta, so they come out as Delta - dP and the MFMAs accumulate -dQ / scale
-// (the epilogue multiplies by -scale).
+// One 64-key stage of the dQ pass for one wave (16 QT queries). The score
+// accumulators start at nL2, so they come out as the exponents of P, times
+// xmul where the policy keeps Q exact (Pol::kExactScale: qf holds Q, nL2 is
+// -L / scale, xmul = scale log2(e)); otherwise qf holds Q scale log2(e) and
+// nL2 is -L log2(e). dof holds -dO and the dP accumulators start at Delta, so
+// they come out as Delta - dP and the MFMAs accumulate -dQ / scale (the
+// epilogue multiplies by -scale).
 template <class Pol, int QT, bool CAUSAL, bool MASK>
 __device__ __forceinline__ void dq_stage(f32x4 (&acc)[Pol::D / 16][QT], const typename Pol::Frag (&qf)[QT][Pol::NC],
                                          const typename Pol::Frag (&dof)[QT][Pol::NC], const float (&nL2)[QT],
                                          const float (&Dl)[QT], const typename Pol::T *sk,
-                                         const typename Pol::T *sv, int k0, int q0, int N, int g, int l16) {
+                                         const typename Pol::T *sv, int k0, int q0, int N, int g, int l16,
+                                         float xmul) {
     using Frag = typename Pol::Frag;
     constexpr int NC = Pol::NC, XT = Pol::D / 16;
 #pragma unroll
@@ -139,7 +142,7 @@ __device__ __forceinline__ void dq_stage(f32x4 (&acc)[Pol::D / 16][QT], const ty
                         const int key = k0 + 32 * blk + Pol::bidx(t, g, r);
                         x = (key >= N || (CAUSAL && key > qi)) ? -INFINITY : x;
                     }
-                    const float pv = fast_exp2(x);
+                    const float pv = fast_exp2(Pol::kExactScale ? x * xmul : x);
                     s[t][qt][r] = pv * dp[t][qt][r];  // -dS / scale
                 }
             }
@@ -208,10 +211,10 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDq) void dq_kernel(Params p) {
         }
 #pragma unroll
         for (int kc = 0; kc < NC; ++kc) {
-            qf[qt][kc] = Pol::scaled(qf[qt][kc], p.scale_log2);
+            if (!Pol::kExactScale) qf[qt][kc] = Pol::scaled(qf[qt][kc], p.scale_log2);
             dof[qt][kc] = Pol::neg(dof[qt][kc]);
         }
-        nL2[qt] = ok ? p.lse[(size_t)bh * N + qi] * -kLog2e : 0.f;
+        nL2[qt] = ok ? p.lse[(size_t)bh * N + qi] * (Pol::kExactScale ? -1.0f / p.scale : -kLog2e) : 0.f;
     }
     f32x4 acc[XT][QT];
 #pragma unroll
@@ -237,7 +240,7 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDq) void dq_kernel(Params p) {
     auto main_stage = [&](auto buf, int st) __attribute__((always_inline)) {
         constexpr int B = decltype(buf)::value;
         if (st + 1 < nsteps) stage_kv<Pol, NT>(sK[B ^ 1], sV[B ^ 1], K, V, (st + 1) * BK, N, plan, wave);
-        dq_stage<Pol, QT, CAUSAL, false>(acc, qf, dof, nL2, Dl, sK[B], sV[B], st * BK, q0, N, g, l16);
+        dq_stage<Pol, QT, CAUSAL, false>(acc, qf, dof, nL2, Dl, sK[B], sV[B], st * BK, q0, N, g, l16, p.scale_log2);
         wait_stage();
         __syncthreads();
     };
@@ -256,7 +259,8 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDq) void dq_kernel(Params p) {
         // one (masked) body for these stages: a second, unmasked body behind a
         // branch makes the register allocator spill at three waves per SIMD
         if (!CAUSAL || k0 <= q0 + 16 * QT - 1) {
-            dq_stage<Pol, QT, CAUSAL, true>(acc, qf, dof, nL2, Dl, sK[cur], sV[cur], k0, q0, N, g, l16);
+            dq_stage<Pol, QT, CAUSAL, true>(acc, qf, dof, nL2, Dl, sK[cur], sV[cur], k0, q0, N, g, l16,
+                                            p.scale_log2);
         }
         wait_stage();
         __syncthreads();
@@ -316,24 +320,25 @@ __device__ __forceinline__ void chain_block(f32x4 (&accK)[4][2], f32x4 (&accV)[4
 // and Delta of rows bidx(t, g, 0..3).
 struct ScoreOps {
     bf16x8 q[2][2], d[2][2];  // [t][kc]
-    f32x4 dl[2], nl[2];       // Delta and -LSE log2(e) of the rows
+    f32x4 dl[2], nl[2];       // Delta and LSE x lmul of the rows
 };
 template <class Pol>
 __device__ __forceinline__ void score_operands(ScoreOps &o, const u16 *sq, const u16 *sdo, const float *sl,
-                                               const float *sd, int blk, int g, int l16) {
+                                               const float *sd, int blk, int g, int l16, float lmul) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
         const int n = blk + Pol::arow(t, l16);
         Pol::lds_row_frags(o.q[t], sq, n, g);
         Pol::lds_row_frags(o.d[t], sdo, n, g);
         o.dl[t] = *reinterpret_cast<const f32x4 *>(sd + blk + Pol::bidx(t, g, 0));
-        o.nl[t] = *reinterpret_cast<const f32x4 *>(sl + blk + Pol::bidx(t, g, 0)) * -kLog2e;
+        o.nl[t] = *reinterpret_cast<const f32x4 *>(sl + blk + Pol::bidx(t, g, 0)) * lmul;
     }
 }
 
-// Exponents S scale log2(e) - L log2(e) = (K scale log2(e)) Q^T + C, C = -L
-// log2(e) (kf holds the scaled K), and Delta - dP = Delta + (-V) dO^T of one
-// block.
+// Scores K Q^T + C with C = L lmul (the exponents of P up to the factor
+// softmax_block applies: kf holds K and lmul = -1 / scale with exact scaling,
+// else kf holds K scale log2(e) and lmul = -log2(e)), and Delta - dP =
+// Delta + (-V) dO^T of one block.
 template <class Pol>
 __device__ __forceinline__ void score_block(f32x4 (&s)[2][2], f32x4 (&dp)[2][2], const bf16x8 (&kf)[2][2],
                                             const bf16x8 (&vf)[2][2], const ScoreOps &o) {
@@ -353,7 +358,8 @@ __device__ __forceinline__ void score_block(f32x4 (&s)[2][2], f32x4 (&dp)[2][2],
     }
 }
 
-// P = exp2(S scale log2(e) - L log2(e)) (s holds the exponents) and
+// P = exp2(S scale log2(e) - L log2(e)) (s holds the exponents, or with
+// exact scaling the exponents / (scale log2(e)), multiplied back here) and
 // -dS / scale = P (Delta - dP), packed as the chain operands. MASK (causal):
 // query row bidx of the block precedes key 16 kt + l16 of the wave iff
 // bidx - l16 < moff + 16 kt, where moff = first key of the wave - first query
@@ -361,7 +367,7 @@ __device__ __forceinline__ void score_block(f32x4 (&s)[2][2], f32x4 (&dp)[2][2],
 // whose P is then all zero).
 template <class Pol, bool MASK>
 __device__ __forceinline__ void softmax_block(f32x4 (&s)[2][2], f32x4 (&dp)[2][2], bf16x8 (&cp)[2],
-                                              bf16x8 (&cds)[2], int moff, int g, int l16) {
+                                              bf16x8 (&cds)[2], int moff, int g, int l16, float xmul) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
 #pragma unroll
@@ -370,7 +376,7 @@ __device__ __forceinline__ void softmax_block(f32x4 (&s)[2][2], f32x4 (&dp)[2][2
             for (int kt = 0; kt < 2; ++kt) {
                 float x = s[t][kt][r];
                 if constexpr (MASK) x = Pol::bidx(t, g, r) - l16 < moff + 16 * kt ? -INFINITY : x;
-                const float pv = fast_exp2(x);
+                const float pv = fast_exp2(Pol::kExactScale ? x * xmul : x);
                 s[t][kt][r] = pv;
                 dp[t][kt][r] = pv * dp[t][kt][r];
             }
@@ -385,17 +391,19 @@ __device__ __forceinline__ void softmax_block(f32x4 (&s)[2][2], f32x4 (&dp)[2][2
 
 }  // namespace pp
 
-// One 64-query stage of the dK/dV pass for one wave (16*KT keys). kf holds
-// K scale log2(e) and the score accumulators start at -L log2(e), so they come
-// out as the exponents of P; vf holds -V and the dP accumulators start at
-// Delta, so they come out as Delta - dP and accK accumulates -dK / scale (the
-// epilogue multiplies by -scale).
+// One 64-query stage of the dK/dV pass for one wave (16*KT keys). The score
+// accumulators start at L lmul, so they come out as the exponents of P, times
+// xmul where the policy keeps K exact (Pol::kExactScale: kf holds K, lmul =
+// -1 / scale, xmul = scale log2(e)); otherwise kf holds K scale log2(e) and
+// lmul = -log2(e). vf holds -V and the dP accumulators start at Delta, so
+// they come out as Delta - dP and accK accumulates -dK / scale (the epilogue
+// multiplies by -scale).
 template <class Pol, int KT, bool CAUSAL, bool MASK>
 __device__ __forceinline__ void dkv_stage(f32x4 (&accK)[Pol::D / 16][KT], f32x4 (&accV)[Pol::D / 16][KT],
                                           const typename Pol::Frag (&kf)[KT][Pol::NC],
                                           const typename Pol::Frag (&vf)[KT][Pol::NC], const typename Pol::T *sq,
                                           const typename Pol::T *sdo, const float *sl, const float *sd, int qs,
-                                          int kw0, int N, int g, int l16) {
+                                          int kw0, int N, int g, int l16, float lmul, float xmul) {
     using Frag = typename Pol::Frag;
     constexpr int NC = Pol::NC, XT = Pol::D / 16;
 #pragma unroll
@@ -405,7 +413,7 @@ __device__ __forceinline__ void dkv_stage(f32x4 (&accK)[Pol::D / 16][KT], f32x4 
         for (int t = 0; t < 2; ++t) {
             // block rows bidx(t, g, 0..3) are consecutive: one 16-byte LDS read
             const int q4 = 32 * blk + Pol::bidx(t, g, 0);
-            const f32x4 nl = *reinterpret_cast<const f32x4 *>(sl + q4) * -kLog2e;
+            const f32x4 nl = *reinterpret_cast<const f32x4 *>(sl + q4) * lmul;
             const f32x4 dl = *reinterpret_cast<const f32x4 *>(sd + q4);
             Frag a[NC];
             const int n = 32 * blk + Pol::arow(t, l16);
@@ -438,7 +446,7 @@ __device__ __forceinline__ void dkv_stage(f32x4 (&accK)[Pol::D / 16][KT], f32x4 
                         const bool before = Pol::bidx(t, g, r) - l16 < kw0 - qs + 16 * kt - 32 * blk;
                         x = before ? -INFINITY : x;
                     }
-                    const float pv = fast_exp2(x);
+                    const float pv = fast_exp2(Pol::kExactScale ? x * xmul : x);
                     s[t][kt][r] = pv;
                     dp[t][kt][r] = pv * dp[t][kt][r];  // -dS / scale
                 }
@@ -501,10 +509,12 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDkv) void dkv_kernel(Params p) 
         Pol::gmem_row_frags(vf[kt], V + (size_t)key * D, g, key < N);
 #pragma unroll
         for (int kc = 0; kc < NC; ++kc) {
-            kf[kt][kc] = Pol::scaled(kf[kt][kc], p.scale_log2);
+            if (!Pol::kExactScale) kf[kt][kc] = Pol::scaled(kf[kt][kc], p.scale_log2);
             vf[kt][kc] = Pol::neg(vf[kt][kc]);
         }
     }
+    const float lmul = Pol::kExactScale ? -1.0f / p.scale : -kLog2e;
+    const float xmul = p.scale_log2;
     f32x4 accK[XT][KT], accV[XT][KT];
 #pragma unroll
     for (int xt = 0; xt < XT; ++xt) {
@@ -558,7 +568,7 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDkv) void dkv_kernel(Params p) 
         // a wave whose keys all follow the stage's queries has nothing to do
         if (!CAUSAL || qs + BQ - 1 >= kw0) {
             dkv_stage<Pol, KT, CAUSAL, MASK>(accK, accV, kf, vf, sQ[cur], sdO[cur], sL[cur], sD[cur], qs, kw0, N, g,
-                                             l16);
+                                             l16, lmul, xmul);
         }
         if (NBUF > 2 && ahead) {
             wait_vmcnt<kLoads>();
@@ -574,7 +584,8 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDkv) void dkv_kernel(Params p) 
         constexpr int B = decltype(buf)::value;
         if (st + 1 < nsteps) issue(st + 1);
         const int qs = qstart + i * BQ;
-        dkv_stage<Pol, KT, CAUSAL, false>(accK, accV, kf, vf, sQ[B], sdO[B], sL[B], sD[B], qs, kw0, N, g, l16);
+        dkv_stage<Pol, KT, CAUSAL, false>(accK, accV, kf, vf, sQ[B], sdO[B], sL[B], sD[B], qs, kw0, N, g, l16, lmul,
+                                          xmul);
         wait_stage();
         barrier_lds();
     };
@@ -710,10 +721,12 @@ __global__ __launch_bounds__(512) void dkv_pp_kernel(Params p) {
         Pol::gmem_row_frags(vf[kt], V + (size_t)key * D, g, key < N);
 #pragma unroll
         for (int kc = 0; kc < 2; ++kc) {
-            kf[kt][kc] = Pol::scaled(kf[kt][kc], p.scale_log2);
+            if (!Pol::kExactScale) kf[kt][kc] = Pol::scaled(kf[kt][kc], p.scale_log2);
             vf[kt][kc] = Pol::neg(vf[kt][kc]);
         }
     }
+    const float lmul = Pol::kExactScale ? -1.0f / p.scale : -kLog2e;
+    const float xmul = p.scale_log2;
     f32x4 accK[XT][KT], accV[XT][KT];
 #pragma unroll
     for (int xt = 0; xt < XT; ++xt) {
@@ -785,19 +798,19 @@ __global__ __launch_bounds__(512) void dkv_pp_kernel(Params p) {
         const int moff = kw0 - (qstart + i * BQ + blk);
         pp::chain_operands<Pol>(cdo, cq, tq(bf), tdo(bf), blk, g, l16);
         if (CAUSAL && moff >= 0) {
-            pp::softmax_block<Pol, true>(s, dp, cp, cds, moff, g, l16);
+            pp::softmax_block<Pol, true>(s, dp, cp, cds, moff, g, l16, xmul);
         } else {
-            pp::softmax_block<Pol, false>(s, dp, cp, cds, 0, g, l16);
+            pp::softmax_block<Pol, false>(s, dp, cp, cds, 0, g, l16, xmul);
         }
     };
     auto m_phase = [&](int st) __attribute__((always_inline)) {
         const int cb = st % NBUF;
-        pp::score_operands<Pol>(so, tq(cb), tdo(cb), vl(cb), vd(cb), blk, g, l16);
+        pp::score_operands<Pol>(so, tq(cb), tdo(cb), vl(cb), vd(cb), blk, g, l16, lmul);
         pp::chain_block<Pol>(accK, accV, cp, cds, cdo, cq);
         pp::score_block<Pol>(s, dp, kf, vf, so);
     };
     auto first_scores = [&]() __attribute__((always_inline)) {
-        pp::score_operands<Pol>(so, tq(0), tdo(0), vl(0), vd(0), blk, g, l16);
+        pp::score_operands<Pol>(so, tq(0), tdo(0), vl(0), vd(0), blk, g, l16, lmul);
         pp::score_block<Pol>(s, dp, kf, vf, so);
     };
 

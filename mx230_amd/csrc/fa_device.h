@@ -125,6 +125,13 @@ struct PolBF16 {
     // faster than two. At d = 128 all three kernels run two waves per SIMD
     // (dK/dV is held there by its 66 KB of LDS; the non-causal forward spills
     // 64 bytes per lane at two and still ran 22% faster than at one).
+    // The register-resident operand of each score GEMM (Q in the forward and
+    // the dQ pass, K in the dK/dV pass) stays as given and the fp32 scores are
+    // multiplied by scale log2(e) (one v_mul per score): rounding the scaled
+    // operand to bf16 instead puts an error of about |S log2(e)| 2^-9 into
+    // every exponent, correlated along a row or a key, which grows with the
+    // logits and reaches the outputs through LSE.
+    static constexpr bool kExactScale = true;
     static constexpr int kWaves = 2;
     static constexpr int kWavesFwdCausal = D == 64 ? 3 : 2;
     static constexpr int kWavesDq = D == 64 ? 3 : 2;
@@ -252,6 +259,8 @@ struct PolF32 {
     static constexpr int EPC = 4;
     static constexpr int NC = D / 4;
     static constexpr int ROWS = 64;
+    // fp32 operands: the scale folds into the operand with a 2^-24 rounding
+    static constexpr bool kExactScale = false;
     static constexpr int kWaves = 1;
     static constexpr int kWavesFwdCausal = 1;
     static constexpr int kWavesDq = 1;

@@ -12,9 +12,11 @@
 //     cross-lane reduction (two permlane swaps);
 //   * the output is accumulated transposed, O^T = V^T P^T, so the per-query
 //     rescale factor is a per-lane scalar as well;
-//   * exponentials are base 2 with log2(e) folded into the scale;
+//   * exponentials are base 2: the fp32 scores are multiplied by
+//     scale log2(e) (bf16, which keeps Q exact) or Q is (fp32);
 //   * after the first stage the running max is only raised (and O and the sum
-//     rescaled) when a score exceeds it by a factor above 2^8 (fwd_stage_lazy);
+//     rescaled) when some p of a row exceeds 2^16 (fwd_stage_lazy), detected
+//     from the per-lane row sums without computing a row maximum;
 //   * only stages that straddle the causal diagonal or the end of the sequence
 //     run the masking code (a separate instantiation of the stage body).
 #include <type_traits>
@@ -24,14 +26,15 @@
 
 namespace mxfa {
 
-// One 64-key stage for one wave: scores (in log2 units: qf holds Q scale
-// log2(e)), online-softmax update, O^T += V^T P^T.
+// One 64-key stage for one wave: scores in log2 units (x xmul when Q is kept
+// exact, else qf holds Q scale log2(e)), online-softmax update,
+// O^T += V^T P^T.
 // qpos0: position of the wave's first query row; Nk: key rows.
 template <class Pol, bool CAUSAL, bool MASK>
 __device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][2], float (&m)[2], float (&lsum)[2],
                                           const typename Pol::Frag (&qf)[2][Pol::NC],
                                           const typename Pol::T *sk, const typename Pol::T *sv, int k0, int qpos0,
-                                          int Nk, int g, int l16) {
+                                          int Nk, int g, int l16, float xmul) {
     using Frag = typename Pol::Frag;
     constexpr int NC = Pol::NC, XT = Pol::D / 16;
     f32x4 s[2][2][2];  // [block][t][qt]
@@ -60,7 +63,7 @@ __device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][2], float (&
             for (int t = 0; t < 2; ++t) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    float v = s[blk][t][qt][r];
+                    float v = Pol::kExactScale ? s[blk][t][qt][r] * xmul : s[blk][t][qt][r];
                     if constexpr (MASK) {
                         const int key = k0 + 32 * blk + Pol::bidx(t, g, r);
                         v = (key >= Nk || (CAUSAL && key > qpos)) ? -INFINITY : v;
@@ -106,25 +109,32 @@ __device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][2], float (&
 
 // fwd_stage for every stage after the first, with lazy rescaling. Key 0 is
 // visible to every query (pos0 >= 0), so after the first stage m is finite for
-// every row. The scores come out of the MFMAs relative to the running max (the
-// accumulators start at -m), and m, O and the sum are only rescaled when some
-// score of the wave exceeds its row's m by more than kLazy (log2 units).
-// Otherwise p = 2^(s - m) with the old m, so p <= 2^kLazy: m never exceeds the
-// row's true running max and never falls more than kLazy below it, so the
-// largest p of each row lies in [1, 2^kLazy] and neither it nor the fp32 sum
-// can overflow or underflow. The result is the online softmax's up to
-// rounding, since LSE = m + log2(l) holds for any m used consistently.
-constexpr float kLazy = 8.0f;
+// every row. The scores come out of the MFMAs relative to the running max m
+// (the accumulators start at -m), and p = 2^(s - m) is taken optimistically
+// with the old m. A lane's per-row sum of its p over the stage (16 keys)
+// bounds each of them, so when no such sum exceeds kLazySum no p does either:
+// O and the row sums then simply accumulate (m stays within log2(kLazySum) of
+// the row's true running max, so nothing overflows or underflows in fp32 and
+// the largest p of a row stays in [1, kLazySum]). Otherwise (an overflow shows
+// as an infinite sum) the stage is redone exactly: the scores are recomputed
+// from LDS, m rises to the row's max, O and the sum are rescaled, and the
+// exponentials are taken again. LSE = m + log2(l) holds for any m used
+// consistently, so the result is the online softmax's up to rounding. No row
+// maximum is computed on the common path.
+constexpr float kLazySum = 65536.0f;
 
+// Scores of one 64-key stage relative to m: s = K Q^T scale log2(e) - m, with
+// masked keys (MASK) at -inf. With Pol::kExactScale the accumulators start at
+// -m / xmul and the fp32 result is multiplied by xmul = scale log2(e).
 template <class Pol, bool CAUSAL, bool MASK>
-__device__ __forceinline__ void fwd_stage_lazy(f32x4 (&acc)[Pol::D / 16][2], float (&m)[2], float (&lsum)[2],
-                                               const typename Pol::Frag (&qf)[2][Pol::NC],
-                                               const typename Pol::T *sk, const typename Pol::T *sv, int k0,
-                                               int qpos0, int Nk, int g, int l16) {
+__device__ __forceinline__ void fwd_scores(f32x4 (&s)[2][2][2], const float (&m)[2],
+                                           const typename Pol::Frag (&qf)[2][Pol::NC], const typename Pol::T *sk,
+                                           int k0, int qpos0, int Nk, int g, int l16, float xmul) {
     using Frag = typename Pol::Frag;
-    constexpr int NC = Pol::NC, XT = Pol::D / 16;
-    f32x4 s[2][2][2];  // [block][t][qt]
-    const f32x4 nm[2] = {f32x4{-m[0], -m[0], -m[0], -m[0]}, f32x4{-m[1], -m[1], -m[1], -m[1]}};
+    constexpr int NC = Pol::NC;
+    const float im = Pol::kExactScale ? 1.0f / xmul : 1.0f;
+    const float n0 = -m[0] * im, n1 = -m[1] * im;
+    const f32x4 nm[2] = {f32x4{n0, n0, n0, n0}, f32x4{n1, n1, n1, n1}};
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
 #pragma unroll
@@ -136,58 +146,34 @@ __device__ __forceinline__ void fwd_stage_lazy(f32x4 (&acc)[Pol::D / 16][2], flo
                 f32x4 c = nm[qt];
 #pragma unroll
                 for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], qf[qt][kc], c);
-                s[blk][t][qt] = c;
+                s[blk][t][qt] = Pol::kExactScale ? c * xmul : c;
             }
         }
     }
-    float mx[2];
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-        const int qpos = qpos0 + 16 * qt + l16;
-        float v = -INFINITY;
-#pragma unroll
-        for (int blk = 0; blk < 2; ++blk) {
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    float x = s[blk][t][qt][r];
-                    if constexpr (MASK) {
-                        const int key = k0 + 32 * blk + Pol::bidx(t, g, r);
-                        x = (key >= Nk || (CAUSAL && key > qpos)) ? -INFINITY : x;
-                        s[blk][t][qt][r] = x;
-                    }
-                    v = fmaxf(v, x);
-                }
-            }
-        }
-        mx[qt] = xg_max(v);
-    }
-    if (__builtin_amdgcn_ballot_w64(mx[0] > kLazy || mx[1] > kLazy) != 0) {
-        // some row of the wave moved up by more than kLazy: rescale (rows whose
-        // max did not rise keep shift 0) and shift its scores in place, so the
-        // exponentials below serve both cases from the same registers
+    if constexpr (MASK) {
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt) {
-            const float shift = fmaxf(mx[qt], 0.f);
-            const float corr = fast_exp2(-shift);
-            m[qt] += shift;
-#pragma unroll
-            for (int xt = 0; xt < XT; ++xt) acc[xt][qt] *= corr;
-            lsum[qt] *= corr;
+            const int qpos = qpos0 + 16 * qt + l16;
 #pragma unroll
             for (int blk = 0; blk < 2; ++blk) {
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) s[blk][t][qt][r] -= shift;
+                    for (int r = 0; r < 4; ++r) {
+                        const int key = k0 + 32 * blk + Pol::bidx(t, g, r);
+                        if (key >= Nk || (CAUSAL && key > qpos)) s[blk][t][qt][r] = -INFINITY;
+                    }
                 }
             }
         }
     }
+}
+
+// p = 2^s in place, added to l (row qt of this lane).
+__device__ __forceinline__ void fwd_exp_sum(f32x4 (&s)[2][2][2], float (&l)[2]) {
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
-        float ls = lsum[qt];
+        float ls = l[qt];
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
 #pragma unroll
@@ -200,7 +186,51 @@ __device__ __forceinline__ void fwd_stage_lazy(f32x4 (&acc)[Pol::D / 16][2], flo
                 }
             }
         }
-        lsum[qt] = ls;
+        l[qt] = ls;
+    }
+}
+
+template <class Pol, bool CAUSAL, bool MASK>
+__device__ __forceinline__ void fwd_stage_lazy(f32x4 (&acc)[Pol::D / 16][2], float (&m)[2], float (&lsum)[2],
+                                               const typename Pol::Frag (&qf)[2][Pol::NC],
+                                               const typename Pol::T *sk, const typename Pol::T *sv, int k0,
+                                               int qpos0, int Nk, int g, int l16, float xmul) {
+    constexpr int XT = Pol::D / 16;
+    f32x4 s[2][2][2];  // [block][t][qt]
+    fwd_scores<Pol, CAUSAL, MASK>(s, m, qf, sk, k0, qpos0, Nk, g, l16, xmul);
+    const float l0[2] = {lsum[0], lsum[1]};
+    fwd_exp_sum(s, lsum);
+    if (__builtin_amdgcn_ballot_w64(lsum[0] > l0[0] + kLazySum || lsum[1] > l0[1] + kLazySum) != 0) {
+        // some p of the wave exceeded kLazySum: redo the stage with m raised to
+        // each row's max (rows whose max did not rise keep shift 0)
+        fwd_scores<Pol, CAUSAL, MASK>(s, m, qf, sk, k0, qpos0, Nk, g, l16, xmul);
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+            float v = -INFINITY;
+#pragma unroll
+            for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) v = fmaxf(v, s[blk][t][qt][r]);
+                }
+            }
+            const float shift = fmaxf(xg_max(v), 0.f);
+            const float corr = fast_exp2(-shift);
+            m[qt] += shift;
+#pragma unroll
+            for (int xt = 0; xt < XT; ++xt) acc[xt][qt] *= corr;
+            lsum[qt] = l0[qt] * corr;
+#pragma unroll
+            for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) s[blk][t][qt][r] -= shift;
+                }
+            }
+        }
+        fwd_exp_sum(s, lsum);
     }
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
@@ -246,9 +276,12 @@ __global__ __launch_bounds__(256, WPS) void fwd_kernel(Params p) {
     for (int qt = 0; qt < 2; ++qt) {
         const int qi = q0 + 16 * qt + l16;
         Pol::gmem_row_frags(qf[qt], Q + (size_t)qi * p.q_rs, g, qi < N);
-        // Q scale log2(e): the scores come out of the MFMAs in log2 units
+        // fp32: Q scale log2(e), so the scores come out of the MFMAs in log2
+        // units; bf16 keeps Q exact and scales the fp32 scores instead
 #pragma unroll
-        for (int kc = 0; kc < NC; ++kc) qf[qt][kc] = Pol::scaled(qf[qt][kc], p.scale_log2);
+        for (int kc = 0; kc < NC; ++kc) {
+            if (!Pol::kExactScale) qf[qt][kc] = Pol::scaled(qf[qt][kc], p.scale_log2);
+        }
     }
     f32x4 acc[XT][2];
 #pragma unroll
@@ -273,9 +306,9 @@ __global__ __launch_bounds__(256, WPS) void fwd_kernel(Params p) {
         constexpr int B = decltype(buf)::value;
         if (st + 1 < nsteps) stage_kv<Pol>(sK[B ^ 1], sV[B ^ 1], K, V, (st + 1) * BK, Nk, plan, wave, p.kv_rs);
         if constexpr (decltype(first)::value) {
-            fwd_stage<Pol, CAUSAL, false>(acc, m, lsum, qf, sK[B], sV[B], st * BK, qpos0, Nk, g, l16);
+            fwd_stage<Pol, CAUSAL, false>(acc, m, lsum, qf, sK[B], sV[B], st * BK, qpos0, Nk, g, l16, p.scale_log2);
         } else {
-            fwd_stage_lazy<Pol, CAUSAL, false>(acc, m, lsum, qf, sK[B], sV[B], st * BK, qpos0, Nk, g, l16);
+            fwd_stage_lazy<Pol, CAUSAL, false>(acc, m, lsum, qf, sK[B], sV[B], st * BK, qpos0, Nk, g, l16, p.scale_log2);
         }
         wait_stage();
         __syncthreads();
@@ -299,9 +332,9 @@ __global__ __launch_bounds__(256, WPS) void fwd_kernel(Params p) {
         // a wave whose queries all precede the stage's keys has nothing to do
         if (!CAUSAL || k0 <= qpos0 + 31) {
             if (st == 0) {
-                fwd_stage<Pol, CAUSAL, true>(acc, m, lsum, qf, sK[cur], sV[cur], k0, qpos0, Nk, g, l16);
+                fwd_stage<Pol, CAUSAL, true>(acc, m, lsum, qf, sK[cur], sV[cur], k0, qpos0, Nk, g, l16, p.scale_log2);
             } else {
-                fwd_stage_lazy<Pol, CAUSAL, true>(acc, m, lsum, qf, sK[cur], sV[cur], k0, qpos0, Nk, g, l16);
+                fwd_stage_lazy<Pol, CAUSAL, true>(acc, m, lsum, qf, sK[cur], sV[cur], k0, qpos0, Nk, g, l16, p.scale_log2);
             }
         }
         wait_stage();

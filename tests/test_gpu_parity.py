@@ -52,6 +52,35 @@ def test_reference_verify_fwd_n512(causal):
     assert oracle.allclose_err(gpu[0], ref[0], 1e-3, 1e-4) < 1.0
 
 
+# ------------------------------------------------ running max that rises --
+
+def _rising(bf16, div):
+    """Key j scaled by (0.5 + j / div): a row's scores grow along the keys, so
+    later 64-key stages exceed the running max by more than the forward's lazy
+    bound (2^16, i.e. 16 in log2 units) and take its exact rescaling path."""
+    q, k, v, do = make_inputs(1, 2, 2, 300, 64, bf16=bf16, seeds=(61, 62, 63, 64))
+    grow = (0.5 + np.arange(300, dtype=np.float32) / div)[None, None, :, None]
+    k = (k * grow).astype(np.float32)
+    if bf16:
+        k = oracle.bf16_round(k)
+    return q, k, v, do
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("bf16", [False, True], ids=["f32", "bf16"])
+@pytest.mark.parametrize("div", [64.0, 16.0], ids=["mild", "steep"])
+def test_running_max_rises(causal, bf16, div):
+    """Scores up to ~22 (mild) or ~80 (steep) in natural-log units, the max of
+    a row rising by up to 27 / 104 (log2) after the first stage, so the
+    forward's exact rescaling path runs in nearly every wave, masked and
+    unmasked (N = 300 is ragged). With bf16 this also checks that the kernels
+    keep the score GEMMs' register operands exact and scale the fp32 scores:
+    rounding a scale log2(e)-scaled operand to bf16 misses the oracle by
+    2-8e-2 at the steep scores."""
+    q, k, v, do = _rising(bf16, div)
+    _check("max-rises", q, k, v, do, causal, bf16)
+
+
 # ---------------------------------------------------------------- goldens --
 
 @pytest.mark.parametrize("path", golden_cases(), ids=lambda p: p.split("/")[-1][:-4])
