@@ -161,25 +161,29 @@ __device__ __forceinline__ void dq_stage(f32x4 (&acc)[Pol::D / 16][QT], const ty
 // DELTA: compute Delta_i = sum_x dO[i,x] O[i,x] here (O from p.o_in, the
 // same fp32 products as preprocess_kernel, summed in another order) and write
 // it to p.delta for the dK/dV pass, instead of reading it from there.
+// LDS of a dQ work-group: double-buffered K and V tiles.
+template <class Pol>
+struct DqSmem {
+    __attribute__((aligned(16))) typename Pol::T sK[2][Pol::ROWS * Pol::D];
+    __attribute__((aligned(16))) typename Pol::T sV[2][Pol::ROWS * Pol::D];
+};
+
+// The dQ work of query block qb (16 QT NW rows) of (batch, query head) bh.
 // QT: 16-query tiles per wave; NW: waves per work-group.
 template <class Pol, bool CAUSAL, int NW, bool DELTA, int QT>
-__global__ __launch_bounds__(64 * NW, Pol::kWavesDq) void dq_kernel(Params p) {
+__device__ __forceinline__ void dq_body(const Params &p, int bh, int qb, DqSmem<Pol> &sm) {
     using T = typename Pol::T;
     using Frag = typename Pol::Frag;
     constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
     constexpr int BQ = 16 * QT * NW, BK = Pol::ROWS, NT = 64 * NW;
     static_assert(BQ % BK == 0, "causal: the masked tail is the work-group's BQ / BK diagonal stages");
-
-    __shared__ __attribute__((aligned(16))) T sK[2][BK * D];
-    __shared__ __attribute__((aligned(16))) T sV[2][BK * D];
+    auto &sK = sm.sK;
+    auto &sV = sm.sV;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, l16 = lane & 15;
     const int N = p.N;
-    const int bh = blockIdx.x;
-    const int nqb = (N + BQ - 1) / BQ;
-    const int qb = CAUSAL ? (nqb - 1 - (int)blockIdx.y) : (int)blockIdx.y;
     const int b = bh / p.Hq, h = bh % p.Hq, kvh = h / p.group;
     const T *Q = static_cast<const T *>(p.q) + (size_t)bh * N * D;
     const T *dO = static_cast<const T *>(p.dout) + (size_t)bh * N * D;
@@ -275,6 +279,15 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDq) void dq_kernel(Params p) {
             for (int xt = 0; xt < XT; ++xt) store4<T>(dQ + (size_t)qi * D + 16 * xt + 4 * g, acc[xt][qt], -p.scale);
         }
     }
+}
+
+// Causal: query blocks from the last (the most keys) to the first.
+template <class Pol, bool CAUSAL, int NW, bool DELTA, int QT>
+__global__ __launch_bounds__(64 * NW, Pol::kWavesDq) void dq_kernel(Params p) {
+    __shared__ DqSmem<Pol> sm;
+    const int nqb = (p.N + 16 * QT * NW - 1) / (16 * QT * NW);
+    const int qb = CAUSAL ? (nqb - 1 - (int)blockIdx.y) : (int)blockIdx.y;
+    dq_body<Pol, CAUSAL, NW, DELTA, QT>(p, blockIdx.x, qb, sm);
 }
 
 // ---------------------------------------------------------------- dK/dV pass
@@ -469,8 +482,21 @@ __device__ __forceinline__ void dkv_stage(f32x4 (&accK)[Pol::D / 16][KT], f32x4 
     }
 }
 
+// LDS of a dK/dV work-group: an NBUF-deep ring of Q / dO tiles and their
+// LSE / Delta rows (loads are issued NBUF - 1 stages ahead).
+template <class Pol>
+struct DkvSmem {
+    static constexpr int NBUF = Pol::kDkvBuffers;
+    __attribute__((aligned(16))) typename Pol::T sQ[NBUF][Pol::ROWS * Pol::D];
+    __attribute__((aligned(16))) typename Pol::T sdO[NBUF][Pol::ROWS * Pol::D];
+    __attribute__((aligned(16))) float sL[NBUF][Pol::ROWS];
+    __attribute__((aligned(16))) float sD[NBUF][Pol::ROWS];
+};
+
+// The dK/dV work of key block kb (16 KT NW keys) of grid column bx =
+// (batch, KV head) * dkv_split + share.
 template <class Pol, int KT, bool CAUSAL, int NW>
-__global__ __launch_bounds__(64 * NW, Pol::kWavesDkv) void dkv_kernel(Params p) {
+__device__ __forceinline__ void dkv_body(const Params &p, int bx, int kb, DkvSmem<Pol> &sm) {
     using T = typename Pol::T;
     using Frag = typename Pol::Frag;
     constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
@@ -478,22 +504,19 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDkv) void dkv_kernel(Params p) 
     constexpr int BKV = 16 * KT * NW; // keys per workgroup
     constexpr int BQ = Pol::ROWS;     // queries per stage
     static_assert(BKV % BQ == 0, "causal start must align to a stage");
-
-    // NBUF-deep ring of stages: loads are issued NBUF-1 stages ahead
-    constexpr int NBUF = Pol::kDkvBuffers;
-    __shared__ __attribute__((aligned(16))) T sQ[NBUF][BQ * D];
-    __shared__ __attribute__((aligned(16))) T sdO[NBUF][BQ * D];
-    __shared__ __attribute__((aligned(16))) float sL[NBUF][BQ];
-    __shared__ __attribute__((aligned(16))) float sD[NBUF][BQ];
+    constexpr int NBUF = DkvSmem<Pol>::NBUF;
+    auto &sQ = sm.sQ;
+    auto &sdO = sm.sdO;
+    auto &sL = sm.sL;
+    auto &sD = sm.sD;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, l16 = lane & 15;
     const int N = p.N;
     const int nsplit = p.dkv_split;
-    const int bkv = blockIdx.x / nsplit;       // b * Hkv + kvh
-    const int sp = blockIdx.x - bkv * nsplit;  // which share of the group's query heads
-    const int kb = blockIdx.y;   // causal: block 0 (most queries) is dispatched first
+    const int bkv = bx / nsplit;       // b * Hkv + kvh
+    const int sp = bx - bkv * nsplit;  // which share of the group's query heads
     const int b = bkv / p.Hkv, kvh = bkv % p.Hkv;
     const int h0 = sp * p.group / nsplit, nh = (sp + 1) * p.group / nsplit - h0;
     const size_t kvoff = (size_t)bkv * N * D;
@@ -640,6 +663,13 @@ __global__ __launch_bounds__(64 * NW, Pol::kWavesDkv) void dkv_kernel(Params p) 
             }
         }
     }
+}
+
+// Causal: key block 0 (the most queries) is dispatched first.
+template <class Pol, int KT, bool CAUSAL, int NW>
+__global__ __launch_bounds__(64 * NW, Pol::kWavesDkv) void dkv_kernel(Params p) {
+    __shared__ DkvSmem<Pol> sm;
+    dkv_body<Pol, KT, CAUSAL, NW>(p, blockIdx.x, blockIdx.y, sm);
 }
 
 // dK / dV of a split dK/dV pass: the sum of the nsplit fp32 partial planes in
