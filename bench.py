@@ -48,6 +48,9 @@ def parse():
     ap.add_argument("--causal", type=int, default=1)
     ap.add_argument("--dtype", choices=["bf16", "f32"], default="bf16")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--two-launch", action="store_true",
+                    help="time the two-launch backward (dQ pass with Delta, then dK/dV) even where one "
+                         "launch is available (sets MXFA_BWD_FUSED=0)")
     ap.add_argument("--separate-delta", action="store_true",
                     help="run the reference-shaped sequence (preprocess launch, then the dQ pass reading Delta)")
     ap.add_argument("--no-probe", action="store_true",
@@ -379,33 +382,42 @@ def main():
     torch.cuda.synchronize()
     fwd_avg = sum(x.elapsed_time(y) for x, y in fwd_ms) / len(fwd_ms)
 
-    def step(evs=None):
-        # the backward from O (mxfa_run_bwd): the dQ pass computes Delta
-        # itself and writes it for the dK/dV pass; with --separate-delta the
-        # reference-shaped preprocess launch runs first instead. evs: events
-        # recorded on the launch stream before each launch and after the last.
-        i = 0
-        if a.separate_delta:
+    if a.two_launch:
+        os.environ["MXFA_BWD_FUSED"] = "0"
+    # the backward from O as mxfa_run_bwd runs it: one launch (dQ work-groups
+    # publish Delta for the dK/dV work-groups of the same launch) where
+    # available, else the dQ pass with Delta then the dK/dV pass; with
+    # --separate-delta the reference-shaped sequence preprocess, dQ, dK/dV
+    one = not a.separate_delta and mx.bwd_one_launch(q, k, causal)
+    if a.separate_delta:
+        launches = [("preprocess", lambda: mx.run_preprocess(do, o, delta)),
+                    ("dq", lambda: mx.run_bwd_dq(q, k, v, do, lse, delta, dq, causal)),
+                    ("dkv", lambda: mx.run_bwd_dkv(q, k, v, do, lse, delta, dk, dv, causal))]
+    elif one:
+        launches = [("bwd", lambda: mx.run_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, causal))]
+    else:
+        launches = [("dq", lambda: mx.run_bwd_dq_delta(q, k, v, o, do, lse, delta, dq, causal)),
+                    ("dkv", lambda: mx.run_bwd_dkv(q, k, v, do, lse, delta, dk, dv, causal))]
+
+    def step(seq, evs=None):
+        # evs: events recorded on the launch stream before each launch and after the last
+        for j, (_, launch) in enumerate(seq):
             if evs:
-                evs[i].record(stream)
-                i += 1
-            mx.run_preprocess(do, o, delta)
+                evs[j].record(stream)
+            launch()
         if evs:
-            evs[i].record(stream)
-            i += 1
-        if a.separate_delta:
-            mx.run_bwd_dq(q, k, v, do, lse, delta, dq, causal)
-        else:
-            mx.run_bwd_dq_delta(q, k, v, o, do, lse, delta, dq, causal)
-        if evs:
-            evs[i].record(stream)
-            i += 1
-        mx.run_bwd_dkv(q, k, v, do, lse, delta, dk, dv, causal)
-        if evs:
-            evs[i].record(stream)
+            evs[len(seq)].record(stream)
+
+    def per_launch_ms(seq):
+        evsets = [[torch.cuda.Event(enable_timing=True) for _ in range(len(seq) + 1)] for _ in range(a.steps)]
+        torch.cuda.synchronize()
+        for evs in evsets:
+            step(seq, evs)
+        torch.cuda.synchronize()
+        return {n: sum(evs[j].elapsed_time(evs[j + 1]) for evs in evsets) / a.steps for j, (n, _) in enumerate(seq)}
 
     for _ in range(a.warmup):
-        step()
+        step(launches)
     torch.cuda.synchronize()
 
     # timed region: exactly K backward steps, synchronised on both sides, timed
@@ -416,20 +428,19 @@ def main():
     torch.cuda.synchronize()
     t0.record(stream)
     for _ in range(a.steps):
-        step()
+        step(launches)
     t1.record(stream)
     torch.cuda.synchronize()
     ms_per_step = t0.elapsed_time(t1) / a.steps
 
     # second timed region of K steps with events between the launches: each
-    # kernel's average duration on the same stream (the roofline's basis)
-    names = (["preprocess"] if a.separate_delta else []) + ["dq", "dkv"]
-    evsets = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)] for _ in range(a.steps)]
-    torch.cuda.synchronize()
-    for evs in evsets:
-        step(evs)
-    torch.cuda.synchronize()
-    kern = {n: sum(evs[j].elapsed_time(evs[j + 1]) for evs in evsets) / a.steps for j, n in enumerate(names)}
+    # launch's average duration on the same stream (the roofline's basis)
+    kern = per_launch_ms(launches)
+    # the two passes on their own (two launches), for the breakdown
+    passes = None
+    if one:
+        passes = per_launch_ms([("dq", lambda: mx.run_bwd_dq_delta(q, k, v, o, do, lse, delta, dq, causal)),
+                                ("dkv", lambda: mx.run_bwd_dkv(q, k, v, do, lse, delta, dk, dv, causal))])
 
     half = 0.5 if causal else 1.0
     bwd_flops = mx.bwd_flops(a.B, a.H, a.N, a.d, causal)
@@ -438,7 +449,10 @@ def main():
     # S, dP, dQ products (6 N^2 d) -- S and dP are recomputed by both passes
     kflops = {"dkv": 8.0 * a.N * a.N * a.d * a.B * a.H * half,
               "dq": 6.0 * a.N * a.N * a.d * a.B * a.H * half}
-    dom = max(("dkv", "dq"), key=lambda n: kern[n])
+    executed = kflops["dkv"] + kflops["dq"]
+    # the one launch does the algorithmic backward (10 N^2 d) and executes 14
+    kflops["bwd"] = bwd_flops
+    dom = max((n for n in kern if n in kflops), key=lambda n: kern[n])
     peak = PEAK_TFLOPS[a.dtype]
     achieved = kflops[dom] / (kern[dom] * 1e-3) / 1e12
     value = bwd_flops / (ms_per_step * 1e-3) / 1e12
@@ -453,21 +467,28 @@ def main():
         "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": a.dtype,
         "data": "synthetic (seeded N(0,1) on the GPU)",
-        "config": {"workload": "flash-attention backward (dQ with Delta folded in + dK/dV), fwd outside timing"
-                   if not a.separate_delta else
-                   "flash-attention backward (preprocess + dQ + dK/dV), fwd outside timing",
+        "config": {"workload": ("flash-attention backward, one launch (dQ with Delta + dK/dV), fwd outside timing"
+                                if one else
+                                "flash-attention backward (dQ with Delta folded in + dK/dV), fwd outside timing"
+                                if not a.separate_delta else
+                                "flash-attention backward (preprocess + dQ + dK/dV), fwd outside timing"),
                    "B": a.B, "Hq": a.H, "Hkv": hkv, "N": a.N, "d": a.d, "causal": causal,
                    "parallelism": "single GPU"},
         "pct_peak": round(100.0 * value / peak, 2),
         # MFMA work the two passes execute per step (the dQ pass recomputes S
         # and dP: 14 N^2 d per (batch, head), halved when causal) over the step
-        "executed_tflops": round((kflops["dkv"] + kflops["dq"]) / (ms_per_step * 1e-3) / 1e12, 2),
+        "executed_tflops": round(executed / (ms_per_step * 1e-3) / 1e12, 2),
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2), "peak": peak,
                      "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic},
         "kernels_ms": {n: round(t, 4) for n, t in kern.items()},
         "fwd": {"ms": round(fwd_avg, 4),
                 "tflops": round(mx.fwd_flops(a.B, a.H, a.N, a.d, causal) / (fwd_avg * 1e-3) / 1e12, 2)},
     }
+    if dom == "bwd":
+        # the one launch executes 14 N^2 d (the dQ pass recomputes S and dP)
+        res["roofline"]["executed"] = round(executed / (kern[dom] * 1e-3) / 1e12, 2)
+    if passes is not None:
+        res["passes_ms"] = {n: round(t, 4) for n, t in passes.items()}
     if not a.no_probe:
         # measured ceilings (probe kernels, after the timed region): the same
         # MFMA pipe at full occupancy with independent accumulators, and HBM

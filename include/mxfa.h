@@ -138,6 +138,18 @@ int mxfa_run_bwd(const mxfa_shape *shape, const void *q, const void *k, const vo
                  const void *dout, const float *lse, float *delta, void *dq, void *dk, void *dv,
                  void *stream);
 
+/* 1 if mxfa_run_bwd (and mxfa_run_bwd_ws without a split) runs the backward
+ * as one launch for this shape, else 0 (two launches, or an invalid shape).
+ * The one-launch form (bf16, d = 64 or 128) runs the dQ work-groups first;
+ * they publish Delta per 128-row query block, and the dK/dV work-groups of the
+ * same launch wait for the blocks they need. Each wait is bounded: after it the
+ * work-group computes those Delta rows from O and dO itself. Results equal the
+ * two-launch form's bitwise whenever no wait runs out. The environment
+ * variable MXFA_BWD_FUSED=0, read on every call, selects two launches.
+ * No counterpart in the reference: it tells callers (and benchmarks) which
+ * kernels the backward from O (main.rs:126-143, :179-210) becomes. */
+int mxfa_bwd_one_launch(const mxfa_shape *shape);
+
 /* Bytes of device workspace the _ws entry points below can use (0 for an
  * invalid shape). dQ is a separate atomic-free pass and needs none. With GQA
  * (Hq > Hkv), when the key blocks alone would leave the GPU underfilled, the

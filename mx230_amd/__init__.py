@@ -44,7 +44,7 @@ STATUS = {
 EXPORTS = (
     "mxfa_version", "mxfa_strerror", "mxfa_init", "mxfa_shutdown", "mxfa_check_shape",
     "mxfa_run_flash", "mxfa_run_flash_lse", "mxfa_run_preprocess", "mxfa_run_bwd_dq",
-    "mxfa_run_bwd_dkv", "mxfa_run_bwd_flash", "mxfa_run_bwd_dq_delta", "mxfa_run_bwd", "mxfa_bwd_workspace_bytes",
+    "mxfa_run_bwd_dkv", "mxfa_run_bwd_flash", "mxfa_run_bwd_dq_delta", "mxfa_run_bwd", "mxfa_bwd_one_launch", "mxfa_bwd_workspace_bytes",
     "mxfa_run_bwd_dkv_ws", "mxfa_run_bwd_ws", "mxfa_run_bwd_naive",
     "mxfa_naive_scratch_bytes", "mxfa_run_naive_fwd", "mxfa_check_prefill", "mxfa_run_prefill",
     "mxfa_probe_sink_len", "mxfa_probe_mfma", "mxfa_probe_read", "mxfa_probe_copy", "mxfa_probe_dq_atomic",
@@ -107,6 +107,7 @@ def load_library(path: str | None = None):
     lib.mxfa_run_bwd.argtypes = [sp, vp, vp, vp, vp, vp, fp, fp, vp, vp, vp, vp]
     lib.mxfa_run_bwd_dq_delta.argtypes = [sp, vp, vp, vp, vp, vp, fp, fp, vp, vp]
     lib.mxfa_run_bwd_naive.argtypes = [sp, vp, vp, vp, vp, fp, fp, vp, vp, vp, vp]
+    lib.mxfa_bwd_one_launch.argtypes = [sp]
     lib.mxfa_bwd_workspace_bytes.argtypes = [sp]
     lib.mxfa_bwd_workspace_bytes.restype = ctypes.c_size_t
     lib.mxfa_run_bwd_dkv_ws.argtypes = [sp, vp, vp, vp, vp, fp, fp, vp, vp, vp, ctypes.c_size_t, vp]
@@ -280,6 +281,13 @@ def run_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, causal: bool, scale: float =
             _expect(do, "do", qs, dt), _vec_ptr(lse, "lse", sh), _vec_ptr(delta, "delta", sh),
             _expect(dq, "dq", qs, dt), _expect(dk, "dk", ks, dt), _expect(dv, "dv", ks, dt)]
     _check("mxfa_run_bwd", load_library().mxfa_run_bwd(ctypes.byref(sh.c()), *args, _stream(stream)))
+
+
+def bwd_one_launch(q, k, causal: bool) -> bool:
+    """True if run_bwd runs the backward as one launch for this shape
+    (mxfa_bwd_one_launch; MXFA_BWD_FUSED=0 selects two launches)."""
+    sh = shape_of(q, k, causal)
+    return bool(load_library().mxfa_bwd_one_launch(ctypes.byref(sh.c())))
 
 
 def bwd_workspace_bytes(q, k, causal: bool) -> int:

@@ -21,6 +21,7 @@
 //     stage. It recomputes S and dP (the price of staying atomic-free and O(N)
 //     in memory).
 #include <algorithm>
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
 #include <type_traits>
@@ -76,7 +77,7 @@ __global__ __launch_bounds__(256) void preprocess_kernel(const T *dout, const T 
 
 // One dK/dV stage: the Pol::ROWS query rows from qs of Q and dO of head bh,
 // and their LSE and Delta, into LDS buffers.
-template <class Pol, int NT = 256>
+template <class Pol, int NT = 256, bool STAGE_DELTA = true>
 __device__ __forceinline__ void stage_qdo(typename Pol::T *sq, typename Pol::T *sdo, float *sl, float *sd,
                                           const Params &p, size_t bh, int qs, int N, const RowPlan<Pol, NT> &pl,
                                           int wave, int lane) {
@@ -86,8 +87,32 @@ __device__ __forceinline__ void stage_qdo(typename Pol::T *sq, typename Pol::T *
     stage_rows<Pol, NT>(sdo, static_cast<const T *>(p.dout) + off, N - qs, pl, wave);
     // rows past N: LSE = +inf makes their p (and so dS) exactly 0
     if (wave == 0) stage_vec64(sl, p.lse + bh * N + qs, N - qs, lane, &kPosInf);
-    if (wave == 1) stage_vec64(sd, p.delta + bh * N + qs, N - qs, lane, p.delta + bh * N + qs);
+    if (STAGE_DELTA && wave == 1) stage_vec64(sd, p.delta + bh * N + qs, N - qs, lane, p.delta + bh * N + qs);
 }
+
+// Delta of the Pol::ROWS rows from qs of head bh, computed by one wave from O
+// and dO (lane r: row qs + r) into LDS: the one-launch backward's fallback
+// when a block's flag has not appeared.
+template <class Pol>
+__device__ __forceinline__ void delta_rows_direct(float *sd, const Params &p, size_t bh, int qs, int N, int lane) {
+    using T = typename Pol::T;
+    using Frag = typename Pol::Frag;
+    const int row = qs + lane;
+    float acc = 0.f;
+    if (row < N) {
+        const size_t off = (bh * N + row) * Pol::D;
+        const Frag *o = reinterpret_cast<const Frag *>(static_cast<const T *>(p.o_in) + off);
+        const Frag *d = reinterpret_cast<const Frag *>(static_cast<const T *>(p.dout) + off);
+#pragma unroll
+        for (int c = 0; c < Pol::D / Pol::EPC; ++c) acc += Pol::dot(d[c], o[c]);
+    }
+    sd[lane] = acc;
+}
+
+// Delta flags of the one-launch backward (see Params::epoch). Zero at load;
+// launch epochs start at 1, so no flag matches before it is published.
+__device__ uint32_t g_delta_flags[kFlagSlots * kMaxFlagBlocks];
+constexpr int kFlagRows = 128;  // query rows per flag: one dQ work-group's block
 
 // ------------------------------------------------------------------ dQ pass
 
@@ -169,8 +194,10 @@ struct DqSmem {
 };
 
 // The dQ work of query block qb (16 QT NW rows) of (batch, query head) bh.
-// QT: 16-query tiles per wave; NW: waves per work-group.
-template <class Pol, bool CAUSAL, int NW, bool DELTA, int QT>
+// QT: 16-query tiles per wave; NW: waves per work-group. PUBLISH (with
+// DELTA, in the one-launch backward): Delta is written through to memory and
+// then the block's flag set to p.epoch, before the main loop.
+template <class Pol, bool CAUSAL, int NW, bool DELTA, int QT, bool PUBLISH = false>
 __device__ __forceinline__ void dq_body(const Params &p, int bh, int qb, DqSmem<Pol> &sm) {
     using T = typename Pol::T;
     using Frag = typename Pol::Frag;
@@ -209,7 +236,13 @@ __device__ __forceinline__ void dq_body(const Params &p, int bh, int qb, DqSmem<
 #pragma unroll
             for (int kc = 0; kc < NC; ++kc) dsum += Pol::dot(dof[qt][kc], of[kc]);
             Dl[qt] = xg_sum(dsum);
-            if (ok && g == 0) p.delta[(size_t)bh * N + qi] = Dl[qt];
+            if (ok && g == 0) {
+                if constexpr (PUBLISH) {
+                    store_wt(p.delta + (size_t)bh * N + qi, __float_as_uint(Dl[qt]));
+                } else {
+                    p.delta[(size_t)bh * N + qi] = Dl[qt];
+                }
+            }
         } else {
             Dl[qt] = ok ? p.delta[(size_t)bh * N + qi] : 0.f;
         }
@@ -225,6 +258,17 @@ __device__ __forceinline__ void dq_body(const Params &p, int bh, int qb, DqSmem<
     for (int xt = 0; xt < XT; ++xt) {
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) acc[xt][qt] = zero4();
+    }
+
+    if constexpr (PUBLISH) {
+        static_assert(DELTA && BQ == kFlagRows, "a published block is one work-group's Delta rows");
+        // every wave's Delta stores acknowledged (written through), then the flag
+        wait_stores();
+        __syncthreads();
+        if (tid == 0) {
+            const int nfb = (N + kFlagRows - 1) / kFlagRows;
+            store_wt(g_delta_flags + (size_t)p.flag_slot * kMaxFlagBlocks + (size_t)bh * nfb + qb, p.epoch);
+        }
     }
 
     const int kend = CAUSAL ? min(N, qb * BQ + BQ) : N;
@@ -491,11 +535,14 @@ struct DkvSmem {
     __attribute__((aligned(16))) typename Pol::T sdO[NBUF][Pol::ROWS * Pol::D];
     __attribute__((aligned(16))) float sL[NBUF][Pol::ROWS];
     __attribute__((aligned(16))) float sD[NBUF][Pol::ROWS];
+    uint32_t sF[2];  // one-launch backward: the flags of the next stages' Delta blocks
 };
 
 // The dK/dV work of key block kb (16 KT NW keys) of grid column bx =
-// (batch, KV head) * dkv_split + share.
-template <class Pol, int KT, bool CAUSAL, int NW>
+// (batch, KV head) * dkv_split + share. WAIT (one-launch backward): Delta
+// comes from the dQ work-groups of the same launch; wave 1 stages a stage's
+// Delta rows only once their block's flag reads p.epoch (see issue below).
+template <class Pol, int KT, bool CAUSAL, int NW, bool WAIT = false>
 __device__ __forceinline__ void dkv_body(const Params &p, int bx, int kb, DkvSmem<Pol> &sm) {
     using T = typename Pol::T;
     using Frag = typename Pol::Frag;
@@ -554,12 +601,45 @@ __device__ __forceinline__ void dkv_body(const Params &p, int bx, int kb, DkvSme
     // within it of the next one (kept incrementally: no division per stage).
     const RowPlan<Pol, NT> plan(tid);
     int ld_h = 0, ld_i = 0;
+    // WAIT: the flag of each stage's Delta block is fetched into sm.sF one
+    // issue ahead, with a load that misses the caches (as are the Delta rows
+    // themselves: the dQ work-group that wrote them may sit on another XCD).
+    // It is checked before the Delta rows are staged; a flag not yet set is
+    // polled (up to p.delta_spin times), and then the wave computes the rows
+    // itself. The first stage, with nothing fetched ahead, is polled directly.
+    // Either way the rows hold Delta of the launch's own O and dO.
+    const int nfb = (N + kFlagRows - 1) / kFlagRows;
+    const uint32_t *flags = g_delta_flags + (size_t)p.flag_slot * kMaxFlagBlocks;
     auto issue = [&](int st) __attribute__((always_inline)) {
         const int bf = st % NBUF;
-        stage_qdo<Pol, NT>(sQ[bf], sdO[bf], sL[bf], sD[bf], p, bh0 + ld_h, qstart + ld_i * BQ, N, plan, wave, lane);
+        const size_t bh = bh0 + ld_h;
+        const int qs = qstart + ld_i * BQ;
+        stage_qdo<Pol, NT, !WAIT>(sQ[bf], sdO[bf], sL[bf], sD[bf], p, bh, qs, N, plan, wave, lane);
         if (++ld_i == nqs) {
             ld_i = 0;
             ++ld_h;
+        }
+        if constexpr (WAIT) {
+            static_assert(NBUF == 2, "flags are fetched one issue ahead");
+            if (wave == 1) {
+                const uint32_t *f = flags + bh * nfb + qs / kFlagRows;
+                // delta_spin < 0 trusts no flag (every stage takes the fallback)
+                bool ready = p.delta_spin >= 0 && st > 0 && sm.sF[st & 1] == p.epoch;
+                for (int i = 0; !ready && i < p.delta_spin; ++i) {
+                    ready = __builtin_amdgcn_readfirstlane(load_uc_sync(f)) == p.epoch;
+                    if (!ready) __builtin_amdgcn_s_sleep(2);
+                }
+                if (ready) {
+                    lds_dma4_uc(lds_addr(sD[bf]), p.delta + bh * N + min(qs + lane, N - 1));
+                } else {
+                    delta_rows_direct<Pol>(sD[bf], p, bh, qs, N, lane);
+                }
+                // one lane: the DMA writes each active lane's dword at base + 4 lane
+                if (ld_h < nh && lane == 0) {
+                    const int qs_next = qstart + ld_i * BQ;
+                    lds_dma4_uc(lds_addr(&sm.sF[(st + 1) & 1]), flags + (bh0 + ld_h) * nfb + qs_next / kFlagRows);
+                }
+            }
         }
     };
     // loads of one stage per thread: the Q and dO tiles (+1 vector on waves
@@ -670,6 +750,34 @@ template <class Pol, int KT, bool CAUSAL, int NW>
 __global__ __launch_bounds__(64 * NW, Pol::kWavesDkv) void dkv_kernel(Params p) {
     __shared__ DkvSmem<Pol> sm;
     dkv_body<Pol, KT, CAUSAL, NW>(p, blockIdx.x, blockIdx.y, sm);
+}
+
+// The whole backward from O in one launch (bf16): work-groups [0, fused_ndq)
+// run the dQ pass with Delta, query blocks in increasing order (so Delta
+// appears in the order the dK/dV work-groups consume it: each walks its query
+// rows upward from its diagonal), and publish Delta per block; the rest run
+// the dK/dV pass, key block 0 first, and wait for the blocks they stage. The
+// dQ work-groups have lower indices, so they are dispatched first and never
+// wait; every wait of a dK/dV work-group is bounded (Params::delta_spin).
+// This removes one kernel boundary per backward.
+template <class Pol>
+union FusedSmem {
+    DqSmem<Pol> dq;
+    DkvSmem<Pol> dkv;
+};
+
+template <class Pol, int KT, bool CAUSAL>
+__global__ __launch_bounds__(256, Pol::kWavesDkv < Pol::kWavesDq ? Pol::kWavesDkv : Pol::kWavesDq) void
+bwd_fused_kernel(Params p) {
+    __shared__ FusedSmem<Pol> sm;
+    const int bid = blockIdx.x;
+    if (bid < p.fused_ndq) {
+        const int nbh = p.B * p.Hq;
+        dq_body<Pol, CAUSAL, Pol::kDqWavesPerGroup, true, Pol::kDqTiles, true>(p, bid % nbh, bid / nbh, sm.dq);
+    } else {
+        const int w = bid - p.fused_ndq, nbk = p.B * p.Hkv;
+        dkv_body<Pol, KT, CAUSAL, 4, true>(p, w % nbk, w / nbk, sm.dkv);
+    }
 }
 
 // dK / dV of a split dK/dV pass: the sum of the nsplit fp32 partial planes in
@@ -965,6 +1073,47 @@ hipError_t launch_bwd_dq(const Params &p, int dtype_bf16, int d, int causal, int
         MXFA_DQ(PolF32, 64)
     }
 #undef MXFA_DQ
+    return hipErrorInvalidValue;
+}
+
+static std::atomic<unsigned> g_epoch{0};
+
+static int env_int(const char *name, int dflt) {
+    const char *e = std::getenv(name);
+    return e != nullptr && *e != '\0' ? std::atoi(e) : dflt;
+}
+
+bool bwd_fused_available(const Params &p, int dtype_bf16, int d) {
+    if (!dtype_bf16 || (d != 64 && d != 128)) return false;
+    const long long nfb = (p.N + kFlagRows - 1) / kFlagRows;
+    if ((long long)p.B * p.Hq * nfb > kMaxFlagBlocks) return false;
+    return env_int("MXFA_BWD_FUSED", 1) != 0;
+}
+
+template <class Pol, int KT, bool CAUSAL>
+static hipError_t launch_fused_t(Params p, hipStream_t stream) {
+    constexpr int BKV = 16 * KT * 4;
+    const long long nfb = (p.N + kFlagRows - 1) / kFlagRows;
+    const long long ndq = (long long)p.B * p.Hq * nfb;
+    const long long ndkv = (long long)p.B * p.Hkv * ((p.N + BKV - 1) / BKV);
+    if (ndq + ndkv > 0x7fffffffLL) return hipErrorInvalidValue;
+    unsigned e = ++g_epoch;
+    if (e == 0) e = ++g_epoch;  // 0 is the flags' initial value
+    p.epoch = e;
+    p.flag_slot = (int)(e % kFlagSlots);
+    p.delta_spin = env_int("MXFA_DELTA_SPIN", 4096);
+    p.fused_ndq = (int)ndq;
+    p.dkv_split = 1;
+    p.dkv_ws = nullptr;
+    hipLaunchKernelGGL((bwd_fused_kernel<Pol, KT, CAUSAL>), dim3((unsigned)(ndq + ndkv)), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_bwd_fused(const Params &p, int d, int causal, hipStream_t stream) {
+    if (d == 64) return causal ? launch_fused_t<PolBF16<64>, 2, true>(p, stream)
+                               : launch_fused_t<PolBF16<64>, 2, false>(p, stream);
+    if (d == 128) return causal ? launch_fused_t<PolBF16<128>, 1, true>(p, stream)
+                                : launch_fused_t<PolBF16<128>, 1, false>(p, stream);
     return hipErrorInvalidValue;
 }
 

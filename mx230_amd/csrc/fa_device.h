@@ -50,7 +50,20 @@ struct Params {
     // reduce launch adds them in split order.
     float *dkv_ws;
     int dkv_split;
+    // One-launch backward (bwd_fused_kernel): work-groups [0, fused_ndq) run
+    // the dQ pass and publish Delta per 128-row query block with flag value
+    // epoch in slot flag_slot of g_delta_flags; the rest run the dK/dV pass
+    // and wait for those flags (at most delta_spin polls per block, then
+    // compute Delta themselves; delta_spin < 0: always compute it).
+    unsigned epoch;
+    int flag_slot, delta_spin, fused_ndq;
 };
+
+// Delta flags of the one-launch backward: kFlagSlots slots (one per launch,
+// round robin, so launches in flight at once on one device do not share
+// flags) of kMaxFlagBlocks flags, one per (batch, query head, 128-row block).
+constexpr int kFlagSlots = 4;
+constexpr int kMaxFlagBlocks = 1 << 18;
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
@@ -375,6 +388,35 @@ __device__ __forceinline__ void lds_dma4(uint32_t base, const void *src) {
         : "v"(src), "s"(__builtin_amdgcn_readfirstlane(base)));
 #endif
 }
+
+// Accesses for data that work-groups on different XCDs exchange within one
+// launch (each XCD has its own L2, which the hardware does not keep coherent
+// with the others): system-coherent (sc0 sc1) stores write through every
+// cache level, and loads of that kind miss them, so both meet in memory.
+// lds_dma4_uc: lds_dma4 with such a load.
+__device__ __forceinline__ void lds_dma4_uc(uint32_t base, const void *src) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    uint32_t save;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\t"
+        "global_load_lds_dword %1, off sc0 sc1\n\ts_mov_b32 m0, %0"
+        : "=&s"(save)
+        : "v"(src), "s"(__builtin_amdgcn_readfirstlane(base)));
+#endif
+}
+// A write-through store of one dword.
+__device__ __forceinline__ void store_wt(void *dst, uint32_t v) {
+    asm volatile("global_store_dword %0, %1, off sc0 sc1" ::"v"(dst), "v"(v) : "memory");
+}
+// A load past the caches, complete on return (it waits for every outstanding
+// vector-memory operation of the wave).
+__device__ __forceinline__ uint32_t load_uc_sync(const void *src) {
+    uint32_t v;
+    asm volatile("global_load_dword %0, %1, off sc0 sc1\n\ts_waitcnt vmcnt(0)" : "=v"(v) : "v"(src) : "memory");
+    return v;
+}
+// Waits until this wave's stores have been acknowledged.
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // Copies rows [0, Pol::ROWS) of a row-major [*, D] matrix into an LDS tile in
 // the policy's layout: load k of the wave fills 16-byte positions

@@ -238,10 +238,28 @@ int mxfa_run_bwd_ws(const mxfa_shape *shape, const void *q, const void *k, const
     if (rc != MXFA_OK) return rc;
     rc = check_workspace(shape, workspace, workspace_bytes);
     if (rc != MXFA_OK) return rc;
+    {
+        // one launch when the dK/dV pass does not split (no workspace in use)
+        Params p = bwd_params(shape, q, k, v, dout, lse, delta);
+        const bool split = workspace != nullptr && mxfa_bwd_workspace_bytes(shape) > 0;
+        if (!split && mxfa::bwd_fused_available(p, shape->dtype == MXFA_BF16, shape->d)) {
+            p.o_in = o;
+            p.dq = dq;
+            p.dk = dk;
+            p.dv = dv;
+            return from_hip(mxfa::launch_bwd_fused(p, shape->d, shape->causal, static_cast<hipStream_t>(stream)));
+        }
+    }
     // dQ pass first: it computes Delta and writes it for the dK/dV pass
     rc = mxfa_run_bwd_dq_delta(shape, q, k, v, o, dout, lse, delta, dq, stream);
     if (rc != MXFA_OK) return rc;
     return mxfa_run_bwd_dkv_ws(shape, q, k, v, dout, lse, delta, dk, dv, workspace, workspace_bytes, stream);
+}
+
+int mxfa_bwd_one_launch(const mxfa_shape *shape) {
+    if (check_shape(shape) != MXFA_OK) return 0;
+    const Params p = make_params(shape);
+    return mxfa::bwd_fused_available(p, shape->dtype == MXFA_BF16, shape->d) ? 1 : 0;
 }
 
 size_t mxfa_bwd_workspace_bytes(const mxfa_shape *shape) {

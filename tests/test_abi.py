@@ -121,6 +121,20 @@ def test_bwd_workspace_bytes(lib, kw, nbytes):
     assert lib.mxfa_bwd_workspace_bytes(ctypes.byref(_shape(**kw))) == nbytes
 
 
+def test_bwd_one_launch(lib, monkeypatch):
+    monkeypatch.delenv("MXFA_BWD_FUSED", raising=False)
+    assert lib.mxfa_bwd_one_launch(ctypes.byref(_shape(B=4, Hq=12, Hkv=12, N=4096))) == 1
+    assert lib.mxfa_bwd_one_launch(ctypes.byref(_shape(d=128))) == 1
+    assert lib.mxfa_bwd_one_launch(ctypes.byref(_shape(dtype=mx.MXFA_F32))) == 0
+    assert lib.mxfa_bwd_one_launch(ctypes.byref(_shape(Hq=3, Hkv=2))) == 0
+    assert lib.mxfa_bwd_one_launch(None) == 0
+    # more (batch, head, 128-row block) flags than one slot holds: two launches
+    assert lib.mxfa_bwd_one_launch(ctypes.byref(_shape(B=64, Hq=64, Hkv=64, N=8192))) == 1  # 2^18: fits
+    assert lib.mxfa_bwd_one_launch(ctypes.byref(_shape(B=64, Hq=64, Hkv=64, N=8193))) == 0
+    monkeypatch.setenv("MXFA_BWD_FUSED", "0")
+    assert lib.mxfa_bwd_one_launch(ctypes.byref(_shape(B=4, Hq=12, Hkv=12, N=4096))) == 0
+
+
 def test_workspace_checks(lib):
     sh = _shape(B=2, Hq=14, Hkv=2, N=4096, d=64)
     need = lib.mxfa_bwd_workspace_bytes(ctypes.byref(sh))

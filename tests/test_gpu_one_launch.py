@@ -1,0 +1,133 @@
+"""The one-launch backward (bwd_fused_kernel, the default of mxfa_run_bwd for
+bf16): dQ work-groups publish Delta per 128-row block behind a flag, and the
+dK/dV work-groups of the same launch wait for it, or compute the rows
+themselves after a bounded wait.
+
+- With flags it is bitwise equal to the two-launch backward
+  (MXFA_BWD_FUSED=0), over shapes and over repeated runs, since it stages
+  the same Delta values. A stale or early read of Delta would show as a
+  mismatch.
+- With every wait forced to give up (MXFA_DELTA_SPIN=-1) the dK/dV work-groups
+  compute Delta from O and dO in another summation order. dK and dV then
+  equal the two-launch ones up to flips of their last bf16 bit: within 2^-7 of
+  the outputs' max (one bf16 ulp of the largest element is 2^-8 of it).
+- Launches in flight together on several streams, more than the flag slots,
+  so later launches see other launches' flags, still give each one its own
+  result.
+"""
+from __future__ import annotations
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+BF16_FLIPS = 2.0 ** -7  # bf16 outputs whose last bit may flip, relative to the max
+
+SHAPES = [
+    ("north-star", (4, 12, 12, 4096, 64), True),
+    ("gqa-ragged", (2, 14, 2, 777, 64), True),
+    ("gqa-noncausal", (1, 6, 2, 576, 64), False),
+    ("d128", (1, 8, 8, 1000, 128), True),
+    ("d128-gqa-noncausal", (1, 4, 1, 2048, 128), False),
+    ("n1", (1, 4, 4, 1, 64), True),
+    ("n130", (2, 3, 3, 130, 64), False),
+]
+
+
+def _setup(B, H, Hkv, N, d, causal, seed=1):
+    import torch
+    import mx230_amd as mx
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    q = torch.randn(B, H, N, d, device="cuda", generator=g).bfloat16()
+    k = torch.randn(B, Hkv, N, d, device="cuda", generator=g).bfloat16()
+    v = torch.randn(B, Hkv, N, d, device="cuda", generator=g).bfloat16()
+    do = torch.randn(B, H, N, d, device="cuda", generator=g).bfloat16()
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, N, device="cuda")
+    mx.run_flash_lse(q, k, v, o, lse, causal)
+    return q, k, v, do, o, lse
+
+
+def _bwd(t, causal, stream=None):
+    import torch
+    import mx230_amd as mx
+    q, k, v, do, o, lse = t
+    delta = torch.full(lse.shape, float("nan"), device="cuda")
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    mx.run_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, causal, stream=stream)
+    return delta, dq, dk, dv
+
+
+def _sync(outs):
+    import torch
+    torch.cuda.synchronize()
+    return outs
+
+
+@pytest.mark.parametrize("name,shape,causal", SHAPES, ids=[s[0] for s in SHAPES])
+def test_one_launch_equals_two_launches(monkeypatch, name, shape, causal):
+    t = _setup(*shape, causal)
+    monkeypatch.setenv("MXFA_BWD_FUSED", "0")
+    ref = _sync(_bwd(t, causal))
+    monkeypatch.setenv("MXFA_BWD_FUSED", "1")
+    import torch
+    for rep in range(3):
+        got = _sync(_bwd(t, causal))
+        for n, a, b in zip(("Delta", "dQ", "dK", "dV"), got, ref):
+            assert torch.equal(a, b), f"{name} run {rep}: {n} differs from the two-launch backward"
+
+
+def test_one_launch_repeated_north_star(monkeypatch):
+    import torch
+    t = _setup(4, 12, 12, 4096, 64, True, seed=7)
+    monkeypatch.setenv("MXFA_BWD_FUSED", "0")
+    ref = _sync(_bwd(t, True))
+    monkeypatch.setenv("MXFA_BWD_FUSED", "1")
+    outs = [_bwd(t, True) for _ in range(20)]
+    torch.cuda.synchronize()
+    bad = sum(not all(torch.equal(a, b) for a, b in zip(got, ref)) for got in outs)
+    assert bad == 0, f"{bad} of 20 one-launch runs differ"
+
+
+def _rel(a, b):
+    a, b = a.float(), b.float()
+    return ((a - b).abs().max() / b.abs().max().clamp_min(1e-30)).item()
+
+
+@pytest.mark.parametrize("name,shape,causal", SHAPES, ids=[s[0] for s in SHAPES])
+def test_one_launch_fallback(monkeypatch, name, shape, causal):
+    t = _setup(*shape, causal, seed=3)
+    monkeypatch.setenv("MXFA_BWD_FUSED", "0")
+    ref = _sync(_bwd(t, causal))
+    monkeypatch.setenv("MXFA_BWD_FUSED", "1")
+    monkeypatch.setenv("MXFA_DELTA_SPIN", "-1")
+    got = _sync(_bwd(t, causal))
+    import torch
+    assert torch.equal(got[0], ref[0]) and torch.equal(got[1], ref[1])  # Delta and dQ come from the dQ pass
+    for n, a, b in zip(("dK", "dV"), got[2:], ref[2:]):
+        e = _rel(a, b)
+        print(f"[{name}] fallback {n} {e:.2e}", flush=True)
+        assert e <= BF16_FLIPS, (name, n, e)
+
+
+def test_one_launch_concurrent_streams(monkeypatch):
+    """Six launches in flight on six streams (four flag slots)."""
+    import torch
+    monkeypatch.setenv("MXFA_BWD_FUSED", "1")
+    cases = [_setup(2, 6, 2, 1000 + 64 * i, 64, True, seed=20 + i) for i in range(6)]
+    monkeypatch.setenv("MXFA_BWD_FUSED", "0")
+    refs = [_sync(_bwd(t, True)) for t in cases]
+    monkeypatch.setenv("MXFA_BWD_FUSED", "1")
+    streams = [torch.cuda.Stream() for _ in cases]
+    torch.cuda.synchronize()
+    outs = []
+    for t, s in zip(cases, streams):
+        with torch.cuda.stream(s):
+            outs.append(_bwd(t, True, stream=s))
+    torch.cuda.synchronize()
+    for i, (got, ref) in enumerate(zip(outs, refs)):
+        assert torch.equal(got[0], ref[0]) and torch.equal(got[1], ref[1]), i
+        for n, a, b in zip(("dK", "dV"), got[2:], ref[2:]):
+            e = _rel(a, b)
+            assert e <= BF16_FLIPS, (i, n, e)
