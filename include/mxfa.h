@@ -138,8 +138,10 @@ int mxfa_run_bwd(const mxfa_shape *shape, const void *q, const void *k, const vo
                  const void *dout, const float *lse, float *delta, void *dq, void *dk, void *dv,
                  void *stream);
 
-/* 1 if mxfa_run_bwd (and mxfa_run_bwd_ws without a split) runs the backward
- * as one launch for this shape, else 0 (two launches, or an invalid shape).
+/* 1 if mxfa_run_bwd and mxfa_run_bwd_ws run the dQ and dK/dV work of this
+ * shape in one launch (followed, for a GQA split through a workspace, by the
+ * launch that adds the split's partial sums), else 0 (a dQ launch and a dK/dV
+ * launch, or an invalid shape).
  * The one-launch form (bf16, d = 64 or 128) runs the dQ work-groups first;
  * they publish Delta per 128-row query block, and the dK/dV work-groups of the
  * same launch wait for the blocks they need. Each wait is bounded: after it the

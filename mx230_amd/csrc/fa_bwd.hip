@@ -775,7 +775,7 @@ bwd_fused_kernel(Params p) {
         const int nbh = p.B * p.Hq;
         dq_body<Pol, CAUSAL, Pol::kDqWavesPerGroup, true, Pol::kDqTiles, true>(p, bid % nbh, bid / nbh, sm.dq);
     } else {
-        const int w = bid - p.fused_ndq, nbk = p.B * p.Hkv;
+        const int w = bid - p.fused_ndq, nbk = p.B * p.Hkv * p.dkv_split;
         dkv_body<Pol, KT, CAUSAL, 4, true>(p, w % nbk, w / nbk, sm.dkv);
     }
 }
@@ -1090,12 +1090,19 @@ bool bwd_fused_available(const Params &p, int dtype_bf16, int d) {
     return env_int("MXFA_BWD_FUSED", 1) != 0;
 }
 
+template <class T>
+static hipError_t launch_dkv_reduce(const Params &p, int d, hipStream_t stream);
+
 template <class Pol, int KT, bool CAUSAL>
 static hipError_t launch_fused_t(Params p, hipStream_t stream) {
     constexpr int BKV = 16 * KT * 4;
+    // with a workspace, GQA shapes split each group's query heads as in the
+    // dK/dV pass; the shares' partial sums are added by a second launch
+    p.dkv_split = p.dkv_ws != nullptr ? dkv_split(p, 1, Pol::D) : 1;
+    if (p.dkv_split == 1) p.dkv_ws = nullptr;
     const long long nfb = (p.N + kFlagRows - 1) / kFlagRows;
     const long long ndq = (long long)p.B * p.Hq * nfb;
-    const long long ndkv = (long long)p.B * p.Hkv * ((p.N + BKV - 1) / BKV);
+    const long long ndkv = (long long)p.B * p.Hkv * p.dkv_split * ((p.N + BKV - 1) / BKV);
     if (ndq + ndkv > 0x7fffffffLL) return hipErrorInvalidValue;
     unsigned e = ++g_epoch;
     if (e == 0) e = ++g_epoch;  // 0 is the flags' initial value
@@ -1103,10 +1110,10 @@ static hipError_t launch_fused_t(Params p, hipStream_t stream) {
     p.flag_slot = (int)(e % kFlagSlots);
     p.delta_spin = env_int("MXFA_DELTA_SPIN", 4096);
     p.fused_ndq = (int)ndq;
-    p.dkv_split = 1;
-    p.dkv_ws = nullptr;
     hipLaunchKernelGGL((bwd_fused_kernel<Pol, KT, CAUSAL>), dim3((unsigned)(ndq + ndkv)), dim3(256), 0, stream, p);
-    return hipGetLastError();
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess || p.dkv_split == 1) return err;
+    return launch_dkv_reduce<u16>(p, Pol::D, stream);
 }
 
 hipError_t launch_bwd_fused(const Params &p, int d, int causal, hipStream_t stream) {

@@ -239,14 +239,14 @@ int mxfa_run_bwd_ws(const mxfa_shape *shape, const void *q, const void *k, const
     rc = check_workspace(shape, workspace, workspace_bytes);
     if (rc != MXFA_OK) return rc;
     {
-        // one launch when the dK/dV pass does not split (no workspace in use)
+        // the dQ and dK/dV work in one launch (plus the reduce of a GQA split)
         Params p = bwd_params(shape, q, k, v, dout, lse, delta);
-        const bool split = workspace != nullptr && mxfa_bwd_workspace_bytes(shape) > 0;
-        if (!split && mxfa::bwd_fused_available(p, shape->dtype == MXFA_BF16, shape->d)) {
+        if (mxfa::bwd_fused_available(p, shape->dtype == MXFA_BF16, shape->d)) {
             p.o_in = o;
             p.dq = dq;
             p.dk = dk;
             p.dv = dv;
+            p.dkv_ws = static_cast<float *>(workspace);
             return from_hip(mxfa::launch_bwd_fused(p, shape->d, shape->causal, static_cast<hipStream_t>(stream)));
         }
     }

@@ -11,6 +11,8 @@ themselves after a bounded wait.
   compute Delta from O and dO in another summation order. dK and dV then
   equal the two-launch ones up to flips of their last bf16 bit: within 2^-7 of
   the outputs' max (one bf16 ulp of the largest element is 2^-8 of it).
+- With a GQA split through a workspace, the one launch plus the reduce equal
+  the two-launch split bitwise.
 - Launches in flight together on several streams, more than the flag slots,
   so later launches see other launches' flags, still give each one its own
   result.
@@ -131,3 +133,30 @@ def test_one_launch_concurrent_streams(monkeypatch):
         for n, a, b in zip(("dK", "dV"), got[2:], ref[2:]):
             e = _rel(a, b)
             assert e <= BF16_FLIPS, (i, n, e)
+
+
+@pytest.mark.parametrize("shape", [(2, 14, 2, 4096, 64), (1, 32, 4, 2048, 128), (1, 8, 2, 300, 64)],
+                         ids=["cfg4", "cfg5-d128", "ragged"])
+def test_one_launch_with_gqa_split(monkeypatch, shape):
+    import torch
+    import mx230_amd as mx
+    t = _setup(*shape, True, seed=9)
+    q, k, v, do, o, lse = t
+    nws = mx.bwd_workspace_bytes(q, k, True)
+    assert nws > 0
+    ws = torch.empty(nws, dtype=torch.uint8, device="cuda")
+
+    def run():
+        delta = torch.full(lse.shape, float("nan"), device="cuda")
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        mx.run_bwd_ws(q, k, v, o, do, lse, delta, dq, dk, dv, ws, True)
+        torch.cuda.synchronize()
+        return delta, dq, dk, dv
+
+    monkeypatch.setenv("MXFA_BWD_FUSED", "0")
+    ref = run()
+    monkeypatch.setenv("MXFA_BWD_FUSED", "1")
+    for rep in range(3):
+        got = run()
+        for n, a, b in zip(("Delta", "dQ", "dK", "dV"), got, ref):
+            assert torch.equal(a, b), f"run {rep}: {n} differs from the two-launch split"
