@@ -147,7 +147,9 @@ int mxfa_run_bwd(const mxfa_shape *shape, const void *q, const void *k, const vo
  * same launch wait for the blocks they need. Each wait is bounded: after it the
  * work-group computes those Delta rows from O and dO itself. Results equal the
  * two-launch form's bitwise whenever no wait runs out. The environment
- * variable MXFA_BWD_FUSED=0, read on every call, selects two launches.
+ * variable MXFA_BWD_FUSED=0, read on every call, selects two launches, and so
+ * does a stream under graph capture (a replayed launch would reuse the
+ * capture's flag epoch); this query answers for an ordinary stream.
  * No counterpart in the reference: it tells callers (and benchmarks) which
  * kernels the backward from O (main.rs:126-143, :179-210) becomes. */
 int mxfa_bwd_one_launch(const mxfa_shape *shape);

@@ -1083,8 +1083,15 @@ static int env_int(const char *name, int dflt) {
     return e != nullptr && *e != '\0' ? std::atoi(e) : dflt;
 }
 
-bool bwd_fused_available(const Params &p, int dtype_bf16, int d) {
+bool bwd_fused_available(const Params &p, int dtype_bf16, int d, hipStream_t stream) {
     if (!dtype_bf16 || (d != 64 && d != 128)) return false;
+    // a launch captured into a graph would replay with the epoch of its
+    // capture, so a replay could take the previous replay's flags for its own
+    // Delta: graphs get the two-launch form
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (stream != nullptr && hipStreamIsCapturing(stream, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone) {
+        return false;
+    }
     const long long nfb = (p.N + kFlagRows - 1) / kFlagRows;
     if ((long long)p.B * p.Hq * nfb > kMaxFlagBlocks) return false;
     return env_int("MXFA_BWD_FUSED", 1) != 0;

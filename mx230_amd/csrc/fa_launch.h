@@ -21,7 +21,7 @@ int dkv_split(const Params &p, int dtype_bf16, int d);
 // The one-launch backward from O (dQ pass with Delta + dK/dV pass, bf16;
 // with p.dkv_ws a GQA split as launch_bwd_dkv, whose reduce then follows as a
 // second launch): available for the shape, and launched with its own epoch.
-bool bwd_fused_available(const Params &p, int dtype_bf16, int d);
+bool bwd_fused_available(const Params &p, int dtype_bf16, int d, hipStream_t stream);
 hipError_t launch_bwd_fused(const Params &p, int d, int causal, hipStream_t stream);
 hipError_t launch_bwd_naive(const Params &p, int d, int causal, hipStream_t stream);
 hipError_t launch_naive_fwd(const Params &p, float *s, int d, int causal, hipStream_t stream);

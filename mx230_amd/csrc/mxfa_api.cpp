@@ -241,7 +241,7 @@ int mxfa_run_bwd_ws(const mxfa_shape *shape, const void *q, const void *k, const
     {
         // the dQ and dK/dV work in one launch (plus the reduce of a GQA split)
         Params p = bwd_params(shape, q, k, v, dout, lse, delta);
-        if (mxfa::bwd_fused_available(p, shape->dtype == MXFA_BF16, shape->d)) {
+        if (mxfa::bwd_fused_available(p, shape->dtype == MXFA_BF16, shape->d, static_cast<hipStream_t>(stream))) {
             p.o_in = o;
             p.dq = dq;
             p.dk = dk;
@@ -259,7 +259,7 @@ int mxfa_run_bwd_ws(const mxfa_shape *shape, const void *q, const void *k, const
 int mxfa_bwd_one_launch(const mxfa_shape *shape) {
     if (check_shape(shape) != MXFA_OK) return 0;
     const Params p = make_params(shape);
-    return mxfa::bwd_fused_available(p, shape->dtype == MXFA_BF16, shape->d) ? 1 : 0;
+    return mxfa::bwd_fused_available(p, shape->dtype == MXFA_BF16, shape->d, nullptr) ? 1 : 0;
 }
 
 size_t mxfa_bwd_workspace_bytes(const mxfa_shape *shape) {
