@@ -1157,18 +1157,21 @@ static hipError_t launch_dkv_t(const Params &p, hipStream_t stream) {
 }
 
 // How many work-groups share the query heads of a key block's GQA group: the
-// smallest divisor of the group that gives the launch at least one work-group
-// per resident slot (256 CUs x the kernel's work-groups per CU), else the
-// whole group (one query head per work-group). 1 without GQA or when the key
-// blocks alone fill the GPU.
+// smallest divisor of the group that gives the launch at least two
+// work-groups per resident slot (256 CUs x the kernel's work-groups per CU),
+// else the whole group (one query head per work-group). 1 without GQA or when
+// the key blocks alone fill the GPU twice over. A share's heads run one after
+// another, so its causal key block 0 is the launch's critical path: at cfg5
+// d = 128 (128 key blocks, 512 slots) 8 shares ran 144 us against 157 us for
+// the 4 that one slot each would give.
 template <class Pol, int KT, int NW = 4>
 static int dkv_split_t(const Params &p) {
     if (p.group <= 1) return 1;
     constexpr int BKV = 16 * KT * NW;
-    constexpr long long kSlots = 256LL * (Pol::kWavesDkv * 4 / NW);
+    constexpr long long kSlots = 256LL * Pol::kWavesDkv;
     const long long base = (long long)p.B * p.Hkv * ((p.N + BKV - 1) / BKV);
     for (int s = 1; s < p.group; ++s) {
-        if (p.group % s == 0 && base * s >= kSlots) return s;
+        if (p.group % s == 0 && base * s >= 2 * kSlots) return s;
     }
     return p.group;
 }

@@ -104,14 +104,16 @@ def test_sizes_and_strings(lib):
     # no GQA: nothing to split
     (dict(B=4, Hq=12, Hkv=12, N=4096, d=64), 0),
     # cfg4 (Qwen2.5, 7:1): 2*2 (b, kv head) x 32 key blocks = 128 work-groups
-    # for 768 slots; 7 is prime, so one query head per work-group
+    # for 2 x 768 slots; 7 is prime, so one query head per work-group
     (dict(B=2, Hq=14, Hkv=2, N=4096, d=64), 2 * 7 * 2 * 2 * 4096 * 64 * 4),
-    # cfg5 d=64 (TinyLlama, 8:1): 64 work-groups; 4 shares give 256 < 768, so 8
+    # cfg5 d=64 (TinyLlama, 8:1): 64 work-groups; 4 shares give 256 < 1536, so 8
     (dict(B=1, Hq=32, Hkv=4, N=2048, d=64), 2 * 8 * 1 * 4 * 2048 * 64 * 4),
-    # cfg5 d=128: 64-key blocks, 128 work-groups for 512 slots: 4 shares
-    (dict(B=1, Hq=32, Hkv=4, N=2048, d=128), 2 * 4 * 1 * 4 * 2048 * 128 * 4),
-    # GQA whose key blocks already fill the GPU: no split
+    # cfg5 d=128: 64-key blocks, 128 work-groups for 2 x 512 slots: 8 shares
+    (dict(B=1, Hq=32, Hkv=4, N=2048, d=128), 2 * 8 * 1 * 4 * 2048 * 128 * 4),
+    # 8 * 8 (b, kv head) x 32 key blocks = 2048 work-groups, twice 768 slots: no split
     (dict(B=8, Hq=16, Hkv=8, N=4096, d=64), 0),
+    # 512 work-groups: 3 shares would be the first to reach 2 x 768, and 4 divides 8
+    (dict(B=4, Hq=32, Hkv=4, N=4096, d=64), 2 * 4 * 4 * 4 * 4096 * 64 * 4),
     # fp32 parity path, tiny GQA shape: whole group split
     (dict(B=1, Hq=2, Hkv=1, N=128, d=64, dtype=mx.MXFA_F32), 2 * 2 * 1 * 1 * 128 * 64 * 4),
     # invalid shape
