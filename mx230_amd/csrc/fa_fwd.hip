@@ -4,7 +4,8 @@
 // Follows the algorithm of attention_flash.cu:17-89 (online softmax, causal
 // tile break, LSE = m + ln l at :85-87), re-tiled for CDNA4:
 //   * workgroup = 4 waves = 128 queries of one (batch, head); each wave owns
-//     32 queries, whose Q rows sit in registers as MFMA B operands;
+//     32 queries, whose Q rows sit in registers as MFMA B operands (64 and
+//     16 on grids too small to fill the GPU otherwise);
 //   * K/V advance 64 keys per stage through double-buffered LDS, filled by
 //     direct global->LDS loads issued one stage ahead;
 //   * scores are computed transposed, S^T = K Q^T, so each lane owns one query
@@ -30,14 +31,14 @@ namespace mxfa {
 // exact, else qf holds Q scale log2(e)), online-softmax update,
 // O^T += V^T P^T.
 // qpos0: position of the wave's first query row; Nk: key rows.
-template <class Pol, bool CAUSAL, bool MASK>
-__device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][2], float (&m)[2], float (&lsum)[2],
-                                          const typename Pol::Frag (&qf)[2][Pol::NC],
+template <class Pol, int QT, bool CAUSAL, bool MASK>
+__device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][QT], float (&m)[QT], float (&lsum)[QT],
+                                          const typename Pol::Frag (&qf)[QT][Pol::NC],
                                           const typename Pol::T *sk, const typename Pol::T *sv, int k0, int qpos0,
                                           int Nk, int g, int l16, float xmul) {
     using Frag = typename Pol::Frag;
     constexpr int NC = Pol::NC, XT = Pol::D / 16;
-    f32x4 s[2][2][2];  // [block][t][qt]
+    f32x4 s[2][2][QT];  // [block][t][qt]
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
 #pragma unroll
@@ -45,7 +46,7 @@ __device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][2], float (&
             Frag a[NC];
             Pol::lds_row_frags(a, sk, 32 * blk + Pol::arow(t, l16), g);
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt) {
+            for (int qt = 0; qt < QT; ++qt) {
                 f32x4 c = zero4();
 #pragma unroll
                 for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], qf[qt][kc], c);
@@ -54,7 +55,7 @@ __device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][2], float (&
         }
     }
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < QT; ++qt) {
         const int qpos = qpos0 + 16 * qt + l16;
         float mx = -INFINITY;
 #pragma unroll
@@ -96,13 +97,15 @@ __device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][2], float (&
     }
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
-        typename Pol::ChainB cb[2];
+        typename Pol::ChainB cb[QT];
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) cb[qt] = Pol::pack(s[blk][0][qt], s[blk][1][qt]);
+        for (int qt = 0; qt < QT; ++qt) cb[qt] = Pol::pack(s[blk][0][qt], s[blk][1][qt]);
 #pragma unroll
         for (int xt = 0; xt < XT; ++xt) {
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt) acc[xt][qt] = Pol::chain(acc[xt][qt], cb[qt], sv, 16 * xt, 32 * blk, g, l16);
+            for (int qt = 0; qt < QT; ++qt) {
+                acc[xt][qt] = Pol::chain(acc[xt][qt], cb[qt], sv, 16 * xt, 32 * blk, g, l16);
+            }
         }
     }
 }
@@ -126,15 +129,19 @@ constexpr float kLazySum = 65536.0f;
 // Scores of one 64-key stage relative to m: s = K Q^T scale log2(e) - m, with
 // masked keys (MASK) at -inf. With Pol::kExactScale the accumulators start at
 // -m / xmul and the fp32 result is multiplied by xmul = scale log2(e).
-template <class Pol, bool CAUSAL, bool MASK>
-__device__ __forceinline__ void fwd_scores(f32x4 (&s)[2][2][2], const float (&m)[2],
-                                           const typename Pol::Frag (&qf)[2][Pol::NC], const typename Pol::T *sk,
+template <class Pol, int QT, bool CAUSAL, bool MASK>
+__device__ __forceinline__ void fwd_scores(f32x4 (&s)[2][2][QT], const float (&m)[QT],
+                                           const typename Pol::Frag (&qf)[QT][Pol::NC], const typename Pol::T *sk,
                                            int k0, int qpos0, int Nk, int g, int l16, float xmul) {
     using Frag = typename Pol::Frag;
     constexpr int NC = Pol::NC;
     const float im = Pol::kExactScale ? 1.0f / xmul : 1.0f;
-    const float n0 = -m[0] * im, n1 = -m[1] * im;
-    const f32x4 nm[2] = {f32x4{n0, n0, n0, n0}, f32x4{n1, n1, n1, n1}};
+    f32x4 nm[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        const float n = -m[qt] * im;
+        nm[qt] = f32x4{n, n, n, n};
+    }
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
 #pragma unroll
@@ -142,7 +149,7 @@ __device__ __forceinline__ void fwd_scores(f32x4 (&s)[2][2][2], const float (&m)
             Frag a[NC];
             Pol::lds_row_frags(a, sk, 32 * blk + Pol::arow(t, l16), g);
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt) {
+            for (int qt = 0; qt < QT; ++qt) {
                 f32x4 c = nm[qt];
 #pragma unroll
                 for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], qf[qt][kc], c);
@@ -152,7 +159,7 @@ __device__ __forceinline__ void fwd_scores(f32x4 (&s)[2][2][2], const float (&m)
     }
     if constexpr (MASK) {
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
+        for (int qt = 0; qt < QT; ++qt) {
             const int qpos = qpos0 + 16 * qt + l16;
 #pragma unroll
             for (int blk = 0; blk < 2; ++blk) {
@@ -170,9 +177,10 @@ __device__ __forceinline__ void fwd_scores(f32x4 (&s)[2][2][2], const float (&m)
 }
 
 // p = 2^s in place, added to l (row qt of this lane).
-__device__ __forceinline__ void fwd_exp_sum(f32x4 (&s)[2][2][2], float (&l)[2]) {
+template <int QT>
+__device__ __forceinline__ void fwd_exp_sum(f32x4 (&s)[2][2][QT], float (&l)[QT]) {
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < QT; ++qt) {
         float ls = l[qt];
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
@@ -190,22 +198,27 @@ __device__ __forceinline__ void fwd_exp_sum(f32x4 (&s)[2][2][2], float (&l)[2]) 
     }
 }
 
-template <class Pol, bool CAUSAL, bool MASK>
-__device__ __forceinline__ void fwd_stage_lazy(f32x4 (&acc)[Pol::D / 16][2], float (&m)[2], float (&lsum)[2],
-                                               const typename Pol::Frag (&qf)[2][Pol::NC],
+template <class Pol, int QT, bool CAUSAL, bool MASK>
+__device__ __forceinline__ void fwd_stage_lazy(f32x4 (&acc)[Pol::D / 16][QT], float (&m)[QT], float (&lsum)[QT],
+                                               const typename Pol::Frag (&qf)[QT][Pol::NC],
                                                const typename Pol::T *sk, const typename Pol::T *sv, int k0,
                                                int qpos0, int Nk, int g, int l16, float xmul) {
     constexpr int XT = Pol::D / 16;
-    f32x4 s[2][2][2];  // [block][t][qt]
-    fwd_scores<Pol, CAUSAL, MASK>(s, m, qf, sk, k0, qpos0, Nk, g, l16, xmul);
-    const float l0[2] = {lsum[0], lsum[1]};
+    f32x4 s[2][2][QT];  // [block][t][qt]
+    fwd_scores<Pol, QT, CAUSAL, MASK>(s, m, qf, sk, k0, qpos0, Nk, g, l16, xmul);
+    float l0[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) l0[qt] = lsum[qt];
     fwd_exp_sum(s, lsum);
-    if (__builtin_amdgcn_ballot_w64(lsum[0] > l0[0] + kLazySum || lsum[1] > l0[1] + kLazySum) != 0) {
+    bool over = false;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) over = over || lsum[qt] > l0[qt] + kLazySum;
+    if (__builtin_amdgcn_ballot_w64(over) != 0) {
         // some p of the wave exceeded kLazySum: redo the stage with m raised to
         // each row's max (rows whose max did not rise keep shift 0)
-        fwd_scores<Pol, CAUSAL, MASK>(s, m, qf, sk, k0, qpos0, Nk, g, l16, xmul);
+        fwd_scores<Pol, QT, CAUSAL, MASK>(s, m, qf, sk, k0, qpos0, Nk, g, l16, xmul);
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
+        for (int qt = 0; qt < QT; ++qt) {
             float v = -INFINITY;
 #pragma unroll
             for (int blk = 0; blk < 2; ++blk) {
@@ -234,24 +247,27 @@ __device__ __forceinline__ void fwd_stage_lazy(f32x4 (&acc)[Pol::D / 16][2], flo
     }
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
-        typename Pol::ChainB cb[2];
+        typename Pol::ChainB cb[QT];
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) cb[qt] = Pol::pack(s[blk][0][qt], s[blk][1][qt]);
+        for (int qt = 0; qt < QT; ++qt) cb[qt] = Pol::pack(s[blk][0][qt], s[blk][1][qt]);
 #pragma unroll
         for (int xt = 0; xt < XT; ++xt) {
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt) acc[xt][qt] = Pol::chain(acc[xt][qt], cb[qt], sv, 16 * xt, 32 * blk, g, l16);
+            for (int qt = 0; qt < QT; ++qt) {
+                acc[xt][qt] = Pol::chain(acc[xt][qt], cb[qt], sv, 16 * xt, 32 * blk, g, l16);
+            }
         }
     }
 }
 
-// WPS: waves per SIMD the kernel is compiled for.
-template <class Pol, bool CAUSAL, int WPS>
+// WPS: waves per SIMD the kernel is compiled for; QT: 16-query tiles per wave
+// (the work-group takes 64 QT queries).
+template <class Pol, bool CAUSAL, int WPS, int QT>
 __global__ __launch_bounds__(256, WPS) void fwd_kernel(Params p) {
     using T = typename Pol::T;
     using Frag = typename Pol::Frag;
     constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
-    constexpr int BQ = 128, BK = Pol::ROWS;
+    constexpr int BQ = 64 * QT, BK = Pol::ROWS;
 
     __shared__ __attribute__((aligned(16))) T sK[2][BK * D];
     __shared__ __attribute__((aligned(16))) T sV[2][BK * D];
@@ -268,12 +284,12 @@ __global__ __launch_bounds__(256, WPS) void fwd_kernel(Params p) {
     const size_t kvoff = b * p.kv_bs + kvh * p.kv_hs;
     const T *K = static_cast<const T *>(p.k) + kvoff;
     const T *V = static_cast<const T *>(p.v) + kvoff;
-    const int q0 = qb * BQ + wave * 32;
+    const int q0 = qb * BQ + wave * 16 * QT;
     const int qpos0 = pos0 + q0;  // position of the wave's first query row
 
-    Frag qf[2][NC];
+    Frag qf[QT][NC];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < QT; ++qt) {
         const int qi = q0 + 16 * qt + l16;
         Pol::gmem_row_frags(qf[qt], Q + (size_t)qi * p.q_rs, g, qi < N);
         // fp32: Q scale log2(e), so the scores come out of the MFMAs in log2
@@ -283,10 +299,15 @@ __global__ __launch_bounds__(256, WPS) void fwd_kernel(Params p) {
             if (!Pol::kExactScale) qf[qt][kc] = Pol::scaled(qf[qt][kc], p.scale_log2);
         }
     }
-    f32x4 acc[XT][2];
+    f32x4 acc[XT][QT];
+    float m[QT], lsum[QT];
 #pragma unroll
-    for (int xt = 0; xt < XT; ++xt) acc[xt][0] = acc[xt][1] = zero4();
-    float m[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.f, 0.f};
+    for (int qt = 0; qt < QT; ++qt) {
+#pragma unroll
+        for (int xt = 0; xt < XT; ++xt) acc[xt][qt] = zero4();
+        m[qt] = -INFINITY;
+        lsum[qt] = 0.f;
+    }
 
     const int kend = CAUSAL ? min(Nk, pos0 + qb * BQ + BQ) : Nk;
     const int nsteps = (kend + BK - 1) / BK;
@@ -306,9 +327,10 @@ __global__ __launch_bounds__(256, WPS) void fwd_kernel(Params p) {
         constexpr int B = decltype(buf)::value;
         if (st + 1 < nsteps) stage_kv<Pol>(sK[B ^ 1], sV[B ^ 1], K, V, (st + 1) * BK, Nk, plan, wave, p.kv_rs);
         if constexpr (decltype(first)::value) {
-            fwd_stage<Pol, CAUSAL, false>(acc, m, lsum, qf, sK[B], sV[B], st * BK, qpos0, Nk, g, l16, p.scale_log2);
+            fwd_stage<Pol, QT, CAUSAL, false>(acc, m, lsum, qf, sK[B], sV[B], st * BK, qpos0, Nk, g, l16, p.scale_log2);
         } else {
-            fwd_stage_lazy<Pol, CAUSAL, false>(acc, m, lsum, qf, sK[B], sV[B], st * BK, qpos0, Nk, g, l16, p.scale_log2);
+            fwd_stage_lazy<Pol, QT, CAUSAL, false>(acc, m, lsum, qf, sK[B], sV[B], st * BK, qpos0, Nk, g, l16,
+                                                   p.scale_log2);
         }
         wait_stage();
         __syncthreads();
@@ -330,11 +352,13 @@ __global__ __launch_bounds__(256, WPS) void fwd_kernel(Params p) {
         if (st + 1 < nsteps) stage_kv<Pol>(sK[cur ^ 1], sV[cur ^ 1], K, V, (st + 1) * BK, Nk, plan, wave, p.kv_rs);
         const int k0 = st * BK;
         // a wave whose queries all precede the stage's keys has nothing to do
-        if (!CAUSAL || k0 <= qpos0 + 31) {
+        if (!CAUSAL || k0 <= qpos0 + 16 * QT - 1) {
             if (st == 0) {
-                fwd_stage<Pol, CAUSAL, true>(acc, m, lsum, qf, sK[cur], sV[cur], k0, qpos0, Nk, g, l16, p.scale_log2);
+                fwd_stage<Pol, QT, CAUSAL, true>(acc, m, lsum, qf, sK[cur], sV[cur], k0, qpos0, Nk, g, l16,
+                                                 p.scale_log2);
             } else {
-                fwd_stage_lazy<Pol, CAUSAL, true>(acc, m, lsum, qf, sK[cur], sV[cur], k0, qpos0, Nk, g, l16, p.scale_log2);
+                fwd_stage_lazy<Pol, QT, CAUSAL, true>(acc, m, lsum, qf, sK[cur], sV[cur], k0, qpos0, Nk, g, l16,
+                                                      p.scale_log2);
             }
         }
         wait_stage();
@@ -343,7 +367,7 @@ __global__ __launch_bounds__(256, WPS) void fwd_kernel(Params p) {
 
     T *O = static_cast<T *>(p.o) + b * p.o_bs + h * p.o_hs;
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < QT; ++qt) {
         const int qi = q0 + 16 * qt + l16;
         const float ltot = xg_sum(lsum[qt]);
         const float inv = 1.0f / ltot;
@@ -355,19 +379,38 @@ __global__ __launch_bounds__(256, WPS) void fwd_kernel(Params p) {
     }
 }
 
-template <class Pol, bool CAUSAL>
-static hipError_t launch_fwd_t(const Params &p, hipStream_t stream) {
-    const dim3 grid(p.B * p.Hq, (p.N + 127) / 128);
+template <class Pol, bool CAUSAL, int QT>
+static hipError_t launch_fwd_qt(const Params &p, hipStream_t stream) {
+    const dim3 grid(p.B * p.Hq, (p.N + 64 * QT - 1) / (64 * QT));
     constexpr int kHi = Pol::kWavesFwdCausal;
-    if constexpr (CAUSAL && kHi > Pol::kWaves) {
+    if constexpr (CAUSAL && kHi > Pol::kWaves && QT > 1) {
         // enough causal work-groups to fill kHi per CU (256 CUs)
         if ((long long)grid.x * grid.y >= 256LL * kHi) {
-            hipLaunchKernelGGL((fwd_kernel<Pol, CAUSAL, kHi>), grid, dim3(256), 0, stream, p);
+            hipLaunchKernelGGL((fwd_kernel<Pol, CAUSAL, kHi, QT>), grid, dim3(256), 0, stream, p);
             return hipGetLastError();
         }
     }
-    hipLaunchKernelGGL((fwd_kernel<Pol, CAUSAL, Pol::kWaves>), grid, dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((fwd_kernel<Pol, CAUSAL, QT == 1 ? kHi : Pol::kWaves, QT>), grid, dim3(256), 0, stream, p);
     return hipGetLastError();
+}
+
+// bf16 launches whose 128-query work-groups would not fill every resident
+// slot (256 CUs x 3) take 64-query work-groups (one 16-query tile per wave):
+// twice the work-groups and half the critical path (the heaviest block's keys
+// times its queries), for twice the LDS reads per MFMA. Measured on the
+// MI355X: causal B1 H12 N4096 d64 54.3 -> 40.3 us, B1 H8 N2048 d128 43.4 ->
+// 28.8 us, non-causal B1 H12 N4096 d64 74.6 -> 65.5 us; at 768 work-groups
+// (causal B1 H12 N8192 d64) 125 against 135 us keeps 128 queries. Non-causal
+// d = 128 keeps them (B1 H8 N4096: 77.2 against 80.2 us).
+constexpr long long kFwdSmallGrid = 768;
+
+template <class Pol, bool CAUSAL>
+static hipError_t launch_fwd_t(const Params &p, hipStream_t stream) {
+    if constexpr (Pol::kExactScale && (CAUSAL || Pol::D == 64)) {
+        const long long wg = (long long)p.B * p.Hq * ((p.N + 127) / 128);
+        if (wg < kFwdSmallGrid) return launch_fwd_qt<Pol, CAUSAL, 1>(p, stream);
+    }
+    return launch_fwd_qt<Pol, CAUSAL, 2>(p, stream);
 }
 
 hipError_t launch_fwd(const Params &p, int dtype_bf16, int d, int causal, hipStream_t stream) {

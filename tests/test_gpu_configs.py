@@ -64,6 +64,37 @@ def test_cfg5_tinyllama_gqa_full(d):
     _group_check(f"cfg5-d{d}", q, k, v, do, True, b=0, kvh=2, tol=TOL_BF16)
 
 
+@pytest.mark.parametrize("causal,d", [(True, 64), (False, 64), (True, 128)])
+def test_forward_tilings_agree(causal, d):
+    """The bf16 forward takes 64-query work-groups when fewer than 768 of 128
+    queries would fill the GPU (not for non-causal d = 128). B1 H12 N4096 gives
+    384 of them (so 64-query work-groups run); B2 gives 768 (128 queries). The
+    same batch-0 heads in both launches agree to bf16 rounding in O (the
+    tilings rescale at different stages) and to fp32 rounding in LSE, and one
+    head of the B1 launch matches the oracle."""
+    import torch
+    import mx230_amd as mx
+    q, k, v, _ = make_inputs(2, 12, 12, 4096, d, bf16=True, seeds=(61, 62, 63, 64))
+    outs = []
+    for B in (1, 2):
+        tq, tk, tv = (to_dev(x[:B], True) for x in (q, k, v))
+        o = torch.empty_like(tq)
+        lse = torch.empty((B, 12, 4096), dtype=torch.float32, device="cuda")
+        mx.run_flash_lse(tq, tk, tv, o, lse, causal)
+        torch.cuda.synchronize()
+        outs.append((to_np(o)[0], to_np(lse)[0]))
+    (o1, l1), (o2, l2) = outs
+    eo, el = rel_err(o1, o2), rel_err(l1, l2)
+    print(f"\n[tilings causal={causal} d={d}] O {eo:.2e} LSE {el:.2e}", flush=True)
+    assert eo <= 2.0 ** -7 and el <= 1e-5, (eo, el)
+    h = 5
+    ro, rl = oracle.mha_fwd(q[:1, h:h + 1], k[:1, h:h + 1], v[:1, h:h + 1], 1, 1, 1, 4096, d, causal,
+                            nthreads=1)
+    errs = (rel_err(o1[h], ro[0, 0]), rel_err(l1[h], rl[0, 0]))
+    print(f"[tilings causal={causal} d={d}] oracle head {h}: O {errs[0]:.2e} LSE {errs[1]:.2e}", flush=True)
+    assert max(errs) <= TOL_BF16, errs
+
+
 # ---------------------------------------------------------- long sequence --
 
 def _rows_f64(q, k, v, do, rows, cols_chunk=4096):
