@@ -122,8 +122,10 @@ constexpr int kFlagRows = 128;  // query rows per flag: one dQ work-group's bloc
 // -L / scale, xmul = scale log2(e)); otherwise qf holds Q scale log2(e) and
 // nL2 is -L log2(e). dof holds -dO and the dP accumulators start at Delta, so
 // they come out as Delta - dP and the MFMAs accumulate -dQ / scale (the
-// epilogue multiplies by -scale).
-template <class Pol, int QT, bool CAUSAL, bool MASK>
+// epilogue multiplies by -scale). PRIO: the matrix products run at raised
+// wave priority, the softmax part at normal priority (the one-launch backward,
+// where dQ and dK/dV work-groups share each SIMD).
+template <class Pol, int QT, bool CAUSAL, bool MASK, bool PRIO = false>
 __device__ __forceinline__ void dq_stage(f32x4 (&acc)[Pol::D / 16][QT], const typename Pol::Frag (&qf)[QT][Pol::NC],
                                          const typename Pol::Frag (&dof)[QT][Pol::NC], const float (&nL2)[QT],
                                          const float (&Dl)[QT], const typename Pol::T *sk,
@@ -134,6 +136,7 @@ __device__ __forceinline__ void dq_stage(f32x4 (&acc)[Pol::D / 16][QT], const ty
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
         f32x4 s[2][QT], dp[2][QT];  // [t][qt]
+        wave_priority<PRIO>(1);
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             Frag a[NC];
@@ -155,6 +158,7 @@ __device__ __forceinline__ void dq_stage(f32x4 (&acc)[Pol::D / 16][QT], const ty
                 dp[t][qt] = c;
             }
         }
+        wave_priority<PRIO>(0);
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
             const int qi = q0 + 16 * qt + l16;
@@ -175,11 +179,15 @@ __device__ __forceinline__ void dq_stage(f32x4 (&acc)[Pol::D / 16][QT], const ty
         typename Pol::ChainB cb[QT];
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) cb[qt] = Pol::pack(s[0][qt], s[1][qt]);
+        wave_priority<PRIO>(1);
 #pragma unroll
         for (int xt = 0; xt < XT; ++xt) {
 #pragma unroll
-            for (int qt = 0; qt < QT; ++qt) acc[xt][qt] = Pol::chain(acc[xt][qt], cb[qt], sk, 16 * xt, 32 * blk, g, l16);
+            for (int qt = 0; qt < QT; ++qt) {
+                acc[xt][qt] = Pol::chain(acc[xt][qt], cb[qt], sk, 16 * xt, 32 * blk, g, l16);
+            }
         }
+        wave_priority<PRIO>(0);
     }
 }
 
@@ -288,7 +296,8 @@ __device__ __forceinline__ void dq_body(const Params &p, int bh, int qb, DqSmem<
     auto main_stage = [&](auto buf, int st) __attribute__((always_inline)) {
         constexpr int B = decltype(buf)::value;
         if (st + 1 < nsteps) stage_kv<Pol, NT>(sK[B ^ 1], sV[B ^ 1], K, V, (st + 1) * BK, N, plan, wave);
-        dq_stage<Pol, QT, CAUSAL, false>(acc, qf, dof, nL2, Dl, sK[B], sV[B], st * BK, q0, N, g, l16, p.scale_log2);
+        dq_stage<Pol, QT, CAUSAL, false, PUBLISH>(acc, qf, dof, nL2, Dl, sK[B], sV[B], st * BK, q0, N, g, l16,
+                                                  p.scale_log2);
         wait_stage();
         __syncthreads();
     };
@@ -307,8 +316,8 @@ __device__ __forceinline__ void dq_body(const Params &p, int bh, int qb, DqSmem<
         // one (masked) body for these stages: a second, unmasked body behind a
         // branch makes the register allocator spill at three waves per SIMD
         if (!CAUSAL || k0 <= q0 + 16 * QT - 1) {
-            dq_stage<Pol, QT, CAUSAL, true>(acc, qf, dof, nL2, Dl, sK[cur], sV[cur], k0, q0, N, g, l16,
-                                            p.scale_log2);
+            dq_stage<Pol, QT, CAUSAL, true, PUBLISH>(acc, qf, dof, nL2, Dl, sK[cur], sV[cur], k0, q0, N, g, l16,
+                                                     p.scale_log2);
         }
         wait_stage();
         __syncthreads();
@@ -454,8 +463,9 @@ __device__ __forceinline__ void softmax_block(f32x4 (&s)[2][2], f32x4 (&dp)[2][2
 // -1 / scale, xmul = scale log2(e)); otherwise kf holds K scale log2(e) and
 // lmul = -log2(e). vf holds -V and the dP accumulators start at Delta, so
 // they come out as Delta - dP and accK accumulates -dK / scale (the epilogue
-// multiplies by -scale).
-template <class Pol, int KT, bool CAUSAL, bool MASK>
+// multiplies by -scale). PRIO: the matrix products run at raised wave
+// priority, the softmax part at normal priority (the one-launch backward).
+template <class Pol, int KT, bool CAUSAL, bool MASK, bool PRIO = false>
 __device__ __forceinline__ void dkv_stage(f32x4 (&accK)[Pol::D / 16][KT], f32x4 (&accV)[Pol::D / 16][KT],
                                           const typename Pol::Frag (&kf)[KT][Pol::NC],
                                           const typename Pol::Frag (&vf)[KT][Pol::NC], const typename Pol::T *sq,
@@ -466,6 +476,7 @@ __device__ __forceinline__ void dkv_stage(f32x4 (&accK)[Pol::D / 16][KT], f32x4 
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
         f32x4 s[2][KT], dp[2][KT];  // [t][kt]
+        wave_priority<PRIO>(1);
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             // block rows bidx(t, g, 0..3) are consecutive: one 16-byte LDS read
@@ -491,6 +502,7 @@ __device__ __forceinline__ void dkv_stage(f32x4 (&accK)[Pol::D / 16][KT], f32x4 
                 dp[t][kt] = c;
             }
         }
+        wave_priority<PRIO>(0);
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
 #pragma unroll
@@ -515,6 +527,7 @@ __device__ __forceinline__ void dkv_stage(f32x4 (&accK)[Pol::D / 16][KT], f32x4 
             cp[kt] = Pol::pack(s[0][kt], s[1][kt]);
             cds[kt] = Pol::pack(dp[0][kt], dp[1][kt]);
         }
+        wave_priority<PRIO>(1);
 #pragma unroll
         for (int xt = 0; xt < XT; ++xt) {
 #pragma unroll
@@ -523,6 +536,7 @@ __device__ __forceinline__ void dkv_stage(f32x4 (&accK)[Pol::D / 16][KT], f32x4 
                 accK[xt][kt] = Pol::chain(accK[xt][kt], cds[kt], sq, 16 * xt, 32 * blk, g, l16);
             }
         }
+        wave_priority<PRIO>(0);
     }
 }
 
@@ -670,8 +684,8 @@ __device__ __forceinline__ void dkv_body(const Params &p, int bx, int kb, DkvSme
         const int qs = qstart + i * BQ;
         // a wave whose keys all follow the stage's queries has nothing to do
         if (!CAUSAL || qs + BQ - 1 >= kw0) {
-            dkv_stage<Pol, KT, CAUSAL, MASK>(accK, accV, kf, vf, sQ[cur], sdO[cur], sL[cur], sD[cur], qs, kw0, N, g,
-                                             l16, lmul, xmul);
+            dkv_stage<Pol, KT, CAUSAL, MASK, WAIT>(accK, accV, kf, vf, sQ[cur], sdO[cur], sL[cur], sD[cur], qs, kw0,
+                                                   N, g, l16, lmul, xmul);
         }
         if (NBUF > 2 && ahead) {
             wait_vmcnt<kLoads>();
@@ -687,8 +701,8 @@ __device__ __forceinline__ void dkv_body(const Params &p, int bx, int kb, DkvSme
         constexpr int B = decltype(buf)::value;
         if (st + 1 < nsteps) issue(st + 1);
         const int qs = qstart + i * BQ;
-        dkv_stage<Pol, KT, CAUSAL, false>(accK, accV, kf, vf, sQ[B], sdO[B], sL[B], sD[B], qs, kw0, N, g, l16, lmul,
-                                          xmul);
+        dkv_stage<Pol, KT, CAUSAL, false, WAIT>(accK, accV, kf, vf, sQ[B], sdO[B], sL[B], sD[B], qs, kw0, N, g, l16,
+                                                lmul, xmul);
         wait_stage();
         barrier_lds();
     };

@@ -418,6 +418,22 @@ __device__ __forceinline__ uint32_t load_uc_sync(const void *src) {
 // Waits until this wave's stores have been acknowledged.
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Issue priority of the calling wave (0 or 1; the scheduling barriers keep the
+// compiler from moving instructions across the change). ON = false compiles
+// to nothing.
+template <bool ON>
+__device__ __forceinline__ void wave_priority(int hi) {
+    if constexpr (ON) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (hi) {
+            __builtin_amdgcn_s_setprio(1);
+        } else {
+            __builtin_amdgcn_s_setprio(0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
 // Copies rows [0, Pol::ROWS) of a row-major [*, D] matrix into an LDS tile in
 // the policy's layout: load k of the wave fills 16-byte positions
 // P = k NT + 64 wave + lane, and each lane fetches the global chunk that
