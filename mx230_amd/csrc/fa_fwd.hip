@@ -29,9 +29,9 @@ namespace mxfa {
 
 // One 64-key stage for one wave: scores in log2 units (x xmul when Q is kept
 // exact, else qf holds Q scale log2(e)), online-softmax update,
-// O^T += V^T P^T.
+// O^T += V^T P^T. PRIO: the matrix products run at raised wave priority.
 // qpos0: position of the wave's first query row; Nk: key rows.
-template <class Pol, int QT, bool CAUSAL, bool MASK>
+template <class Pol, int QT, bool CAUSAL, bool MASK, bool PRIO = false>
 __device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][QT], float (&m)[QT], float (&lsum)[QT],
                                           const typename Pol::Frag (&qf)[QT][Pol::NC],
                                           const typename Pol::T *sk, const typename Pol::T *sv, int k0, int qpos0,
@@ -39,6 +39,7 @@ __device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][QT], float (
     using Frag = typename Pol::Frag;
     constexpr int NC = Pol::NC, XT = Pol::D / 16;
     f32x4 s[2][2][QT];  // [block][t][qt]
+    wave_priority<PRIO>(1);
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
 #pragma unroll
@@ -54,6 +55,7 @@ __device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][QT], float (
             }
         }
     }
+    wave_priority<PRIO>(0);
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
         const int qpos = qpos0 + 16 * qt + l16;
@@ -95,6 +97,7 @@ __device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][QT], float (
         }
         lsum[qt] = ls;
     }
+    wave_priority<PRIO>(1);
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
         typename Pol::ChainB cb[QT];
@@ -108,6 +111,7 @@ __device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][QT], float (
             }
         }
     }
+    wave_priority<PRIO>(0);
 }
 
 // fwd_stage for every stage after the first, with lazy rescaling. Key 0 is
@@ -129,7 +133,7 @@ constexpr float kLazySum = 65536.0f;
 // Scores of one 64-key stage relative to m: s = K Q^T scale log2(e) - m, with
 // masked keys (MASK) at -inf. With Pol::kExactScale the accumulators start at
 // -m / xmul and the fp32 result is multiplied by xmul = scale log2(e).
-template <class Pol, int QT, bool CAUSAL, bool MASK>
+template <class Pol, int QT, bool CAUSAL, bool MASK, bool PRIO = false>
 __device__ __forceinline__ void fwd_scores(f32x4 (&s)[2][2][QT], const float (&m)[QT],
                                            const typename Pol::Frag (&qf)[QT][Pol::NC], const typename Pol::T *sk,
                                            int k0, int qpos0, int Nk, int g, int l16, float xmul) {
@@ -142,6 +146,7 @@ __device__ __forceinline__ void fwd_scores(f32x4 (&s)[2][2][QT], const float (&m
         const float n = -m[qt] * im;
         nm[qt] = f32x4{n, n, n, n};
     }
+    wave_priority<PRIO>(1);
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
 #pragma unroll
@@ -157,6 +162,7 @@ __device__ __forceinline__ void fwd_scores(f32x4 (&s)[2][2][QT], const float (&m
             }
         }
     }
+    wave_priority<PRIO>(0);
     if constexpr (MASK) {
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
@@ -198,14 +204,14 @@ __device__ __forceinline__ void fwd_exp_sum(f32x4 (&s)[2][2][QT], float (&l)[QT]
     }
 }
 
-template <class Pol, int QT, bool CAUSAL, bool MASK>
+template <class Pol, int QT, bool CAUSAL, bool MASK, bool PRIO = false>
 __device__ __forceinline__ void fwd_stage_lazy(f32x4 (&acc)[Pol::D / 16][QT], float (&m)[QT], float (&lsum)[QT],
                                                const typename Pol::Frag (&qf)[QT][Pol::NC],
                                                const typename Pol::T *sk, const typename Pol::T *sv, int k0,
                                                int qpos0, int Nk, int g, int l16, float xmul) {
     constexpr int XT = Pol::D / 16;
     f32x4 s[2][2][QT];  // [block][t][qt]
-    fwd_scores<Pol, QT, CAUSAL, MASK>(s, m, qf, sk, k0, qpos0, Nk, g, l16, xmul);
+    fwd_scores<Pol, QT, CAUSAL, MASK, PRIO>(s, m, qf, sk, k0, qpos0, Nk, g, l16, xmul);
     float l0[QT];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) l0[qt] = lsum[qt];
@@ -216,7 +222,7 @@ __device__ __forceinline__ void fwd_stage_lazy(f32x4 (&acc)[Pol::D / 16][QT], fl
     if (__builtin_amdgcn_ballot_w64(over) != 0) {
         // some p of the wave exceeded kLazySum: redo the stage with m raised to
         // each row's max (rows whose max did not rise keep shift 0)
-        fwd_scores<Pol, QT, CAUSAL, MASK>(s, m, qf, sk, k0, qpos0, Nk, g, l16, xmul);
+        fwd_scores<Pol, QT, CAUSAL, MASK, PRIO>(s, m, qf, sk, k0, qpos0, Nk, g, l16, xmul);
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
             float v = -INFINITY;
@@ -245,6 +251,7 @@ __device__ __forceinline__ void fwd_stage_lazy(f32x4 (&acc)[Pol::D / 16][QT], fl
         }
         fwd_exp_sum(s, lsum);
     }
+    wave_priority<PRIO>(1);
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
         typename Pol::ChainB cb[QT];
@@ -258,6 +265,7 @@ __device__ __forceinline__ void fwd_stage_lazy(f32x4 (&acc)[Pol::D / 16][QT], fl
             }
         }
     }
+    wave_priority<PRIO>(0);
 }
 
 // WPS: waves per SIMD the kernel is compiled for; QT: 16-query tiles per wave
@@ -268,6 +276,11 @@ __global__ __launch_bounds__(256, WPS) void fwd_kernel(Params p) {
     using Frag = typename Pol::Frag;
     constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
     constexpr int BQ = 64 * QT, BK = Pol::ROWS;
+    // bf16: the matrix products at raised wave priority, the softmax at normal
+    // (A/B on one box: cfg4 78.1 -> 74.3 us, cfg5 d = 128 51.0 -> 47.2,
+    // non-causal B2 H12 N4096 112.2 -> 109.7; the 64-query d = 64 launches
+    // lost 1-3% with it)
+    constexpr bool kPrio = Pol::kExactScale && (QT == 2 || D == 128);
 
     __shared__ __attribute__((aligned(16))) T sK[2][BK * D];
     __shared__ __attribute__((aligned(16))) T sV[2][BK * D];
@@ -327,10 +340,11 @@ __global__ __launch_bounds__(256, WPS) void fwd_kernel(Params p) {
         constexpr int B = decltype(buf)::value;
         if (st + 1 < nsteps) stage_kv<Pol>(sK[B ^ 1], sV[B ^ 1], K, V, (st + 1) * BK, Nk, plan, wave, p.kv_rs);
         if constexpr (decltype(first)::value) {
-            fwd_stage<Pol, QT, CAUSAL, false>(acc, m, lsum, qf, sK[B], sV[B], st * BK, qpos0, Nk, g, l16, p.scale_log2);
+            fwd_stage<Pol, QT, CAUSAL, false, kPrio>(acc, m, lsum, qf, sK[B], sV[B], st * BK, qpos0, Nk, g, l16,
+                                                     p.scale_log2);
         } else {
-            fwd_stage_lazy<Pol, QT, CAUSAL, false>(acc, m, lsum, qf, sK[B], sV[B], st * BK, qpos0, Nk, g, l16,
-                                                   p.scale_log2);
+            fwd_stage_lazy<Pol, QT, CAUSAL, false, kPrio>(acc, m, lsum, qf, sK[B], sV[B], st * BK, qpos0, Nk, g, l16,
+                                                          p.scale_log2);
         }
         wait_stage();
         __syncthreads();
@@ -354,11 +368,11 @@ __global__ __launch_bounds__(256, WPS) void fwd_kernel(Params p) {
         // a wave whose queries all precede the stage's keys has nothing to do
         if (!CAUSAL || k0 <= qpos0 + 16 * QT - 1) {
             if (st == 0) {
-                fwd_stage<Pol, QT, CAUSAL, true>(acc, m, lsum, qf, sK[cur], sV[cur], k0, qpos0, Nk, g, l16,
-                                                 p.scale_log2);
+                fwd_stage<Pol, QT, CAUSAL, true, kPrio>(acc, m, lsum, qf, sK[cur], sV[cur], k0, qpos0, Nk, g, l16,
+                                                        p.scale_log2);
             } else {
-                fwd_stage_lazy<Pol, QT, CAUSAL, true>(acc, m, lsum, qf, sK[cur], sV[cur], k0, qpos0, Nk, g, l16,
-                                                      p.scale_log2);
+                fwd_stage_lazy<Pol, QT, CAUSAL, true, kPrio>(acc, m, lsum, qf, sK[cur], sV[cur], k0, qpos0, Nk, g, l16,
+                                                             p.scale_log2);
             }
         }
         wait_stage();
