@@ -212,6 +212,9 @@ __device__ __forceinline__ void dq_body(const Params &p, int bh, int qb, DqSmem<
     constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
     constexpr int BQ = 16 * QT * NW, BK = Pol::ROWS, NT = 64 * NW;
     static_assert(BQ % BK == 0, "causal: the masked tail is the work-group's BQ / BK diagonal stages");
+    // raised priority for the matrix products in the one launch at d = 64
+    // (at d = 128 it measured 7-13% slower)
+    constexpr bool kPrio = PUBLISH && D == 64;
     auto &sK = sm.sK;
     auto &sV = sm.sV;
 
@@ -296,7 +299,7 @@ __device__ __forceinline__ void dq_body(const Params &p, int bh, int qb, DqSmem<
     auto main_stage = [&](auto buf, int st) __attribute__((always_inline)) {
         constexpr int B = decltype(buf)::value;
         if (st + 1 < nsteps) stage_kv<Pol, NT>(sK[B ^ 1], sV[B ^ 1], K, V, (st + 1) * BK, N, plan, wave);
-        dq_stage<Pol, QT, CAUSAL, false, PUBLISH>(acc, qf, dof, nL2, Dl, sK[B], sV[B], st * BK, q0, N, g, l16,
+        dq_stage<Pol, QT, CAUSAL, false, kPrio>(acc, qf, dof, nL2, Dl, sK[B], sV[B], st * BK, q0, N, g, l16,
                                                   p.scale_log2);
         wait_stage();
         __syncthreads();
@@ -316,7 +319,7 @@ __device__ __forceinline__ void dq_body(const Params &p, int bh, int qb, DqSmem<
         // one (masked) body for these stages: a second, unmasked body behind a
         // branch makes the register allocator spill at three waves per SIMD
         if (!CAUSAL || k0 <= q0 + 16 * QT - 1) {
-            dq_stage<Pol, QT, CAUSAL, true, PUBLISH>(acc, qf, dof, nL2, Dl, sK[cur], sV[cur], k0, q0, N, g, l16,
+            dq_stage<Pol, QT, CAUSAL, true, kPrio>(acc, qf, dof, nL2, Dl, sK[cur], sV[cur], k0, q0, N, g, l16,
                                                      p.scale_log2);
         }
         wait_stage();
@@ -565,6 +568,9 @@ __device__ __forceinline__ void dkv_body(const Params &p, int bx, int kb, DkvSme
     constexpr int BKV = 16 * KT * NW; // keys per workgroup
     constexpr int BQ = Pol::ROWS;     // queries per stage
     static_assert(BKV % BQ == 0, "causal start must align to a stage");
+    // raised priority for the matrix products in the one launch at d = 64
+    // (at d = 128 it measured 7-13% slower)
+    constexpr bool kPrio = WAIT && D == 64;
     constexpr int NBUF = DkvSmem<Pol>::NBUF;
     auto &sQ = sm.sQ;
     auto &sdO = sm.sdO;
@@ -684,7 +690,7 @@ __device__ __forceinline__ void dkv_body(const Params &p, int bx, int kb, DkvSme
         const int qs = qstart + i * BQ;
         // a wave whose keys all follow the stage's queries has nothing to do
         if (!CAUSAL || qs + BQ - 1 >= kw0) {
-            dkv_stage<Pol, KT, CAUSAL, MASK, WAIT>(accK, accV, kf, vf, sQ[cur], sdO[cur], sL[cur], sD[cur], qs, kw0,
+            dkv_stage<Pol, KT, CAUSAL, MASK, kPrio>(accK, accV, kf, vf, sQ[cur], sdO[cur], sL[cur], sD[cur], qs, kw0,
                                                    N, g, l16, lmul, xmul);
         }
         if (NBUF > 2 && ahead) {
@@ -701,7 +707,7 @@ __device__ __forceinline__ void dkv_body(const Params &p, int bx, int kb, DkvSme
         constexpr int B = decltype(buf)::value;
         if (st + 1 < nsteps) issue(st + 1);
         const int qs = qstart + i * BQ;
-        dkv_stage<Pol, KT, CAUSAL, false, WAIT>(accK, accV, kf, vf, sQ[B], sdO[B], sL[B], sD[B], qs, kw0, N, g, l16,
+        dkv_stage<Pol, KT, CAUSAL, false, kPrio>(accK, accV, kf, vf, sQ[B], sdO[B], sL[B], sD[B], qs, kw0, N, g, l16,
                                                 lmul, xmul);
         wait_stage();
         barrier_lds();
