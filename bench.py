@@ -53,7 +53,12 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--two-launch", action="store_true",
                     help="time the two-launch backward (dQ pass with Delta, then dK/dV) even where one "
-                         "launch is available (sets MXFA_BWD_FUSED=0)")
+                         "launch is available (set_bwd_options(one_launch=False))")
+    # the MI355X raises its clocks over the first ~30 ms of sustained load and
+    # drops them again within 0.5 s idle: before the --warmup steps, steps run
+    # for at least this long (reported as clock_warmup_ms / clock_warmup_steps,
+    # apart from "warmup")
+    ap.add_argument("--clock-warmup-ms", type=float, default=150.0)
     ap.add_argument("--separate-delta", action="store_true",
                     help="run the reference-shaped sequence (preprocess launch, then the dQ pass reading Delta)")
     ap.add_argument("--no-probe", action="store_true",
@@ -386,7 +391,7 @@ def main():
     torch.cuda.synchronize()
 
     if a.two_launch:
-        os.environ["MXFA_BWD_FUSED"] = "0"
+        mx.set_bwd_options(one_launch=False)
     # the backward from O as mxfa_run_bwd runs it: one launch (dQ work-groups
     # publish Delta for the dK/dV work-groups of the same launch) where
     # available, else the dQ pass with Delta then the dK/dV pass; with
@@ -419,22 +424,37 @@ def main():
         torch.cuda.synchronize()
         return {n: sum(evs[j].elapsed_time(evs[j + 1]) for evs in evsets) / a.steps for j, (n, _) in enumerate(seq)}
 
+    # clock warm-up (reported on its own), then the requested warm-up steps
+    cw0 = time.perf_counter()
+    cw_steps = 0
+    while (time.perf_counter() - cw0) * 1e3 < a.clock_warmup_ms:
+        step(launches)
+        cw_steps += 1
+        if cw_steps % 8 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    cw_ms = (time.perf_counter() - cw0) * 1e3
     for _ in range(a.warmup):
         step(launches)
     torch.cuda.synchronize()
+    fb0 = mx.bwd_delta_fallbacks() if one else 0
 
-    # timed region: exactly K backward steps, synchronised on both sides, timed
-    # by one event pair around them on the launch stream (an event recorded
-    # between two launches costs a few microseconds of stream time, so the
-    # per-kernel events are kept out of this region)
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # timed region: exactly K backward steps, synchronised on both sides, with
+    # an event on the launch stream before each step and after the last: the
+    # median of the K per-step times is the headline (the reference's
+    # time_median_ms, common/src/lib.rs:22-43), their mean beside it
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(a.steps + 1)]
     torch.cuda.synchronize()
-    t0.record(stream)
-    for _ in range(a.steps):
+    for i in range(a.steps):
+        evs[i].record(stream)
         step(launches)
-    t1.record(stream)
+    evs[a.steps].record(stream)
     torch.cuda.synchronize()
-    ms_per_step = t0.elapsed_time(t1) / a.steps
+    per_step = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(a.steps))
+    ms_median = per_step[a.steps // 2] if a.steps % 2 else 0.5 * (per_step[a.steps // 2 - 1] +
+                                                                  per_step[a.steps // 2])
+    ms_mean = evs[0].elapsed_time(evs[a.steps]) / a.steps
+    ms_per_step = ms_median
 
     # second timed region of K steps with events between the launches: each
     # launch's average duration on the same stream (the roofline's basis)
@@ -481,6 +501,9 @@ def main():
     res = {
         "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step_mean": round(ms_mean, 4), "ms_per_step_min_max": [round(per_step[0], 4), round(per_step[-1], 4)],
+        "timing": "median of the per-step event pairs of the timed region (mean beside it)",
+        "clock_warmup_ms": round(cw_ms, 1), "clock_warmup_steps": cw_steps,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": a.dtype,
         "data": "synthetic (seeded N(0,1) on the GPU)",
         "config": {"workload": ("flash-attention backward, one launch (dQ with Delta + dK/dV), fwd outside timing"
@@ -503,14 +526,23 @@ def main():
     if dom == "bwd":
         # the one launch executes 14 N^2 d (the dQ pass recomputes S and dP)
         res["roofline"]["executed"] = round(executed / (kern[dom] * 1e-3) / 1e12, 2)
+    if one:
+        # Delta blocks whose wait ran out in the timed regions (0 expected;
+        # results are the same either way)
+        res["delta_fallbacks"] = mx.bwd_delta_fallbacks() - fb0
     if passes is not None:
         res["passes_ms"] = {n: round(t, 4) for n, t in passes.items()}
     if not a.no_probe:
         # measured ceilings (probe kernels, after the timed region): the same
         # MFMA pipe at full occupancy with independent accumulators, and HBM
         # streaming reads; `peak` stays AMD's published figure
-        mfma = mx.probe_mfma_tflops(bf16=a.dtype == "bf16", iters=256)
+        # the MFMA form the backward runs: 32x32x16 for bf16 at d = 64
+        big = a.dtype == "bf16" and a.d == 64
+        mfma = mx.probe_mfma_tflops(bf16=a.dtype == "bf16", iters=256, big=big)
         res["roofline"]["measured_peak"] = round(mfma, 1)
+        res["roofline"]["measured_peak_mfma"] = ("v_mfma_f32_32x32x16_bf16" if big else
+                                                 "v_mfma_f32_16x16x32_bf16" if a.dtype == "bf16" else
+                                                 "v_mfma_f32_16x16x4_f32")
         res["roofline"]["frac_of_measured"] = round(achieved / mfma, 4)
         res["roofline"]["hbm_measured_gbps"] = round(mx.probe_hbm_gbps(mib=1024), 1)
     if not a.no_cpu:

@@ -21,9 +21,14 @@
  *   - dtype MXFA_F32: every tensor above is fp32. dtype MXFA_BF16: Q, K, V,
  *     O, dO, dQ, dK, dV are bf16 (raw uint16 storage), LSE and Delta fp32,
  *     and all accumulation is fp32.
- *   - All launches are asynchronous on `stream`. The library never
- *     synchronises, never allocates device memory and keeps no per-call
- *     state, so calls are thread-safe; ordering is the caller's stream order.
+ *   - All launches are asynchronous on `stream`. The run_* entry points never
+ *     synchronise and never allocate device memory. The library's own state
+ *     is the one-launch backward's: a static 4 MB array of Delta flags per
+ *     device, a launch counter (epoch), the counter of mxfa_bwd_delta_fallbacks
+ *     and the settings of mxfa_set_bwd_options. Launches in flight together
+ *     on one device are safe (see mxfa_bwd_one_launch); ordering is the
+ *     caller's stream order.
+ *   - The roofline and measurement probes are declared in mxfa_probes.h.
  *   - Errors are returned as negative codes (see mxfa_status); nothing aborts
  *     and no C++ exception crosses this boundary. The reference panics on a
  *     launch failure (02-flash-attention/src/main.rs:87,122,142,172,204,209).
@@ -144,15 +149,36 @@ int mxfa_run_bwd(const mxfa_shape *shape, const void *q, const void *k, const vo
  * launch, or an invalid shape).
  * The one-launch form (bf16, d = 64 or 128) runs the dQ work-groups first;
  * they publish Delta per 128-row query block, and the dK/dV work-groups of the
- * same launch wait for the blocks they need. Each wait is bounded: after it the
- * work-group computes those Delta rows from O and dO itself. Results equal the
- * two-launch form's bitwise whenever no wait runs out. The environment
- * variable MXFA_BWD_FUSED=0, read on every call, selects two launches, and so
- * does a stream under graph capture (a replayed launch would reuse the
- * capture's flag epoch); this query answers for an ordinary stream.
+ * same launch wait for the blocks they need. Each wait is bounded in time
+ * (mxfa_bwd_options.delta_wait_us): after it the work-group computes those
+ * Delta rows from O and dO itself, with the same arithmetic as the dQ
+ * work-groups, so the results equal the two-launch form's bitwise either way.
+ * mxfa_bwd_options.one_launch = 0 selects two launches, and so does a stream
+ * under graph capture (a replayed launch would reuse the capture's flag
+ * epoch); this query answers for an ordinary stream.
  * No counterpart in the reference: it tells callers (and benchmarks) which
  * kernels the backward from O (main.rs:126-143, :179-210) becomes. */
 int mxfa_bwd_one_launch(const mxfa_shape *shape);
+
+/* Process-wide settings of the one-launch backward, read at every launch
+ * (default {1, 200}). Meant for tests and measurement; settings changed while
+ * other threads launch take effect at their next launch.
+ * No counterpart in the reference (its backward is always two launches,
+ * main.rs:179-210). */
+typedef struct {
+    int one_launch;    /* 1: one launch where available (bf16); 0: always two */
+    int delta_wait_us; /* bound of each Delta wait in microseconds; < 0: never
+                          wait, always compute Delta in the dK/dV work-group */
+} mxfa_bwd_options;
+int mxfa_set_bwd_options(const mxfa_bwd_options *options);
+int mxfa_get_bwd_options(mxfa_bwd_options *options);
+
+/* Delta blocks (64 query rows of one head) that the one-launch backward's
+ * dK/dV work-groups computed themselves on the current device, because their
+ * wait ran out, since the library was loaded. A synchronous device-to-host
+ * copy: call it after the launches of interest have completed. 0 in normal
+ * operation; a count does not change results (see mxfa_bwd_one_launch). */
+int mxfa_bwd_delta_fallbacks(unsigned long long *count);
 
 /* Bytes of device workspace the _ws entry points below can use (0 for an
  * invalid shape). dQ is a separate atomic-free pass and needs none. With GQA
@@ -237,35 +263,6 @@ typedef struct {
 int mxfa_check_prefill(const mxfa_prefill_shape *shape);
 int mxfa_run_prefill(const mxfa_prefill_shape *shape, const void *q, const void *kcache, const void *vcache,
                      void *out, void *stream);
-
-/* ---- Roofline probes: measured ceilings next to the published peaks.
- * Replace the reference's throughput audit, common/kernels/isa.cu:11-63
- * (fma_f32 / dp4a_s32 / fma_h2 chains and the stream_f4 read) driven by
- * common/examples/isa.rs:17-88, with the pipes this path runs on. The caller
- * times the launches (e.g. with events on `stream`). */
-
-/* Floats in the probes' device sink (one per probe thread). */
-int mxfa_probe_sink_len(void);
-/* Launches `iters` x 8 independent MFMAs per wave over 2048 x 256 threads:
- * v_mfma_f32_16x16x32_bf16 for MXFA_BF16, v_mfma_f32_16x16x4_f32 for
- * MXFA_F32. Writes the flops the launch performs to *flops. `sink` is a device
- * float[mxfa_probe_sink_len()] (written; the values are meaningless). */
-int mxfa_probe_mfma(int dtype, int iters, float *sink, double *flops, void *stream);
-/* Launches a grid-stride streaming read of `bytes` (a multiple of 16) at `x`,
- * the stream_f4 shape (isa.cu:55-63). */
-int mxfa_probe_read(const void *x, size_t bytes, float *sink, void *stream);
-/* Launches a grid-stride copy of `bytes` (a multiple of 16) from x to y. */
-int mxfa_probe_copy(const void *x, void *y, size_t bytes, void *stream);
-/* Replays the global writes a dQ pass fused into the dK/dV pass would make at a
- * causal shape with `bh` (batch, head) pairs, N = n (a multiple of 128) and
- * d = 64: the work-group of each 128-key block adds one 64 x 64 fp32 partial
- * tile per 64-query stage from its diagonal stage on. atomic = 1: fp32 atomic
- * adds of 1.0 (on a zeroed `acc`, element (h, row, x) ends at row / 128 + 1);
- * atomic = 0: plain stores of the same bytes. `acc` is a device
- * float[bh * n * 64]; the payload bytes are written to *bytes. No counterpart
- * in the reference: it measures the alternative that the reference's separate
- * dQ pass (attention_bwd.cu:96-158) avoids. */
-int mxfa_probe_dq_atomic(float *acc, int bh, int n, int atomic, double *bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,52 @@
+/*
+ * mxfa_probes.h - measurement probes of libmxfa (gfx950): the ceilings the
+ * flash-attention kernels of mxfa.h are measured against, and a replay of the
+ * alternative to the separate dQ pass. Not part of the attention interface;
+ * same conventions and status codes as mxfa.h.
+ */
+#ifndef MXFA_PROBES_H
+#define MXFA_PROBES_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Roofline probes: measured ceilings next to the published peaks.
+ * Replace the reference's throughput audit, common/kernels/isa.cu:11-63
+ * (fma_f32 / dp4a_s32 / fma_h2 chains and the stream_f4 read) driven by
+ * common/examples/isa.rs:17-88, with the pipes this path runs on. The caller
+ * times the launches (e.g. with events on `stream`). */
+
+/* Floats in the probes' device sink (one per probe thread). */
+int mxfa_probe_sink_len(void);
+/* Launches `iters` x 8 independent MFMAs per wave over 2048 x 256 threads:
+ * v_mfma_f32_16x16x32_bf16 for MXFA_BF16, v_mfma_f32_16x16x4_f32 for
+ * MXFA_F32. Writes the flops the launch performs to *flops. `sink` is a device
+ * float[mxfa_probe_sink_len()] (written; the values are meaningless). */
+int mxfa_probe_mfma(int dtype, int iters, float *sink, double *flops, void *stream);
+/* The same with v_mfma_f32_32x32x16_bf16 (4 independent accumulators per
+ * wave, iters x 4 MFMAs per wave): the MFMA of the bf16 d = 64 backward. */
+int mxfa_probe_mfma32(int iters, float *sink, double *flops, void *stream);
+/* Launches a grid-stride streaming read of `bytes` (a multiple of 16) at `x`,
+ * the stream_f4 shape (isa.cu:55-63). */
+int mxfa_probe_read(const void *x, size_t bytes, float *sink, void *stream);
+/* Launches a grid-stride copy of `bytes` (a multiple of 16) from x to y. */
+int mxfa_probe_copy(const void *x, void *y, size_t bytes, void *stream);
+/* Replays the global writes a dQ pass fused into the dK/dV pass would make at a
+ * causal shape with `bh` (batch, head) pairs, N = n (a multiple of 128) and
+ * d = 64: the work-group of each 128-key block adds one 64 x 64 fp32 partial
+ * tile per 64-query stage from its diagonal stage on. atomic = 1: fp32 atomic
+ * adds of 1.0 (on a zeroed `acc`, element (h, row, x) ends at row / 128 + 1);
+ * atomic = 0: plain stores of the same bytes. `acc` is a device
+ * float[bh * n * 64]; the payload bytes are written to *bytes. No counterpart
+ * in the reference: it measures the alternative that the reference's separate
+ * dQ pass (attention_bwd.cu:96-158) avoids. */
+int mxfa_probe_dq_atomic(float *acc, int bh, int n, int atomic, double *bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MXFA_PROBES_H */

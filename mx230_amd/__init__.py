@@ -47,7 +47,12 @@ EXPORTS = (
     "mxfa_run_bwd_dkv", "mxfa_run_bwd_flash", "mxfa_run_bwd_dq_delta", "mxfa_run_bwd", "mxfa_bwd_one_launch", "mxfa_bwd_workspace_bytes",
     "mxfa_run_bwd_dkv_ws", "mxfa_run_bwd_ws", "mxfa_run_bwd_naive",
     "mxfa_naive_scratch_bytes", "mxfa_run_naive_fwd", "mxfa_check_prefill", "mxfa_run_prefill",
-    "mxfa_probe_sink_len", "mxfa_probe_mfma", "mxfa_probe_read", "mxfa_probe_copy", "mxfa_probe_dq_atomic",
+    "mxfa_set_bwd_options", "mxfa_get_bwd_options", "mxfa_bwd_delta_fallbacks",
+)
+# Every symbol include/mxfa_probes.h declares.
+PROBE_EXPORTS = (
+    "mxfa_probe_sink_len", "mxfa_probe_mfma", "mxfa_probe_mfma32", "mxfa_probe_read", "mxfa_probe_copy",
+    "mxfa_probe_dq_atomic",
 )
 
 
@@ -63,6 +68,10 @@ class MxfaShape(ctypes.Structure):
     _fields_ = [("B", ctypes.c_int), ("Hq", ctypes.c_int), ("Hkv", ctypes.c_int), ("N", ctypes.c_int),
                 ("d", ctypes.c_int), ("causal", ctypes.c_int), ("dtype", ctypes.c_int),
                 ("scale", ctypes.c_float)]
+
+
+class MxfaBwdOptions(ctypes.Structure):
+    _fields_ = [("one_launch", ctypes.c_int), ("delta_wait_us", ctypes.c_int)]
 
 
 class MxfaPrefillShape(ctypes.Structure):
@@ -120,11 +129,16 @@ def load_library(path: str | None = None):
     lib.mxfa_run_prefill.argtypes = [pp, vp, vp, vp, vp, vp]
     lib.mxfa_probe_sink_len.argtypes = []
     lib.mxfa_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_int, fp, ctypes.POINTER(ctypes.c_double), vp]
+    lib.mxfa_probe_mfma32.argtypes = [ctypes.c_int, fp, ctypes.POINTER(ctypes.c_double), vp]
     lib.mxfa_probe_read.argtypes = [vp, ctypes.c_size_t, fp, vp]
     lib.mxfa_probe_copy.argtypes = [vp, vp, ctypes.c_size_t, vp]
     lib.mxfa_probe_dq_atomic.argtypes = [fp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                          ctypes.POINTER(ctypes.c_double), vp]
-    for name in EXPORTS:
+    op = ctypes.POINTER(MxfaBwdOptions)
+    lib.mxfa_set_bwd_options.argtypes = [op]
+    lib.mxfa_get_bwd_options.argtypes = [op]
+    lib.mxfa_bwd_delta_fallbacks.argtypes = [ctypes.POINTER(ctypes.c_ulonglong)]
+    for name in EXPORTS + PROBE_EXPORTS:
         if name not in ("mxfa_version", "mxfa_strerror", "mxfa_bwd_workspace_bytes",
                         "mxfa_naive_scratch_bytes"):
             getattr(lib, name).restype = ctypes.c_int
@@ -271,10 +285,10 @@ def run_bwd_flash(q, k, v, do, lse, delta, dq, dk, dv, causal: bool, scale: floa
 
 
 def run_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, causal: bool, scale: float = 0.0, stream=None):
-    """The whole backward from O in two launches (mxfa_run_bwd): the dQ pass
-    computes Delta = rowsum(dO * O) itself and writes it to ``delta`` for the
-    dK/dV pass (run_preprocess + run_bwd_flash with the preprocess launch folded
-    in). Outputs are overwritten."""
+    """The whole backward from O (mxfa_run_bwd): the dQ work computes
+    Delta = rowsum(dO * O) itself and writes it to ``delta`` for the dK/dV
+    work (run_preprocess + run_bwd_flash with the preprocess launch folded in);
+    one launch for bf16 (bwd_one_launch), else two. Outputs are overwritten."""
     sh = shape_of(q, k, causal, scale)
     dt, qs, ks = _io(sh)
     args = [_expect(q, "q", qs, dt), _expect(k, "k", ks, dt), _expect(v, "v", ks, dt), _expect(o, "o", qs, dt),
@@ -285,9 +299,37 @@ def run_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, causal: bool, scale: float =
 
 def bwd_one_launch(q, k, causal: bool) -> bool:
     """True if run_bwd runs the backward as one launch for this shape
-    (mxfa_bwd_one_launch; MXFA_BWD_FUSED=0 selects two launches)."""
+    (mxfa_bwd_one_launch; set_bwd_options(one_launch=False) selects two
+    launches)."""
     sh = shape_of(q, k, causal)
     return bool(load_library().mxfa_bwd_one_launch(ctypes.byref(sh.c())))
+
+
+def get_bwd_options() -> dict:
+    """The one-launch backward's process-wide settings (mxfa_get_bwd_options)."""
+    o = MxfaBwdOptions()
+    _check("mxfa_get_bwd_options", load_library().mxfa_get_bwd_options(ctypes.byref(o)))
+    return {"one_launch": bool(o.one_launch), "delta_wait_us": o.delta_wait_us}
+
+
+def set_bwd_options(one_launch: bool | None = None, delta_wait_us: int | None = None) -> dict:
+    """Changes the given settings (mxfa_set_bwd_options) and returns the
+    previous ones. one_launch=False: always two launches; delta_wait_us < 0:
+    the dK/dV work-groups never wait for Delta and compute it themselves."""
+    old = get_bwd_options()
+    o = MxfaBwdOptions(int(old["one_launch"] if one_launch is None else one_launch),
+                       old["delta_wait_us"] if delta_wait_us is None else int(delta_wait_us))
+    _check("mxfa_set_bwd_options", load_library().mxfa_set_bwd_options(ctypes.byref(o)))
+    return old
+
+
+def bwd_delta_fallbacks() -> int:
+    """Delta blocks the one-launch backward computed in its dK/dV work-groups
+    on the current device since load (mxfa_bwd_delta_fallbacks; synchronise the
+    launches of interest first)."""
+    n = ctypes.c_ulonglong(0)
+    _check("mxfa_bwd_delta_fallbacks", load_library().mxfa_bwd_delta_fallbacks(ctypes.byref(n)))
+    return int(n.value)
 
 
 def bwd_workspace_bytes(q, k, causal: bool) -> int:
@@ -470,9 +512,10 @@ def _time_ms(launch, reps: int) -> float:
     return start.elapsed_time(stop) / reps
 
 
-def probe_mfma_tflops(bf16: bool = True, iters: int = 256, reps: int = 5) -> float:
+def probe_mfma_tflops(bf16: bool = True, iters: int = 256, reps: int = 5, big: bool = False) -> float:
     """Measured MFMA throughput (TFLOP/s) of the whole device: every wave issues
-    independent v_mfma_f32_16x16x32_bf16 (bf16) or v_mfma_f32_16x16x4_f32 (fp32)."""
+    independent v_mfma_f32_16x16x32_bf16 (bf16), v_mfma_f32_32x32x16_bf16
+    (bf16, big) or v_mfma_f32_16x16x4_f32 (fp32)."""
     torch = _torch()
     lib = load_library()
     sink = torch.empty(lib.mxfa_probe_sink_len(), dtype=torch.float32, device="cuda")
@@ -481,8 +524,11 @@ def probe_mfma_tflops(bf16: bool = True, iters: int = 256, reps: int = 5) -> flo
     stream = _stream(None)
 
     def launch():
-        _check("mxfa_probe_mfma", lib.mxfa_probe_mfma(dt, iters, _ptr(sink, "sink", torch.float32),
-                                                      ctypes.byref(flops), stream))
+        sp = _ptr(sink, "sink", torch.float32)
+        if bf16 and big:
+            _check("mxfa_probe_mfma32", lib.mxfa_probe_mfma32(iters, sp, ctypes.byref(flops), stream))
+        else:
+            _check("mxfa_probe_mfma", lib.mxfa_probe_mfma(dt, iters, sp, ctypes.byref(flops), stream))
     ms = _time_ms(launch, reps)
     return flops.value / (ms * 1e-3) / 1e12
 

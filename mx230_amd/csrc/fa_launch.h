@@ -23,6 +23,15 @@ int dkv_split(const Params &p, int dtype_bf16, int d);
 // second launch): available for the shape, and launched with its own epoch.
 bool bwd_fused_available(const Params &p, int dtype_bf16, int d, hipStream_t stream);
 hipError_t launch_bwd_fused(const Params &p, int d, int causal, hipStream_t stream);
+// Process-wide settings of the one-launch backward: whether it is used where
+// available, and the bound of each Delta wait in microseconds (< 0: never
+// wait, always compute Delta); read at every launch.
+void set_bwd_options(int one_launch, int delta_wait_us);
+void get_bwd_options(int *one_launch, int *delta_wait_us);
+// Delta blocks the one-launch backward's dK/dV work-groups computed
+// themselves on the current device since the library was loaded (a
+// synchronous copy).
+hipError_t read_delta_fallbacks(unsigned long long *count);
 hipError_t launch_bwd_naive(const Params &p, int d, int causal, hipStream_t stream);
 hipError_t launch_naive_fwd(const Params &p, float *s, int d, int causal, hipStream_t stream);
 
@@ -30,6 +39,8 @@ hipError_t launch_naive_fwd(const Params &p, float *s, int d, int causal, hipStr
 int probe_sink_len();
 double probe_mfma_flops(int bf16, int iters);
 hipError_t launch_probe_mfma(int bf16, int iters, float *sink, hipStream_t stream);
+double probe_mfma32_flops(int iters);
+hipError_t launch_probe_mfma32(int iters, float *sink, hipStream_t stream);
 hipError_t launch_probe_read(const void *x, size_t bytes, float *sink, hipStream_t stream);
 hipError_t launch_probe_copy(const void *x, void *y, size_t bytes, hipStream_t stream);
 double probe_dq_atomic_bytes(int bh, int n);

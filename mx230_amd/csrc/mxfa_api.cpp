@@ -2,6 +2,7 @@
 // mapping of mxfa_shape onto kernel parameters, and error translation. No
 // device memory is allocated and nothing synchronises here.
 #include "../../include/mxfa.h"
+#include "../../include/mxfa_probes.h"
 
 #include <hip/hip_runtime.h>
 
@@ -30,6 +31,9 @@ int check_shape(const mxfa_shape *s) {
     const long long bh = (long long)s->B * s->Hq;
     if (bh > 0x7fffffffLL) return MXFA_ERR_SHAPE;
     if (((long long)s->N + 63) / 64 > kMaxGridY) return MXFA_ERR_SHAPE;
+    // every tensor (and workspace) size in bytes must be far from overflowing
+    // size_t: at most 2^40 elements per tensor (no single GPU holds more)
+    if ((double)bh * (double)s->N * (double)s->d > 1099511627776.0) return MXFA_ERR_SHAPE;
     if (s->d != 64 && s->d != 128) return MXFA_ERR_UNSUPPORTED;
     if (s->dtype == MXFA_F32 && s->d != 64) return MXFA_ERR_UNSUPPORTED;
     return MXFA_OK;
@@ -262,6 +266,24 @@ int mxfa_bwd_one_launch(const mxfa_shape *shape) {
     return mxfa::bwd_fused_available(p, shape->dtype == MXFA_BF16, shape->d, nullptr) ? 1 : 0;
 }
 
+int mxfa_set_bwd_options(const mxfa_bwd_options *options) {
+    if (options == nullptr) return MXFA_ERR_NULL;
+    if (options->one_launch != 0 && options->one_launch != 1) return MXFA_ERR_SHAPE;
+    mxfa::set_bwd_options(options->one_launch, options->delta_wait_us);
+    return MXFA_OK;
+}
+
+int mxfa_get_bwd_options(mxfa_bwd_options *options) {
+    if (options == nullptr) return MXFA_ERR_NULL;
+    mxfa::get_bwd_options(&options->one_launch, &options->delta_wait_us);
+    return MXFA_OK;
+}
+
+int mxfa_bwd_delta_fallbacks(unsigned long long *count) {
+    if (count == nullptr) return MXFA_ERR_NULL;
+    return mxfa::read_delta_fallbacks(count) == hipSuccess ? MXFA_OK : MXFA_ERR_DEVICE;
+}
+
 size_t mxfa_bwd_workspace_bytes(const mxfa_shape *shape) {
     if (check_shape(shape) != MXFA_OK) return 0;
     const Params p = make_params(shape);
@@ -363,6 +385,14 @@ int mxfa_probe_mfma(int dtype, int iters, float *sink, double *flops, void *stre
     if (!aligned16(sink)) return MXFA_ERR_ALIGN;
     *flops = mxfa::probe_mfma_flops(dtype == MXFA_BF16, iters);
     return from_hip(mxfa::launch_probe_mfma(dtype == MXFA_BF16, iters, sink, static_cast<hipStream_t>(stream)));
+}
+
+int mxfa_probe_mfma32(int iters, float *sink, double *flops, void *stream) {
+    if (iters < 1) return MXFA_ERR_SHAPE;
+    if (sink == nullptr || flops == nullptr) return MXFA_ERR_NULL;
+    if (!aligned16(sink)) return MXFA_ERR_ALIGN;
+    *flops = mxfa::probe_mfma32_flops(iters);
+    return from_hip(mxfa::launch_probe_mfma32(iters, sink, static_cast<hipStream_t>(stream)));
 }
 
 int mxfa_probe_read(const void *x, size_t bytes, float *sink, void *stream) {

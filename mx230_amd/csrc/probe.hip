@@ -64,6 +64,40 @@ __global__ __launch_bounds__(kProbeThreads) void probe_mfma_kernel(float *sink, 
     sink[blockIdx.x * kProbeThreads + tid] = s;
 }
 
+// The same for v_mfma_f32_32x32x16_bf16 (the backward's tiles at d = 64):
+// 4 independent 16-register accumulators per wave.
+constexpr int kChains32 = 4;
+__global__ __launch_bounds__(kProbeThreads) void probe_mfma32_kernel(float *sink, int iters) {
+    const int tid = threadIdx.x;
+    f32x16 acc[kChains32];
+#pragma unroll
+    for (int j = 0; j < kChains32; ++j) acc[j] = f32x16{};
+    constexpr int kUnroll = 4;
+    const int outer = (iters + kUnroll - 1) / kUnroll;
+    bf16x8 a, b;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        a[e] = (__bf16)(0.001f * (float)((tid + e) & 7));
+        b[e] = (__bf16)(0.002f * (float)((tid ^ e) & 7));
+    }
+    for (int i = 0; i < outer; ++i) {
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+#pragma unroll
+            for (int j = 0; j < kChains32; ++j)
+                asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc[j]) : "v"(a), "v"(b));
+        }
+    }
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");  // results settle before the VALU reads them
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < kChains32; ++j) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s += acc[j][r];
+    }
+    sink[blockIdx.x * kProbeThreads + tid] = s;
+}
+
 // Streaming read of n16 16-byte vectors, grid-stride (the stream_f4 shape).
 __global__ __launch_bounds__(kProbeThreads) void probe_read_kernel(const float4 *x, size_t n16, float *sink) {
     float s = 0.f;
@@ -139,6 +173,17 @@ hipError_t launch_probe_mfma(int bf16, int iters, float *sink, hipStream_t strea
     } else {
         hipLaunchKernelGGL((probe_mfma_kernel<false>), dim3(kProbeBlocks), dim3(kProbeThreads), 0, stream, sink, iters);
     }
+    return hipGetLastError();
+}
+
+double probe_mfma32_flops(int iters) {
+    const double waves = (double)kProbeBlocks * (kProbeThreads / 64);
+    const int rounded = (iters + 3) / 4 * 4;
+    return waves * (double)rounded * kChains32 * (2.0 * 32 * 32 * 16);
+}
+
+hipError_t launch_probe_mfma32(int iters, float *sink, hipStream_t stream) {
+    hipLaunchKernelGGL(probe_mfma32_kernel, dim3(kProbeBlocks), dim3(kProbeThreads), 0, stream, sink, iters);
     return hipGetLastError();
 }
 

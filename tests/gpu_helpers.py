@@ -81,6 +81,27 @@ def gpu_fwd_bwd(q, k, v, do, causal, bf16, scale=0.0):
     return tuple(to_np(t) for t in (o, lse, delta, dq, dk, dv))
 
 
+def gpu_fwd_bwd_timed(q, k, v, do, causal, bf16, scale=0.0):
+    """The forward, then the backward exactly as bench.py and its config table
+    time it: mxfa_run_bwd_ws (one launch for bf16; the dQ work computes Delta
+    itself) with the GQA split's workspace where the shape has one. Returns
+    numpy float32 (O, LSE, Delta, dQ, dK, dV)."""
+    import torch
+    import mx230_amd as mx
+    tq, tk, tv, tdo = (to_dev(x, bf16) for x in (q, k, v, do))
+    B, Hq, N, d = q.shape
+    o = torch.empty_like(tq)
+    lse = torch.empty((B, Hq, N), dtype=torch.float32, device="cuda")
+    delta = torch.empty_like(lse)
+    mx.run_flash_lse(tq, tk, tv, o, lse, causal, scale)
+    nws = mx.bwd_workspace_bytes(tq, tk, causal)
+    ws = torch.empty(nws, dtype=torch.uint8, device="cuda") if nws else None
+    dq, dk, dv = torch.empty_like(tq), torch.empty_like(tk), torch.empty_like(tv)
+    mx.run_bwd_ws(tq, tk, tv, o, tdo, lse, delta, dq, dk, dv, ws, causal, scale)
+    torch.cuda.synchronize()
+    return tuple(to_np(t) for t in (o, lse, delta, dq, dk, dv))
+
+
 def oracle_fwd_bwd(q, k, v, do, causal, scale=None):
     B, Hq, N, d = q.shape
     Hkv = k.shape[1]

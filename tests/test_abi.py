@@ -14,6 +14,7 @@ import mx230_amd as mx
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "mxfa.h")
+PROBE_HEADER = os.path.join(ROOT, "include", "mxfa_probes.h")
 
 
 @pytest.fixture(scope="module")
@@ -23,20 +24,21 @@ def lib():
     return mx.load_library()
 
 
-def _declared():
-    text = open(HEADER).read()
-    return sorted(set(re.findall(r"\b(mxfa_[a-z_]+)\s*\(", text)))
+def _declared(header=HEADER):
+    text = open(header).read()
+    return sorted(set(re.findall(r"\b(mxfa_[a-z0-9_]+)\s*\(", text)))
 
 
 def test_header_and_python_agree():
     assert sorted(mx.EXPORTS) == _declared()
+    assert sorted(mx.PROBE_EXPORTS) == _declared(PROBE_HEADER)
 
 
 def test_every_declared_symbol_is_exported(lib):
     out = subprocess.run(["nm", "-D", "--defined-only", mx.LIB_PATH], capture_output=True,
                          text=True, check=True).stdout
     exported = set(re.findall(r"\bT (mxfa_\w+)", out))
-    for name in _declared():
+    for name in _declared() + _declared(PROBE_HEADER):
         assert name in exported, name
         assert hasattr(lib, name)
 
@@ -123,8 +125,26 @@ def test_bwd_workspace_bytes(lib, kw, nbytes):
     assert lib.mxfa_bwd_workspace_bytes(ctypes.byref(_shape(**kw))) == nbytes
 
 
-def test_bwd_one_launch(lib, monkeypatch):
-    monkeypatch.delenv("MXFA_BWD_FUSED", raising=False)
+@pytest.fixture
+def default_options():
+    old = mx.set_bwd_options(one_launch=True, delta_wait_us=200)
+    yield
+    mx.set_bwd_options(**old)
+
+
+def test_bwd_options(lib, default_options):
+    o = mx.MxfaBwdOptions()
+    assert lib.mxfa_get_bwd_options(ctypes.byref(o)) == 0
+    assert (o.one_launch, o.delta_wait_us) == (1, 200)
+    assert lib.mxfa_set_bwd_options(None) == mx_status("MXFA_ERR_NULL")
+    assert lib.mxfa_get_bwd_options(None) == mx_status("MXFA_ERR_NULL")
+    assert lib.mxfa_set_bwd_options(ctypes.byref(mx.MxfaBwdOptions(2, 5))) == mx_status("MXFA_ERR_SHAPE")
+    assert lib.mxfa_set_bwd_options(ctypes.byref(mx.MxfaBwdOptions(0, -1))) == 0
+    assert mx.get_bwd_options() == {"one_launch": False, "delta_wait_us": -1}
+    assert lib.mxfa_bwd_delta_fallbacks(None) == mx_status("MXFA_ERR_NULL")
+
+
+def test_bwd_one_launch(lib, default_options):
     assert lib.mxfa_bwd_one_launch(ctypes.byref(_shape(B=4, Hq=12, Hkv=12, N=4096))) == 1
     assert lib.mxfa_bwd_one_launch(ctypes.byref(_shape(d=128))) == 1
     assert lib.mxfa_bwd_one_launch(ctypes.byref(_shape(dtype=mx.MXFA_F32))) == 0
@@ -133,7 +153,7 @@ def test_bwd_one_launch(lib, monkeypatch):
     # more (batch, head, 128-row block) flags than one slot holds: two launches
     assert lib.mxfa_bwd_one_launch(ctypes.byref(_shape(B=64, Hq=64, Hkv=64, N=8192))) == 1  # 2^18: fits
     assert lib.mxfa_bwd_one_launch(ctypes.byref(_shape(B=64, Hq=64, Hkv=64, N=8193))) == 0
-    monkeypatch.setenv("MXFA_BWD_FUSED", "0")
+    mx.set_bwd_options(one_launch=False)
     assert lib.mxfa_bwd_one_launch(ctypes.byref(_shape(B=4, Hq=12, Hkv=12, N=4096))) == 0
 
 

@@ -1,21 +1,21 @@
 """The one-launch backward (bwd_fused_kernel, the default of mxfa_run_bwd for
 bf16): dQ work-groups publish Delta per 128-row block behind a flag, and the
 dK/dV work-groups of the same launch wait for it, or compute the rows
-themselves after a bounded wait.
+themselves after a wait bounded in time.
 
 - With flags it is bitwise equal to the two-launch backward
-  (MXFA_BWD_FUSED=0), over shapes and over repeated runs, since it stages
-  the same Delta values. A stale or early read of Delta would show as a
-  mismatch.
-- With every wait forced to give up (MXFA_DELTA_SPIN=-1) the dK/dV work-groups
-  compute Delta from O and dO in another summation order. dK and dV then
-  equal the two-launch ones up to flips of their last bf16 bit: within 2^-7 of
-  the outputs' max (one bf16 ulp of the largest element is 2^-8 of it).
+  (set_bwd_options(one_launch=False)), over shapes and over repeated runs,
+  since it stages the same Delta values. A stale or early read of Delta would
+  show as a mismatch.
+- With every wait forced to give up (delta_wait_us < 0) the dK/dV work-groups
+  compute Delta from O and dO with the dQ work-groups' own arithmetic, so the
+  results are still bitwise equal, and the device's fallback counter grows by
+  one per stage.
 - With a GQA split through a workspace, the one launch plus the reduce equal
   the two-launch split bitwise.
 - Launches in flight together on several streams, more than the flag slots,
   so later launches see other launches' flags, still give each one its own
-  result.
+  result, bitwise.
 """
 from __future__ import annotations
 
@@ -23,10 +23,9 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-BF16_FLIPS = 2.0 ** -7  # bf16 outputs whose last bit may flip, relative to the max
-
 SHAPES = [
     ("north-star", (4, 12, 12, 4096, 64), True),
+    ("cfg5-d64", (1, 32, 4, 2048, 64), True),
     ("gqa-ragged", (2, 14, 2, 777, 64), True),
     ("gqa-noncausal", (1, 6, 2, 576, 64), False),
     ("d128", (1, 8, 8, 1000, 128), True),
@@ -34,6 +33,15 @@ SHAPES = [
     ("n1", (1, 4, 4, 1, 64), True),
     ("n130", (2, 3, 3, 130, 64), False),
 ]
+
+
+@pytest.fixture
+def opts():
+    """set(one_launch=..., delta_wait_us=...) for the test; the defaults after it."""
+    import mx230_amd as mx
+    old = mx.set_bwd_options(one_launch=True, delta_wait_us=200)
+    yield lambda **kw: mx.set_bwd_options(**kw)
+    mx.set_bwd_options(**old)
 
 
 def _setup(B, H, Hkv, N, d, causal, seed=1):
@@ -68,11 +76,11 @@ def _sync(outs):
 
 
 @pytest.mark.parametrize("name,shape,causal", SHAPES, ids=[s[0] for s in SHAPES])
-def test_one_launch_equals_two_launches(monkeypatch, name, shape, causal):
+def test_one_launch_equals_two_launches(opts, name, shape, causal):
     t = _setup(*shape, causal)
-    monkeypatch.setenv("MXFA_BWD_FUSED", "0")
+    opts(one_launch=False)
     ref = _sync(_bwd(t, causal))
-    monkeypatch.setenv("MXFA_BWD_FUSED", "1")
+    opts(one_launch=True)
     import torch
     for rep in range(3):
         got = _sync(_bwd(t, causal))
@@ -80,47 +88,48 @@ def test_one_launch_equals_two_launches(monkeypatch, name, shape, causal):
             assert torch.equal(a, b), f"{name} run {rep}: {n} differs from the two-launch backward"
 
 
-def test_one_launch_repeated_north_star(monkeypatch):
+def test_one_launch_repeated_north_star(opts):
     import torch
     t = _setup(4, 12, 12, 4096, 64, True, seed=7)
-    monkeypatch.setenv("MXFA_BWD_FUSED", "0")
+    opts(one_launch=False)
     ref = _sync(_bwd(t, True))
-    monkeypatch.setenv("MXFA_BWD_FUSED", "1")
+    opts(one_launch=True)
     outs = [_bwd(t, True) for _ in range(20)]
     torch.cuda.synchronize()
     bad = sum(not all(torch.equal(a, b) for a, b in zip(got, ref)) for got in outs)
     assert bad == 0, f"{bad} of 20 one-launch runs differ"
 
 
-def _rel(a, b):
-    a, b = a.float(), b.float()
-    return ((a - b).abs().max() / b.abs().max().clamp_min(1e-30)).item()
-
-
 @pytest.mark.parametrize("name,shape,causal", SHAPES, ids=[s[0] for s in SHAPES])
-def test_one_launch_fallback(monkeypatch, name, shape, causal):
-    t = _setup(*shape, causal, seed=3)
-    monkeypatch.setenv("MXFA_BWD_FUSED", "0")
-    ref = _sync(_bwd(t, causal))
-    monkeypatch.setenv("MXFA_BWD_FUSED", "1")
-    monkeypatch.setenv("MXFA_DELTA_SPIN", "-1")
-    got = _sync(_bwd(t, causal))
+def test_one_launch_fallback(opts, name, shape, causal):
     import torch
-    assert torch.equal(got[0], ref[0]) and torch.equal(got[1], ref[1])  # Delta and dQ come from the dQ pass
-    for n, a, b in zip(("dK", "dV"), got[2:], ref[2:]):
-        e = _rel(a, b)
-        print(f"[{name}] fallback {n} {e:.2e}", flush=True)
-        assert e <= BF16_FLIPS, (name, n, e)
+    import mx230_amd as mx
+    t = _setup(*shape, causal, seed=3)
+    opts(one_launch=False)
+    ref = _sync(_bwd(t, causal))
+    opts(one_launch=True, delta_wait_us=-1)
+    n0 = mx.bwd_delta_fallbacks()
+    got = _sync(_bwd(t, causal))
+    n1 = mx.bwd_delta_fallbacks()
+    for n, a, b in zip(("Delta", "dQ", "dK", "dV"), got, ref):
+        assert torch.equal(a, b), f"{name}: {n} of the fallback differs from the two-launch backward"
+    # one fallback per stage of every dK/dV work-group: at least one per
+    # (KV head, key block), and none when the waits are allowed
+    B, H, Hkv, N, d = shape
+    assert n1 - n0 >= B * Hkv * ((N + 127) // 128) // 2, (n0, n1)
+    opts(delta_wait_us=200)
+    _sync(_bwd(t, causal))
+    print(f"[{name}] fallbacks forced {n1 - n0}, then {mx.bwd_delta_fallbacks() - n1}", flush=True)
 
 
-def test_one_launch_concurrent_streams(monkeypatch):
+def test_one_launch_concurrent_streams(opts):
     """Six launches in flight on six streams (four flag slots)."""
     import torch
-    monkeypatch.setenv("MXFA_BWD_FUSED", "1")
+    opts(one_launch=True)
     cases = [_setup(2, 6, 2, 1000 + 64 * i, 64, True, seed=20 + i) for i in range(6)]
-    monkeypatch.setenv("MXFA_BWD_FUSED", "0")
+    opts(one_launch=False)
     refs = [_sync(_bwd(t, True)) for t in cases]
-    monkeypatch.setenv("MXFA_BWD_FUSED", "1")
+    opts(one_launch=True)
     streams = [torch.cuda.Stream() for _ in cases]
     torch.cuda.synchronize()
     outs = []
@@ -129,15 +138,14 @@ def test_one_launch_concurrent_streams(monkeypatch):
             outs.append(_bwd(t, True, stream=s))
     torch.cuda.synchronize()
     for i, (got, ref) in enumerate(zip(outs, refs)):
-        assert torch.equal(got[0], ref[0]) and torch.equal(got[1], ref[1]), i
-        for n, a, b in zip(("dK", "dV"), got[2:], ref[2:]):
-            e = _rel(a, b)
-            assert e <= BF16_FLIPS, (i, n, e)
+        for n, a, b in zip(("Delta", "dQ", "dK", "dV"), got, ref):
+            assert torch.equal(a, b), (i, n)
 
 
-@pytest.mark.parametrize("shape", [(2, 14, 2, 4096, 64), (1, 32, 4, 2048, 128), (1, 8, 2, 300, 64)],
-                         ids=["cfg4", "cfg5-d128", "ragged"])
-def test_one_launch_with_gqa_split(monkeypatch, shape):
+@pytest.mark.parametrize("shape", [(2, 14, 2, 4096, 64), (1, 32, 4, 2048, 64), (1, 32, 4, 2048, 128),
+                                   (1, 8, 2, 300, 64)],
+                         ids=["cfg4", "cfg5-d64", "cfg5-d128", "ragged"])
+def test_one_launch_with_gqa_split(opts, shape):
     import torch
     import mx230_amd as mx
     t = _setup(*shape, True, seed=9)
@@ -153,9 +161,9 @@ def test_one_launch_with_gqa_split(monkeypatch, shape):
         torch.cuda.synchronize()
         return delta, dq, dk, dv
 
-    monkeypatch.setenv("MXFA_BWD_FUSED", "0")
+    opts(one_launch=False)
     ref = run()
-    monkeypatch.setenv("MXFA_BWD_FUSED", "1")
+    opts(one_launch=True)
     for rep in range(3):
         got = run()
         for n, a, b in zip(("Delta", "dQ", "dK", "dV"), got, ref):

@@ -1,7 +1,9 @@
 """Roofline probes on the MI355X: measured ceilings fall inside what the part
 can physically do (AMD's published dense peaks: bf16 MFMA 2516.6 TFLOP/s, fp32
-MFMA 157.3 TFLOP/s, HBM3E 8 TB/s) and well above what a broken probe (a
-serialised chain, a partial grid) would show."""
+MFMA 157.3 TFLOP/s, HBM3E 8 TB/s) and above 60% of those peaks: boxes measured
+so far hold 1.86-2.40 PFLOP/s bf16, 127-137 TFLOP/s fp32 and 6.3-6.4 TB/s of
+streaming reads, while a broken probe (a serialised chain, a partial grid, an
+accumulator round trip through memory) shows half or less."""
 from __future__ import annotations
 
 import pytest
@@ -9,18 +11,19 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 
-def test_probe_mfma_bf16():
+@pytest.mark.parametrize("big", [False, True], ids=["16x16x32", "32x32x16"])
+def test_probe_mfma_bf16(big):
     import mx230_amd as mx
-    t = mx.probe_mfma_tflops(bf16=True)
-    print(f"\n[probe] bf16 MFMA {t:.0f} TFLOP/s", flush=True)
-    assert 1000.0 < t < 2600.0
+    t = mx.probe_mfma_tflops(bf16=True, big=big)
+    print(f"\n[probe] bf16 MFMA {'32x32x16' if big else '16x16x32'} {t:.0f} TFLOP/s", flush=True)
+    assert 0.6 * 2516.6 < t < 2600.0
 
 
 def test_probe_mfma_fp32():
     import mx230_amd as mx
     t = mx.probe_mfma_tflops(bf16=False)
     print(f"\n[probe] fp32 MFMA {t:.1f} TFLOP/s", flush=True)
-    assert 60.0 < t < 165.0
+    assert 0.6 * 157.3 < t < 165.0
 
 
 @pytest.mark.parametrize("copy", [False, True], ids=["read", "copy"])
@@ -28,7 +31,7 @@ def test_probe_hbm(copy):
     import mx230_amd as mx
     g = mx.probe_hbm_gbps(mib=1024, copy=copy)
     print(f"\n[probe] HBM {'copy' if copy else 'read'} {g:.0f} GB/s", flush=True)
-    assert 2000.0 < g < 8200.0
+    assert (0.6 if not copy else 0.45) * 8000.0 < g < 8200.0
 
 
 def test_probe_dq_atomic_counts_and_rates():
