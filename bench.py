@@ -536,12 +536,10 @@ def main():
         # measured ceilings (probe kernels, after the timed region): the same
         # MFMA pipe at full occupancy with independent accumulators, and HBM
         # streaming reads; `peak` stays AMD's published figure
-        # the MFMA form the backward runs: 32x32x16 for bf16 at d = 64
-        big = a.dtype == "bf16" and a.d == 64
-        mfma = mx.probe_mfma_tflops(bf16=a.dtype == "bf16", iters=256, big=big)
+        # the MFMA form the backward runs
+        mfma = mx.probe_mfma_tflops(bf16=a.dtype == "bf16", iters=256)
         res["roofline"]["measured_peak"] = round(mfma, 1)
-        res["roofline"]["measured_peak_mfma"] = ("v_mfma_f32_32x32x16_bf16" if big else
-                                                 "v_mfma_f32_16x16x32_bf16" if a.dtype == "bf16" else
+        res["roofline"]["measured_peak_mfma"] = ("v_mfma_f32_16x16x32_bf16" if a.dtype == "bf16" else
                                                  "v_mfma_f32_16x16x4_f32")
         res["roofline"]["frac_of_measured"] = round(achieved / mfma, 4)
         res["roofline"]["hbm_measured_gbps"] = round(mx.probe_hbm_gbps(mib=1024), 1)

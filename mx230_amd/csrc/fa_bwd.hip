@@ -20,9 +20,8 @@
 //     head), Q/dO rows in registers; K/V stream through LDS 64 keys per stage.
 //     It recomputes S and dP (the price of staying atomic-free and O(N) in
 //     memory).
-// The per-wave register state and arithmetic of each pass is a tile class:
-// the 32x32x16 bf16 MFMA tiles (DqTileW64, DkvTileW64) for bf16 with d = 64,
-// the 16x16 MFMA tiles (DqTile16, DkvTile16) for fp32 and for bf16 d = 128.
+// The per-wave register state and arithmetic of each pass is a tile class
+// (DqTile16, DkvTile16: 16x16 MFMA tiles, 32 rows per wave at d = 64).
 #include <algorithm>
 #include <atomic>
 #include <cmath>
@@ -376,13 +375,13 @@ struct DkvTile16 {
                 for (int r = 0; r < 4; ++r) {
 #pragma unroll
                     for (int kt = 0; kt < KT; ++kt) {
-                        float x = s[t][kt][r];
+                        float x = Pol::kExactScale ? s[t][kt][r] * xmul : s[t][kt][r];
                         if constexpr (MASK) {
                             // causal: query qs + 32 blk + bidx(t, g, r) before key kw0 + 16 kt + l16
                             const bool before = Pol::bidx(t, g, r) - l16 < kw0 - qs + 16 * kt - 32 * blk;
                             x = before ? -INFINITY : x;
                         }
-                        const float pv = fast_exp2(Pol::kExactScale ? x * xmul : x);
+                        const float pv = fast_exp2(x);
                         s[t][kt][r] = pv;
                         dp[t][kt][r] = pv * dp[t][kt][r];  // -dS / scale
                     }
@@ -421,266 +420,6 @@ struct DkvTile16 {
                     store4<U>(dK + (size_t)key * D + 16 * xt + 4 * g, accK[xt][kt], kmul);
                     store4<U>(dV + (size_t)key * D + 16 * xt + 4 * g, accV[xt][kt], 1.0f);
                 }
-            }
-        }
-    }
-};
-
-// 32x32x16 bf16 MFMA tiles, d = 64 (PolW64): a wave owns 32 rows, one 32x32
-// C tile per matrix, and each 32-row block of a stage is one chain: the first
-// products (S, dP) over d in 4 MFMAs each, their C tile packed to bf16 as the
-// B operand of the chained products (2 MFMAs of k = 16 over the block's 32
-// rows per 32 columns of d). Half the MFMA issues of the 16x16 form for the
-// same work, so more of the softmax VALU work runs in the MFMAs' shadow.
-
-// dQ: S^T = K Q^T and (Delta - dP)^T = Delta + (-V)(dO)^T with keys on the C
-// rows and this wave's 32 queries on the columns, so each lane's LSE and Delta
-// are one value. The exponent is s scale log2(e) - L log2(e), one fma per
-// score from exact Q, and the score accumulators start at zero.
-struct DqTileW64 {
-    using Pol = PolW64;
-    using T = u16;
-    using Frag = bf16x8;
-    static constexpr int D = 64, ROWS = 32;
-    static constexpr int kWaves = 3;
-    static constexpr bool kPrioFused = true;
-
-    Frag qf[4], dof[4];  // [m]: d elements 16m + 8h .. +7 of query q0 + l%32
-    float nl, xm;        // exponent of P = s xm + nl
-    float Dl;
-    f32x16 acc[2];  // [xt]: (-dQ / scale)^T, rows d 32xt + 8i + 4h + j, column query
-
-    // Delta of the 32 d elements of lane group h (chunks 2m + h of the row);
-    // the two halves are added with a lane swap.
-    __device__ static __forceinline__ float half_part(const Frag (&a)[4], const Frag (&b)[4]) {
-        float t = 0.f;
-#pragma unroll
-        for (int m = 0; m < 4; ++m) t += dot8(a[m], b[m]);
-        return t;
-    }
-
-    template <bool DELTA, bool PUBLISH>
-    __device__ __forceinline__ void load(const Params &p, int bh, int q0, int lane) {
-        const int h = lane >> 5;
-        const int N = p.N;
-        const int qi = q0 + (lane & 31);
-        const bool ok = qi < N;
-        const size_t row = ((size_t)bh * N + qi) * D;
-        const T *Q = static_cast<const T *>(p.q) + row;
-        const T *dO = static_cast<const T *>(p.dout) + row;
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            qf[m] = ok ? *reinterpret_cast<const Frag *>(Q + 16 * m + 8 * h) : Frag{};
-            dof[m] = ok ? *reinterpret_cast<const Frag *>(dO + 16 * m + 8 * h) : Frag{};
-        }
-        if constexpr (DELTA) {
-            const T *O = static_cast<const T *>(p.o_in) + row;
-            Frag of[4];
-#pragma unroll
-            for (int m = 0; m < 4; ++m) of[m] = ok ? *reinterpret_cast<const Frag *>(O + 16 * m + 8 * h) : Frag{};
-            const float t = half_part(dof, of);
-            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(t), __float_as_uint(t), false, false);
-            Dl = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-            if (ok && h == 0) {
-                if constexpr (PUBLISH) {
-                    store_wt(p.delta + (size_t)bh * N + qi, __float_as_uint(Dl));
-                } else {
-                    p.delta[(size_t)bh * N + qi] = Dl;
-                }
-            }
-        } else {
-            Dl = ok ? p.delta[(size_t)bh * N + qi] : 0.f;
-        }
-#pragma unroll
-        for (int m = 0; m < 4; ++m) dof[m] = PolBF16<64>::neg(dof[m]);
-        xm = p.scale_log2;
-        nl = ok ? -p.lse[(size_t)bh * N + qi] * kLog2e : 0.f;
-        acc[0] = acc[1] = f32x16{};
-    }
-
-    __device__ static __forceinline__ void delta_fallback(float *sd, const Params &p, size_t bh, int qs, int N,
-                                                          int lane) {
-        const int row = qs + lane;
-        float acc = 0.f;
-        if (row < N) {
-            const size_t off = (bh * N + row) * D;
-            const Frag *o = reinterpret_cast<const Frag *>(static_cast<const T *>(p.o_in) + off);
-            const Frag *d = reinterpret_cast<const Frag *>(static_cast<const T *>(p.dout) + off);
-            // half_part of each half (t = 0, then t += dot8 in m order), a
-            // chunk pair at a time: this runs inside the dK/dV loop, where the
-            // accumulators leave no room for the whole row
-            float t0 = 0.f, t1 = 0.f;
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                t0 += dot8(d[2 * m], o[2 * m]);
-                t1 += dot8(d[2 * m + 1], o[2 * m + 1]);
-                __builtin_amdgcn_sched_barrier(0);
-                asm volatile("" ::: "memory");
-            }
-            acc = t0 + t1;
-        }
-        sd[lane] = acc;
-    }
-
-    template <bool CAUSAL, bool MASK, bool PRIO>
-    __device__ __forceinline__ void stage(const T *sk, const T *sv, int k0, int q0, int N, int lane, float) {
-        const int h = lane >> 5, c32 = lane & 31;
-        const int qi = q0 + c32;
-        f32x16 dinit;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) dinit[r] = Dl;
-#pragma unroll
-        for (int blk = 0; blk < 2; ++blk) {
-            const int kb0 = k0 + 32 * blk;
-            // masked stages: a block wholly past N or after every query of the
-            // wave contributes nothing
-            if (MASK && (kb0 >= N || (CAUSAL && kb0 > q0 + 31))) continue;
-            wave_priority<PRIO>(1);
-            f32x16 s = f32x16{}, dp = dinit;
-#pragma unroll
-            for (int m = 0; m < 4; ++m) s = Pol::mma(Pol::row_frag(sk, 32 * blk + c32, m, h), qf[m], s);
-#pragma unroll
-            for (int m = 0; m < 4; ++m) dp = Pol::mma(Pol::row_frag(sv, 32 * blk + c32, m, h), dof[m], dp);
-            wave_priority<PRIO>(0);
-            // key kb0 + 8(r/4) + 4h + r%4 is masked (past N, or after query
-            // qi when causal) iff 8(r/4) + r%4 >= lim
-            const int lim = (CAUSAL ? min(N, qi + 1) : N) - kb0 - 4 * h;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                float x = __builtin_fmaf(s[r], xm, nl);
-                if constexpr (MASK) x = 8 * (r >> 2) + (r & 3) >= lim ? -INFINITY : x;
-                dp[r] *= fast_exp2(x);  // -dS / scale
-            }
-            const Frag c0 = Pol::pack8(dp, 0), c1 = Pol::pack8(dp, 1);
-            wave_priority<PRIO>(1);
-#pragma unroll
-            for (int xt = 0; xt < 2; ++xt) {
-                acc[xt] = Pol::mma(Pol::chain_a(sk, 32 * xt, 32 * blk, lane), c0, acc[xt]);
-                acc[xt] = Pol::mma(Pol::chain_a(sk, 32 * xt, 32 * blk + 16, lane), c1, acc[xt]);
-            }
-            wave_priority<PRIO>(0);
-        }
-    }
-
-    __device__ __forceinline__ void store(const Params &p, int bh, int q0, int lane) const {
-        const int h = lane >> 5;
-        const int qi = q0 + (lane & 31);
-        if (qi >= p.N) return;
-        T *dQ = static_cast<T *>(p.dq) + ((size_t)bh * p.N + qi) * D;
-#pragma unroll
-        for (int xt = 0; xt < 2; ++xt) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const f32x4 v = {acc[xt][4 * i], acc[xt][4 * i + 1], acc[xt][4 * i + 2], acc[xt][4 * i + 3]};
-                store4<T>(dQ + 32 * xt + 8 * i + 4 * h, v, -p.scale);
-            }
-        }
-    }
-};
-
-// dK/dV: S = Q K^T and Delta - dP = Delta + dO (-V)^T with the stage's queries
-// on the C rows and this wave's 32 keys on the columns (the chained products
-// contract over the C rows). POW2 (the softmax scale is a power of two, e.g.
-// 1/8 at d = 64): kf holds -K scale, exact in bf16, so the score accumulators
-// start at L straight from LDS and come out as L - s scale, the exponent of P
-// times -1/log2(e). Otherwise kf holds K, the accumulators start at -L /
-// scale and come out as s - L / scale, the exponent times 1 / (scale
-// log2(e)).
-template <bool POW2>
-struct DkvTileW64 {
-    using Pol = PolW64;
-    using T = u16;
-    using Frag = bf16x8;
-    static constexpr int D = 64, ROWS = 32;
-    static constexpr int kWaves = 3;
-    static constexpr bool kPrioFused = true;
-
-    Frag kf[4], vf[4];     // [m]: d elements 16m + 8h .. +7 of key kw0 + l%32
-    f32x16 accK[2], accV[2];  // [xt]: rows d 32xt + 8i + 4h + j, column key
-    float lmul, xm;
-
-    __device__ __forceinline__ void load(const Params &p, const T *K, const T *V, int kw0, int lane) {
-        const int h = lane >> 5;
-        const int key = kw0 + (lane & 31);
-        const bool ok = key < p.N;
-        const float ks = POW2 ? -p.scale : 1.0f;
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const Frag k = ok ? *reinterpret_cast<const Frag *>(K + (size_t)key * D + 16 * m + 8 * h) : Frag{};
-            const Frag v = ok ? *reinterpret_cast<const Frag *>(V + (size_t)key * D + 16 * m + 8 * h) : Frag{};
-            kf[m] = POW2 ? PolBF16<64>::scaled(k, ks) : k;
-            vf[m] = PolBF16<64>::neg(v);
-        }
-        lmul = -1.0f / p.scale;
-        xm = POW2 ? -kLog2e : p.scale_log2;
-        accK[0] = accK[1] = accV[0] = accV[1] = f32x16{};
-    }
-
-    template <bool CAUSAL, bool MASK, bool PRIO>
-    __device__ __forceinline__ void stage(const T *sq, const T *sdo, const float *sl, const float *sd, int qs, int kw0,
-                                          int lane) {
-        const int h = lane >> 5, c32 = lane & 31;
-        const int key = kw0 + c32;
-#pragma unroll
-        for (int blk = 0; blk < 2; ++blk) {
-            // (a block of a diagonal stage whose queries all precede the wave's
-            // keys has P = 0, but skipping it makes the causal kernels spill)
-            f32x16 s, dp;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const f32x4 lv = *reinterpret_cast<const f32x4 *>(sl + 32 * blk + 8 * i + 4 * h);
-                const f32x4 dv = *reinterpret_cast<const f32x4 *>(sd + 32 * blk + 8 * i + 4 * h);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    s[4 * i + j] = POW2 ? lv[j] : lv[j] * lmul;
-                    dp[4 * i + j] = dv[j];
-                }
-            }
-            wave_priority<PRIO>(1);
-#pragma unroll
-            for (int m = 0; m < 4; ++m) s = Pol::mma(Pol::row_frag(sq, 32 * blk + c32, m, h), kf[m], s);
-#pragma unroll
-            for (int m = 0; m < 4; ++m) dp = Pol::mma(Pol::row_frag(sdo, 32 * blk + c32, m, h), vf[m], dp);
-            wave_priority<PRIO>(0);
-            // query qs + 32 blk + 8(r/4) + 4h + r%4 precedes the lane's key
-            // (causal mask) iff 8(r/4) + r%4 < thr
-            const int thr = key - qs - 32 * blk - 4 * h;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                float x = s[r] * xm;
-                if constexpr (MASK) x = 8 * (r >> 2) + (r & 3) < thr ? -INFINITY : x;
-                const float pv = fast_exp2(x);
-                s[r] = pv;
-                dp[r] *= pv;  // -dS / scale
-            }
-            const Frag p0 = Pol::pack8(s, 0), p1 = Pol::pack8(s, 1);
-            const Frag d0 = Pol::pack8(dp, 0), d1 = Pol::pack8(dp, 1);
-            wave_priority<PRIO>(1);
-#pragma unroll
-            for (int xt = 0; xt < 2; ++xt) {
-                accV[xt] = Pol::mma(Pol::chain_a(sdo, 32 * xt, 32 * blk, lane), p0, accV[xt]);
-                accK[xt] = Pol::mma(Pol::chain_a(sq, 32 * xt, 32 * blk, lane), d0, accK[xt]);
-                accV[xt] = Pol::mma(Pol::chain_a(sdo, 32 * xt, 32 * blk + 16, lane), p1, accV[xt]);
-                accK[xt] = Pol::mma(Pol::chain_a(sq, 32 * xt, 32 * blk + 16, lane), d1, accK[xt]);
-            }
-            wave_priority<PRIO>(0);
-        }
-    }
-
-    template <class U>
-    __device__ __forceinline__ void store(U *dK, U *dV, int kw0, int N, float kmul, int lane) const {
-        const int h = lane >> 5;
-        const int key = kw0 + (lane & 31);
-        if (key >= N) return;
-#pragma unroll
-        for (int xt = 0; xt < 2; ++xt) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int x = 32 * xt + 8 * i + 4 * h;
-                const f32x4 k = {accK[xt][4 * i], accK[xt][4 * i + 1], accK[xt][4 * i + 2], accK[xt][4 * i + 3]};
-                const f32x4 v = {accV[xt][4 * i], accV[xt][4 * i + 1], accV[xt][4 * i + 2], accV[xt][4 * i + 3]};
-                store4<U>(dK + (size_t)key * D + x, k, kmul);
-                store4<U>(dV + (size_t)key * D + x, v, 1.0f);
             }
         }
     }
@@ -1009,21 +748,13 @@ __global__ __launch_bounds__(256) void dkv_reduce_kernel(const float *ws, T *dk,
 
 // ----------------------------------------------------------------- launchers
 
-// The tiles of each dtype / head dim. bf16 at d = 64: the 16x16 tiles (the
-// 32x32x16 tiles measured slower, see DqTileW64).
+// The tiles of each dtype / head dim.
 using DqB64 = DqTile16<PolBF16<64>, 2>;
-template <bool POW2>
 using DkvB64 = DkvTile16<PolBF16<64>, 2>;
 using DqF32 = DqTile16<PolF32<64>, 2>;
 using DkvF32 = DkvTile16<PolF32<64>, 2>;
 using DqB128 = DqTile16<PolBF16<128>, 2>;
 using DkvB128 = DkvTile16<PolBF16<128>, 1>;
-
-// Whether the softmax scale is a power of two (then K scale is exact in bf16).
-static bool pow2_scale(float s) {
-    int e = 0;
-    return s > 0.0f && std::frexp(s, &e) == 0.5f;
-}
 
 hipError_t launch_preprocess(const Params &p, int dtype_bf16, int d, hipStream_t stream) {
     const long rows = (long)p.B * p.Hq * p.N;
@@ -1128,7 +859,7 @@ static int dkv_split_t(const Params &p) {
 
 int dkv_split(const Params &p, int dtype_bf16, int d) {
     if (dtype_bf16) {
-        if (d == 64) return dkv_split_t<DkvB64<true>>(p);
+        if (d == 64) return dkv_split_t<DkvB64>(p);
         if (d == 128) return dkv_split_t<DkvB128>(p);
     } else if (d == 64) {
         return dkv_split_t<DkvF32>(p);
@@ -1168,8 +899,7 @@ static hipError_t launch_fused_c(const Params &p, int causal, hipStream_t stream
 
 hipError_t launch_bwd_fused(const Params &p, int d, int causal, hipStream_t stream) {
     if (d == 64) {
-        return pow2_scale(p.scale) ? launch_fused_c<DqB64, DkvB64<true>>(p, causal, stream)
-                                   : launch_fused_c<DqB64, DkvB64<false>>(p, causal, stream);
+        return launch_fused_c<DqB64, DkvB64>(p, causal, stream);
     }
     if (d == 128) return launch_fused_c<DqB128, DkvB128>(p, causal, stream);
     return hipErrorInvalidValue;
@@ -1195,8 +925,7 @@ static hipError_t launch_dkv_c(Params p, int causal, hipStream_t stream) {
 
 hipError_t launch_bwd_dkv(const Params &p, int dtype_bf16, int d, int causal, hipStream_t stream) {
     if (dtype_bf16 && d == 64) {
-        return pow2_scale(p.scale) ? launch_dkv_c<DkvB64<true>>(p, causal, stream)
-                                   : launch_dkv_c<DkvB64<false>>(p, causal, stream);
+        return launch_dkv_c<DkvB64>(p, causal, stream);
     }
     if (dtype_bf16 && d == 128) return launch_dkv_c<DkvB128>(p, causal, stream);
     if (!dtype_bf16 && d == 64) return launch_dkv_c<DkvF32>(p, causal, stream);

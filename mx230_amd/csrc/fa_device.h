@@ -354,78 +354,6 @@ struct PolF32 {
     }
 };
 
-// bf16, d = 64, for the v_mfma_f32_32x32x16_bf16 tiles of the backward.
-//
-// MFMA layout: A (32 x 16): lane l holds row l%32, k-slots (h, e) = (l/32,
-// 0..7); B (16 x 32): lane l holds column l%32, k-slots (l/32, 0..7); the two
-// operands' k-slots pair up, so any assignment of a contraction index to slot
-// (h, e) used by both is the same product. C (32 x 32): lane l holds column
-// l%32 and rows 8i + 4h + j as element 4i + j (i, j = 0..3, h = l/32).
-//
-// LDS tiles (64 rows x 64 bf16) are row-major, 128 bytes per row, with the
-// 16-byte chunk c of row r stored at chunk position c ^ swz(r), swz(r) =
-// (r1 << 2) | ((r0 ^ r3) << 1) | r2. With 128 or 256 bytes of banks per cycle
-// (8 lanes of a 16-byte read, or 16 lanes of an 8-byte read, per 128 bytes)
-// both access patterns are conflict-free:
-//   * row reads (ds_read_b128): lanes l = 0..31 read chunk c of rows
-//     r0 + l: any 8 (16) aligned consecutive rows land on distinct 16-byte
-//     slots of a 128-byte (256-byte) window, as swz is a bijection of r0..r2
-//     and (r0, swz) a bijection of r0..r3;
-//   * transposing reads (ds_read_b64_tr_b16): a 16-lane group reads 4
-//     aligned consecutive rows x chunks (2n, 2n + 1), two groups the same rows x
-//     chunks (4m .. 4m + 3): bits 1-2 of swz are a bijection of r0, r1 and bit
-//     2 flips with r1, so the 16 (32) 8-byte pieces are on distinct banks.
-struct PolW64 {
-    static constexpr int D = 64;
-    using T = u16;
-    using Frag = bf16x8;
-    static constexpr int EPC = 8;
-    static constexpr int ROWS = 64;
-
-    __device__ static __forceinline__ int swz(int r) {
-        return (((r >> 1) & 1) << 2) | (((r ^ (r >> 3)) & 1) << 1) | ((r >> 2) & 1);
-    }
-    __device__ static __forceinline__ int chunk_off(int row, int chunk) {
-        return row * (D * 2) + ((chunk ^ swz(row)) << 4);
-    }
-    __device__ static __forceinline__ void chunk_at(int P, int &row, int &chunk) {
-        row = P >> 3;
-        chunk = (P & 7) ^ swz(row);
-    }
-    __device__ static __forceinline__ f32x16 mma(Frag a, Frag b, f32x16 c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-    }
-    // 16 bytes (k-slots of lane group h of MFMA m: elements 16m + 8h .. +7)
-    // of LDS row n
-    __device__ static __forceinline__ Frag row_frag(const T *tile, int n, int m, int h) {
-        return *reinterpret_cast<const Frag *>(reinterpret_cast<const char *>(tile) + chunk_off(n, 2 * m + h));
-    }
-    // The operand Other[y][k] = tile[rows(k)][y0 + y] of a chained MFMA (y =
-    // l%32), read transposed: k-slot (h, e) <-> row r0 + 4h + e for e < 4 and
-    // r0 + 8 + 4h + (e - 4) for e >= 4 (ds_read_b64_tr_b16: lane j of a
-    // 16-lane group addresses row j/4 of 4 and columns 4(j%4)..+3 of the
-    // group's 16, and receives column j of the 4 rows).
-    __device__ static __forceinline__ Frag chain_a(const T *tile, int y0, int r0, int lane) {
-        const char *base = reinterpret_cast<const char *>(tile);
-        const int h = lane >> 5, j = lane & 15;
-        const int row = r0 + 4 * h + (j >> 2);
-        const int col = y0 + (lane & 16) + 4 * (j & 3);
-        const int off = chunk_off(row, col >> 3) + ((col & 7) << 1);
-        const int off8 = chunk_off(row + 8, col >> 3) + ((col & 7) << 1);
-        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(base + off));
-        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(base + off8));
-        return __builtin_bit_cast(Frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-    }
-    // bf16 of C elements 8c .. 8c + 7 (rows 16c + 8(e/4) + 4h + e%4, e =
-    // 0..7): the B operand of a chained MFMA whose k-slot (h, e) is that row
-    __device__ static __forceinline__ Frag pack8(const f32x16 &c, int half) {
-        Frag b;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) b[e] = (__bf16)c[8 * half + e];
-        return b;
-    }
-};
-
 // --------------------------------------------------------------- LDS staging
 
 // Wave-wide direct global->LDS loads (global_load_lds_dwordx4 / _dword: no

@@ -64,7 +64,7 @@ __global__ __launch_bounds__(kProbeThreads) void probe_mfma_kernel(float *sink, 
     sink[blockIdx.x * kProbeThreads + tid] = s;
 }
 
-// The same for v_mfma_f32_32x32x16_bf16 (the backward's tiles at d = 64):
+// The same for v_mfma_f32_32x32x16_bf16 (the other bf16 MFMA shape):
 // 4 independent 16-register accumulators per wave.
 constexpr int kChains32 = 4;
 __global__ __launch_bounds__(kProbeThreads) void probe_mfma32_kernel(float *sink, int iters) {

@@ -4,8 +4,8 @@ BASELINE sizes: against the CPU oracle on one head or one KV-head group, and on
 every head against the size-independent closed forms of the VJP
 (sum_j dK_j = 0, sum_j dV_j = sum over the group's query heads of sum_i dO_i).
 The long sequence (cfg3) is checked on sampled rows and keys against float64.
-Also the softmax scales the bf16 d = 64 tiles treat differently: a power of
-two other than 1/sqrt(d), and a scale that is not a power of two."""
+Also explicit softmax scales at bf16 d = 64: a power of two other than
+1/sqrt(d), and a scale that is not a power of two."""
 from __future__ import annotations
 
 import numpy as np
