@@ -52,7 +52,9 @@ typedef enum {
     MXFA_ERR_ALIGN = -5,       /* a device pointer is not 16-byte aligned */
     MXFA_ERR_LAUNCH = -6,      /* the HIP runtime rejected a launch */
     MXFA_ERR_DEVICE = -7,      /* no usable gfx950 device */
-    MXFA_ERR_WORKSPACE = -8    /* a workspace smaller than mxfa_bwd_workspace_bytes(shape) */
+    MXFA_ERR_WORKSPACE = -8,   /* a workspace smaller than mxfa_bwd_workspace_bytes(shape) */
+    MXFA_ERR_CODE_OBJECT = -9  /* the gfx950 code object is missing, malformed, for another
+                                  processor, or lacks a kernel */
 } mxfa_status;
 
 typedef enum { MXFA_F32 = 0, MXFA_BF16 = 1 } mxfa_dtype;
@@ -74,14 +76,36 @@ int mxfa_version(void);
 /* Human-readable text of a status code (static storage). */
 const char *mxfa_strerror(int status);
 
-/* Checks that `device` exists and is a gfx950 (MI355X) and makes it current.
- * Optional: the run_* entry points work on the current device without it.
- * Replaces CudaContext::new(0) + load_kernels / load_bwd
+/* The kernels are not part of libmxfa.so: they are one gfx950 code object,
+ * mxfa_gfx950.hsaco (built by hipcc beside the library), loaded per device with
+ * hipModuleLoadData and launched by name. */
+
+/* Checks that `device` exists and is a gfx950 (MI355X), makes it current and
+ * loads the code object on it (MXFA_ERR_CODE_OBJECT if that fails).
+ * Optional: the run_* entry points load it on the current device at their
+ * first launch there, and return MXFA_ERR_CODE_OBJECT if they cannot.
+ * Replaces CudaContext::new(0) + load_kernels / load_bwd, which load the PTX
+ * modules and look the kernels up by name
  * (02-flash-attention/src/main.rs:392-415, 514). */
 int mxfa_init(int device);
 
-/* Releases nothing (the library holds no resources); kept for symmetry. */
+/* Unloads the code object from every device it was loaded on (each device's
+ * work must have completed); a later launch loads it again. */
 int mxfa_shutdown(void);
+
+/* Sets the code object file later loads read (NULL: mxfa_gfx950.hsaco in the
+ * directory of libmxfa.so). Devices that already loaded one keep it until
+ * mxfa_shutdown. Returns MXFA_OK; the file is checked when loaded.
+ * Replaces the PTX paths the reference's build.rs exports to the crate
+ * (kernel-build/src/lib.rs:37-55, :89-115). */
+int mxfa_set_code_object(const char *path);
+
+/* Checks a code object file on the host, with no device access (NULL: the
+ * file later loads read): present and readable, a 64-bit little-endian ELF for
+ * EM_AMDGPU with the AMDGPU HSA OS/ABI, built for gfx950. MXFA_OK or
+ * MXFA_ERR_CODE_OBJECT. The counterpart of load_ptx's guard against an empty
+ * stub module (common/src/lib.rs:11-18). */
+int mxfa_check_code_object(const char *path);
 
 /* Validates a shape exactly as every run_* entry point does; no GPU access. */
 int mxfa_check_shape(const mxfa_shape *shape);

@@ -25,6 +25,8 @@ from dataclasses import dataclass
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmxfa.so")
+# the kernels: one gfx950 code object the library loads per device
+CODE_OBJECT_PATH = os.path.join(_HERE, "mxfa_gfx950.hsaco")
 
 MXFA_F32, MXFA_BF16 = 0, 1
 
@@ -38,11 +40,13 @@ STATUS = {
     -6: "MXFA_ERR_LAUNCH",
     -7: "MXFA_ERR_DEVICE",
     -8: "MXFA_ERR_WORKSPACE",
+    -9: "MXFA_ERR_CODE_OBJECT",
 }
 
 # Every symbol include/mxfa.h declares (the tests check the library exports them).
 EXPORTS = (
-    "mxfa_version", "mxfa_strerror", "mxfa_init", "mxfa_shutdown", "mxfa_check_shape",
+    "mxfa_version", "mxfa_strerror", "mxfa_init", "mxfa_shutdown", "mxfa_set_code_object",
+    "mxfa_check_code_object", "mxfa_check_shape",
     "mxfa_run_flash", "mxfa_run_flash_lse", "mxfa_run_preprocess", "mxfa_run_bwd_dq",
     "mxfa_run_bwd_dkv", "mxfa_run_bwd_flash", "mxfa_run_bwd_dq_delta", "mxfa_run_bwd", "mxfa_bwd_one_launch", "mxfa_bwd_workspace_bytes",
     "mxfa_run_bwd_dkv_ws", "mxfa_run_bwd_ws", "mxfa_run_bwd_naive",
@@ -100,12 +104,17 @@ def load_library(path: str | None = None):
     if not os.path.exists(p):
         raise ImportError(f"{p} is missing: build it with `make -C mx230_amd/csrc` "
                           "(or __graft_entry__.build()); there is no fallback path")
+    if path is None and not os.path.exists(CODE_OBJECT_PATH):
+        raise ImportError(f"{CODE_OBJECT_PATH} (the kernels) is missing: build it with "
+                          "`make -C mx230_amd/csrc`; there is no fallback path")
     lib = ctypes.CDLL(p)
     vp, sp, fp = ctypes.c_void_p, ctypes.POINTER(MxfaShape), ctypes.c_void_p
     lib.mxfa_version.restype = ctypes.c_int
     lib.mxfa_strerror.restype = ctypes.c_char_p
     lib.mxfa_strerror.argtypes = [ctypes.c_int]
     lib.mxfa_init.argtypes = [ctypes.c_int]
+    lib.mxfa_set_code_object.argtypes = [ctypes.c_char_p]
+    lib.mxfa_check_code_object.argtypes = [ctypes.c_char_p]
     lib.mxfa_check_shape.argtypes = [sp]
     lib.mxfa_run_flash.argtypes = [sp, vp, vp, vp, vp, vp]
     lib.mxfa_run_flash_lse.argtypes = [sp, vp, vp, vp, vp, fp, vp]
@@ -578,8 +587,22 @@ def probe_hbm_gbps(mib: int = 1024, reps: int = 5, copy: bool = False) -> float:
 
 
 def init(device: int = 0):
-    """mxfa_init: checks that ``device`` is a gfx950 and makes it current."""
+    """mxfa_init: checks that ``device`` is a gfx950, makes it current and
+    loads the code object on it."""
     _check("mxfa_init", load_library().mxfa_init(device))
+
+
+def check_code_object(path: str | None = None) -> int:
+    """mxfa_check_code_object: 0 if ``path`` (default: the library's code
+    object) is a gfx950 code object, else the MXFA_ERR_CODE_OBJECT status. Host
+    only, no device access."""
+    return int(load_library().mxfa_check_code_object(path.encode() if path else None))
+
+
+def set_code_object(path: str | None):
+    """mxfa_set_code_object: the code object file later loads read (None: the
+    default beside libmxfa.so)."""
+    _check("mxfa_set_code_object", load_library().mxfa_set_code_object(path.encode() if path else None))
 
 
 def fwd_flops(B, Hq, N, d, causal) -> float:

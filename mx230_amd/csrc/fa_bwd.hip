@@ -38,8 +38,7 @@ namespace mxfa {
 
 // Delta_i = sum_x dO[i][x] * O[i][x], 8 lanes per row (attention_bwd.cu:32-44).
 template <class T, int D>
-__global__ __launch_bounds__(256) void preprocess_kernel(const T *dout, const T *o, float *delta,
-                                                         long rows) {
+__device__ __forceinline__ void preprocess_body(const T *dout, const T *o, float *delta, long rows) {
     const long t = (long)blockIdx.x * 256 + threadIdx.x;
     const long row = t >> 3;
     const int part = (int)(t & 7);
@@ -94,12 +93,19 @@ __device__ __forceinline__ void stage_qdo(typename Pol::T *sq, typename Pol::T *
 }
 
 // Delta flags of the one-launch backward (see Params::epoch). Zero at load;
-// launch epochs start at 1, so no flag matches before it is published.
+// launch epochs start at 1, so no flag matches before it is published. And
+// the stages whose Delta a dK/dV work-group of the one-launch backward
+// computed itself (its wait ran out), counted since the code object was
+// loaded (read by name, see module.cpp).
+#if defined(__HIP_DEVICE_COMPILE__)
 __device__ uint32_t g_delta_flags[kFlagSlots * kMaxFlagBlocks];
+extern "C" __device__ unsigned long long mxfa_delta_fallbacks;
+__device__ unsigned long long mxfa_delta_fallbacks;
+#else
+extern __device__ uint32_t g_delta_flags[kFlagSlots * kMaxFlagBlocks];
+extern "C" __device__ unsigned long long mxfa_delta_fallbacks;
+#endif
 constexpr int kFlagRows = 128;  // query rows per flag: one dQ work-group's block
-// Stages whose Delta a dK/dV work-group of the one-launch backward computed
-// itself (its wait ran out), counted since the library was loaded.
-__device__ unsigned long long g_delta_fallbacks;
 
 // ---------------------------------------------------------------- wave tiles
 //
@@ -517,9 +523,10 @@ __device__ __forceinline__ void dq_body(const Params &p, int bh, int qb, DqSmem<
     t.store(p, bh, q0, lane);
 }
 
-// Causal: query blocks from the last (the most keys) to the first.
+// The dQ pass as its own launch, grid (B Hq, query blocks). Causal: query
+// blocks from the last (the most keys) to the first.
 template <class Tile, bool CAUSAL, bool DELTA>
-__global__ __launch_bounds__(256, Tile::kWaves) void dq_kernel(Params p) {
+__device__ __forceinline__ void dq_entry(const Params &p) {
     __shared__ DqSmem<typename Tile::Pol> sm;
     const int nqb = (p.N + 4 * Tile::ROWS - 1) / (4 * Tile::ROWS);
     const int qb = CAUSAL ? (nqb - 1 - (int)blockIdx.y) : (int)blockIdx.y;
@@ -620,7 +627,7 @@ __device__ __forceinline__ void dkv_body(const Params &p, int bx, int kb, DkvSme
                     lds_dma4_uc(lds_addr(sD[bf]), p.delta + bh * N + min(qs + lane, N - 1));
                 } else {
                     DqTile::delta_fallback(sD[bf], p, bh, qs, N, lane);
-                    if (lane == 0) atomicAdd(&g_delta_fallbacks, 1ull);
+                    if (lane == 0) atomicAdd(&mxfa_delta_fallbacks, 1ull);
                 }
                 // one lane: the DMA writes each active lane's dword at base + 4 lane
                 if (ld_h < nh && lane == 0) {
@@ -688,9 +695,10 @@ __device__ __forceinline__ void dkv_body(const Params &p, int bx, int kb, DkvSme
     t.store(static_cast<T *>(p.dk) + kvoff, static_cast<T *>(p.dv) + kvoff, kw0, N, -p.scale, lane);
 }
 
-// Causal: key block 0 (the most queries) is dispatched first.
+// The dK/dV pass as its own launch, grid (B Hkv split, key blocks). Causal:
+// key block 0 (the most queries) is dispatched first.
 template <class Tile, bool CAUSAL>
-__global__ __launch_bounds__(256, Tile::kWaves) void dkv_kernel(Params p) {
+__device__ __forceinline__ void dkv_entry(const Params &p) {
     __shared__ DkvSmem<typename Tile::Pol> sm;
     dkv_body<Tile, CAUSAL>(p, blockIdx.x, blockIdx.y, sm);
 }
@@ -710,8 +718,7 @@ union FusedSmem {
 };
 
 template <class DqT, class DkvT, bool CAUSAL>
-__global__ __launch_bounds__(256, DkvT::kWaves < DqT::kWaves ? DkvT::kWaves : DqT::kWaves) void
-bwd_fused_kernel(Params p) {
+__device__ __forceinline__ void bwd_fused_entry(const Params &p) {
     static_assert(std::is_same<typename DqT::Pol, typename DkvT::Pol>::value, "one LDS layout");
     __shared__ FusedSmem<typename DqT::Pol> sm;
     const int bid = blockIdx.x;
@@ -728,8 +735,7 @@ bwd_fused_kernel(Params p) {
 // split order (so the result is deterministic), times -scale for dK. n4 =
 // float4 groups per plane; the dV planes follow the dK planes.
 template <class T>
-__global__ __launch_bounds__(256) void dkv_reduce_kernel(const float *ws, T *dk, T *dv, size_t n4, int nsplit,
-                                                         float kscale) {
+__device__ __forceinline__ void dkv_reduce_body(const float *ws, T *dk, T *dv, size_t n4, int nsplit, float kscale) {
     const f32x4 *w = reinterpret_cast<const f32x4 *>(ws);
     const size_t stride = (size_t)gridDim.x * 256;
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < 2 * n4; i += stride) {
@@ -746,7 +752,7 @@ __global__ __launch_bounds__(256) void dkv_reduce_kernel(const float *ws, T *dk,
     }
 }
 
-// ----------------------------------------------------------------- launchers
+// ------------------------------------------------------------------ kernels
 
 // The tiles of each dtype / head dim.
 using DqB64 = DqTile16<PolBF16<64>, 2>;
@@ -756,43 +762,122 @@ using DkvF32 = DkvTile16<PolF32<64>, 2>;
 using DqB128 = DqTile16<PolBF16<128>, 2>;
 using DkvB128 = DkvTile16<PolBF16<128>, 1>;
 
+// The code object's kernels (names: fa_kernels.h), one per instantiation.
+#if defined(__HIP_DEVICE_COMPILE__)
+#define MXFA_PREPROCESS(NAME, T, D)                                                                      \
+    extern "C" __global__ __launch_bounds__(256) void NAME(const T *dout, const T *o, float *delta, long rows) { \
+        preprocess_body<T, D>(dout, o, delta, rows);                                                     \
+    }
+#define MXFA_DQ(NAME, TILE, CAUSAL, DELTA)                                                               \
+    extern "C" __global__ __launch_bounds__(256, TILE::kWaves) void NAME(Params p) {                    \
+        dq_entry<TILE, CAUSAL, DELTA>(p);                                                                \
+    }
+#define MXFA_DKV(NAME, TILE, CAUSAL)                                                                     \
+    extern "C" __global__ __launch_bounds__(256, TILE::kWaves) void NAME(Params p) { dkv_entry<TILE, CAUSAL>(p); }
+#define MXFA_FUSED(NAME, DQT, DKVT, CAUSAL)                                                              \
+    extern "C" __global__ __launch_bounds__(256, DKVT::kWaves < DQT::kWaves ? DKVT::kWaves : DQT::kWaves) void \
+    NAME(Params p) {                                                                                     \
+        bwd_fused_entry<DQT, DKVT, CAUSAL>(p);                                                           \
+    }
+#define MXFA_REDUCE(NAME, T)                                                                             \
+    extern "C" __global__ __launch_bounds__(256) void NAME(const float *ws, T *dk, T *dv, size_t n4, int nsplit, \
+                                                           float kscale) {                               \
+        dkv_reduce_body<T>(ws, dk, dv, n4, nsplit, kscale);                                              \
+    }
+MXFA_PREPROCESS(mxfa_preprocess_b64, u16, 64)
+MXFA_PREPROCESS(mxfa_preprocess_b128, u16, 128)
+MXFA_PREPROCESS(mxfa_preprocess_f64, float, 64)
+MXFA_DQ(mxfa_dq_b64_c, DqB64, true, false)
+MXFA_DQ(mxfa_dq_b64_c_d, DqB64, true, true)
+MXFA_DQ(mxfa_dq_b64_n, DqB64, false, false)
+MXFA_DQ(mxfa_dq_b64_n_d, DqB64, false, true)
+MXFA_DQ(mxfa_dq_b128_c, DqB128, true, false)
+MXFA_DQ(mxfa_dq_b128_c_d, DqB128, true, true)
+MXFA_DQ(mxfa_dq_b128_n, DqB128, false, false)
+MXFA_DQ(mxfa_dq_b128_n_d, DqB128, false, true)
+MXFA_DQ(mxfa_dq_f64_c, DqF32, true, false)
+MXFA_DQ(mxfa_dq_f64_c_d, DqF32, true, true)
+MXFA_DQ(mxfa_dq_f64_n, DqF32, false, false)
+MXFA_DQ(mxfa_dq_f64_n_d, DqF32, false, true)
+MXFA_DKV(mxfa_dkv_b64_c, DkvB64, true)
+MXFA_DKV(mxfa_dkv_b64_n, DkvB64, false)
+MXFA_DKV(mxfa_dkv_b128_c, DkvB128, true)
+MXFA_DKV(mxfa_dkv_b128_n, DkvB128, false)
+MXFA_DKV(mxfa_dkv_f64_c, DkvF32, true)
+MXFA_DKV(mxfa_dkv_f64_n, DkvF32, false)
+MXFA_FUSED(mxfa_bwd_b64_c, DqB64, DkvB64, true)
+MXFA_FUSED(mxfa_bwd_b64_n, DqB64, DkvB64, false)
+MXFA_FUSED(mxfa_bwd_b128_c, DqB128, DkvB128, true)
+MXFA_FUSED(mxfa_bwd_b128_n, DqB128, DkvB128, false)
+MXFA_REDUCE(mxfa_dkv_reduce_bf16, u16)
+MXFA_REDUCE(mxfa_dkv_reduce_f32, float)
+#undef MXFA_PREPROCESS
+#undef MXFA_DQ
+#undef MXFA_DKV
+#undef MXFA_FUSED
+#undef MXFA_REDUCE
+#endif
+
+// ----------------------------------------------------------------- launchers
+
+// The kernels of each (dtype, head dim): the tiles and their code-object
+// names, [causal] and [causal][computes Delta].
+struct KernelsB64 {
+    using Dq = DqB64;
+    using Dkv = DkvB64;
+    static constexpr KernelId dq[2][2] = {{k_mxfa_dq_b64_n, k_mxfa_dq_b64_n_d}, {k_mxfa_dq_b64_c, k_mxfa_dq_b64_c_d}};
+    static constexpr KernelId dkv[2] = {k_mxfa_dkv_b64_n, k_mxfa_dkv_b64_c};
+    static constexpr KernelId fused[2] = {k_mxfa_bwd_b64_n, k_mxfa_bwd_b64_c};
+    static constexpr KernelId reduce = k_mxfa_dkv_reduce_bf16;
+};
+struct KernelsB128 {
+    using Dq = DqB128;
+    using Dkv = DkvB128;
+    static constexpr KernelId dq[2][2] = {{k_mxfa_dq_b128_n, k_mxfa_dq_b128_n_d},
+                                          {k_mxfa_dq_b128_c, k_mxfa_dq_b128_c_d}};
+    static constexpr KernelId dkv[2] = {k_mxfa_dkv_b128_n, k_mxfa_dkv_b128_c};
+    static constexpr KernelId fused[2] = {k_mxfa_bwd_b128_n, k_mxfa_bwd_b128_c};
+    static constexpr KernelId reduce = k_mxfa_dkv_reduce_bf16;
+};
+struct KernelsF64 {
+    using Dq = DqF32;
+    using Dkv = DkvF32;
+    static constexpr KernelId dq[2][2] = {{k_mxfa_dq_f64_n, k_mxfa_dq_f64_n_d}, {k_mxfa_dq_f64_c, k_mxfa_dq_f64_c_d}};
+    static constexpr KernelId dkv[2] = {k_mxfa_dkv_f64_n, k_mxfa_dkv_f64_c};
+    static constexpr KernelId reduce = k_mxfa_dkv_reduce_f32;
+};
+
 hipError_t launch_preprocess(const Params &p, int dtype_bf16, int d, hipStream_t stream) {
-    const long rows = (long)p.B * p.Hq * p.N;
+    long rows = (long)p.B * p.Hq * p.N;
     const dim3 grid((unsigned)((rows * 8 + 255) / 256));
-    if (dtype_bf16) {
-        if (d == 64) hipLaunchKernelGGL((preprocess_kernel<u16, 64>), grid, dim3(256), 0, stream,
-                                        static_cast<const u16 *>(p.dout), static_cast<const u16 *>(p.o_in), p.delta, rows);
-        else if (d == 128) hipLaunchKernelGGL((preprocess_kernel<u16, 128>), grid, dim3(256), 0, stream,
-                                              static_cast<const u16 *>(p.dout), static_cast<const u16 *>(p.o_in), p.delta, rows);
-        else return hipErrorInvalidValue;
+    KernelId id;
+    if (dtype_bf16 && d == 64) {
+        id = k_mxfa_preprocess_b64;
+    } else if (dtype_bf16 && d == 128) {
+        id = k_mxfa_preprocess_b128;
+    } else if (!dtype_bf16 && d == 64) {
+        id = k_mxfa_preprocess_f64;
     } else {
-        if (d == 64) hipLaunchKernelGGL((preprocess_kernel<float, 64>), grid, dim3(256), 0, stream,
-                                        static_cast<const float *>(p.dout), static_cast<const float *>(p.o_in), p.delta, rows);
-        else return hipErrorInvalidValue;
+        return hipErrorInvalidValue;
     }
-    return hipGetLastError();
+    const void *dout = p.dout, *o = p.o_in;
+    float *delta = p.delta;
+    void *args[] = {&dout, &o, &delta, &rows};
+    return launch_kernel(id, grid, dim3(256), args, stream);
 }
 
-template <class Tile, bool CAUSAL>
-static hipError_t launch_dq_t(const Params &p, int delta, hipStream_t stream) {
-    const dim3 grid(p.B * p.Hq, (p.N + 4 * Tile::ROWS - 1) / (4 * Tile::ROWS));
-    if (delta) {
-        hipLaunchKernelGGL((dq_kernel<Tile, CAUSAL, true>), grid, dim3(256), 0, stream, p);
-    } else {
-        hipLaunchKernelGGL((dq_kernel<Tile, CAUSAL, false>), grid, dim3(256), 0, stream, p);
-    }
-    return hipGetLastError();
-}
-
-template <class Tile>
-static hipError_t launch_dq_c(const Params &p, int causal, int delta, hipStream_t stream) {
-    return causal ? launch_dq_t<Tile, true>(p, delta, stream) : launch_dq_t<Tile, false>(p, delta, stream);
+template <class K>
+static hipError_t launch_dq_k(Params p, int causal, int delta, hipStream_t stream) {
+    constexpr int BQ = 4 * K::Dq::ROWS;
+    const dim3 grid(p.B * p.Hq, (p.N + BQ - 1) / BQ);
+    void *args[] = {&p};
+    return launch_kernel(K::dq[causal ? 1 : 0][delta ? 1 : 0], grid, dim3(256), args, stream);
 }
 
 hipError_t launch_bwd_dq(const Params &p, int dtype_bf16, int d, int causal, int delta, hipStream_t stream) {
-    if (dtype_bf16 && d == 64) return launch_dq_c<DqB64>(p, causal, delta, stream);
-    if (dtype_bf16 && d == 128) return launch_dq_c<DqB128>(p, causal, delta, stream);
-    if (!dtype_bf16 && d == 64) return launch_dq_c<DqF32>(p, causal, delta, stream);
+    if (dtype_bf16 && d == 64) return launch_dq_k<KernelsB64>(p, causal, delta, stream);
+    if (dtype_bf16 && d == 128) return launch_dq_k<KernelsB128>(p, causal, delta, stream);
+    if (!dtype_bf16 && d == 64) return launch_dq_k<KernelsF64>(p, causal, delta, stream);
     return hipErrorInvalidValue;
 }
 
@@ -810,10 +895,6 @@ void get_bwd_options(int *one_launch, int *delta_wait_us) {
     *delta_wait_us = g_delta_wait_us.load();
 }
 
-hipError_t read_delta_fallbacks(unsigned long long *count) {
-    return hipMemcpyFromSymbol(count, HIP_SYMBOL(g_delta_fallbacks), sizeof(*count), 0, hipMemcpyDeviceToHost);
-}
-
 bool bwd_fused_available(const Params &p, int dtype_bf16, int d, hipStream_t stream) {
     if (!dtype_bf16 || (d != 64 && d != 128)) return false;
     // a launch captured into a graph would replay with the epoch of its
@@ -828,13 +909,17 @@ bool bwd_fused_available(const Params &p, int dtype_bf16, int d, hipStream_t str
     return g_one_launch.load() != 0;
 }
 
-template <class T>
-static hipError_t launch_dkv_reduce(const Params &p, int d, hipStream_t stream) {
-    const size_t n4 = (size_t)p.B * p.Hkv * p.N * (d / 4);
+template <class K>
+static hipError_t launch_dkv_reduce(const Params &p, hipStream_t stream) {
+    using T = typename K::Dkv::T;
+    size_t n4 = (size_t)p.B * p.Hkv * p.N * (K::Dkv::D / 4);
     const size_t blocks = std::min<size_t>((2 * n4 + 255) / 256, 4096);
-    hipLaunchKernelGGL((dkv_reduce_kernel<T>), dim3((unsigned)blocks), dim3(256), 0, stream, p.dkv_ws,
-                       static_cast<T *>(p.dk), static_cast<T *>(p.dv), n4, p.dkv_split, -p.scale);
-    return hipGetLastError();
+    const float *ws = p.dkv_ws;
+    T *dk = static_cast<T *>(p.dk), *dv = static_cast<T *>(p.dv);
+    int nsplit = p.dkv_split;
+    float kscale = -p.scale;
+    void *args[] = {&ws, &dk, &dv, &n4, &nsplit, &kscale};
+    return launch_kernel(K::reduce, dim3((unsigned)blocks), dim3(256), args, stream);
 }
 
 // How many work-groups share the query heads of a key block's GQA group: the
@@ -867,12 +952,12 @@ int dkv_split(const Params &p, int dtype_bf16, int d) {
     return 1;
 }
 
-template <class DqT, class DkvT, bool CAUSAL>
-static hipError_t launch_fused_t(Params p, hipStream_t stream) {
-    constexpr int BKV = 4 * DkvT::ROWS;
+template <class K>
+static hipError_t launch_fused_k(Params p, int causal, hipStream_t stream) {
+    constexpr int BKV = 4 * K::Dkv::ROWS;
     // with a workspace, GQA shapes split each group's query heads as in the
     // dK/dV pass; the shares' partial sums are added by a second launch
-    p.dkv_split = p.dkv_ws != nullptr ? dkv_split_t<DkvT>(p) : 1;
+    p.dkv_split = p.dkv_ws != nullptr ? dkv_split_t<typename K::Dkv>(p) : 1;
     if (p.dkv_split == 1) p.dkv_ws = nullptr;
     const long long nfb = (p.N + kFlagRows - 1) / kFlagRows;
     const long long ndq = (long long)p.B * p.Hq * nfb;
@@ -886,49 +971,37 @@ static hipError_t launch_fused_t(Params p, hipStream_t stream) {
     const int wait_us = g_delta_wait_us.load();
     p.delta_wait = wait_us < 0 ? -1 : (int)std::min(100LL * wait_us, 0x7fffffffLL);
     p.fused_ndq = (int)ndq;
-    hipLaunchKernelGGL((bwd_fused_kernel<DqT, DkvT, CAUSAL>), dim3((unsigned)(ndq + ndkv)), dim3(256), 0, stream, p);
-    const hipError_t err = hipGetLastError();
+    void *args[] = {&p};
+    const hipError_t err = launch_kernel(K::fused[causal ? 1 : 0], dim3((unsigned)(ndq + ndkv)), dim3(256), args,
+                                         stream);
     if (err != hipSuccess || p.dkv_split == 1) return err;
-    return launch_dkv_reduce<u16>(p, DkvT::D, stream);
-}
-
-template <class DqT, class DkvT>
-static hipError_t launch_fused_c(const Params &p, int causal, hipStream_t stream) {
-    return causal ? launch_fused_t<DqT, DkvT, true>(p, stream) : launch_fused_t<DqT, DkvT, false>(p, stream);
+    return launch_dkv_reduce<K>(p, stream);
 }
 
 hipError_t launch_bwd_fused(const Params &p, int d, int causal, hipStream_t stream) {
-    if (d == 64) {
-        return launch_fused_c<DqB64, DkvB64>(p, causal, stream);
-    }
-    if (d == 128) return launch_fused_c<DqB128, DkvB128>(p, causal, stream);
+    if (d == 64) return launch_fused_k<KernelsB64>(p, causal, stream);
+    if (d == 128) return launch_fused_k<KernelsB128>(p, causal, stream);
     return hipErrorInvalidValue;
 }
 
-template <class Tile, bool CAUSAL>
-static hipError_t launch_dkv_t(const Params &p, hipStream_t stream) {
-    const dim3 grid(p.B * p.Hkv * p.dkv_split, (p.N + 4 * Tile::ROWS - 1) / (4 * Tile::ROWS));
-    hipLaunchKernelGGL((dkv_kernel<Tile, CAUSAL>), grid, dim3(256), 0, stream, p);
-    return hipGetLastError();
-}
-
-template <class Tile>
-static hipError_t launch_dkv_c(Params p, int causal, hipStream_t stream) {
+template <class K>
+static hipError_t launch_dkv_k(Params p, int causal, hipStream_t stream) {
+    using Tile = typename K::Dkv;
     // with a workspace, GQA shapes whose key blocks alone underfill the GPU
     // split each group's query heads over several work-groups
     p.dkv_split = p.dkv_ws != nullptr ? dkv_split_t<Tile>(p) : 1;
     if (p.dkv_split == 1) p.dkv_ws = nullptr;
-    const hipError_t e = causal ? launch_dkv_t<Tile, true>(p, stream) : launch_dkv_t<Tile, false>(p, stream);
+    const dim3 grid(p.B * p.Hkv * p.dkv_split, (p.N + 4 * Tile::ROWS - 1) / (4 * Tile::ROWS));
+    void *args[] = {&p};
+    const hipError_t e = launch_kernel(K::dkv[causal ? 1 : 0], grid, dim3(256), args, stream);
     if (e != hipSuccess || p.dkv_split == 1) return e;
-    return launch_dkv_reduce<typename Tile::T>(p, Tile::D, stream);
+    return launch_dkv_reduce<K>(p, stream);
 }
 
 hipError_t launch_bwd_dkv(const Params &p, int dtype_bf16, int d, int causal, hipStream_t stream) {
-    if (dtype_bf16 && d == 64) {
-        return launch_dkv_c<DkvB64>(p, causal, stream);
-    }
-    if (dtype_bf16 && d == 128) return launch_dkv_c<DkvB128>(p, causal, stream);
-    if (!dtype_bf16 && d == 64) return launch_dkv_c<DkvF32>(p, causal, stream);
+    if (dtype_bf16 && d == 64) return launch_dkv_k<KernelsB64>(p, causal, stream);
+    if (dtype_bf16 && d == 128) return launch_dkv_k<KernelsB128>(p, causal, stream);
+    if (!dtype_bf16 && d == 64) return launch_dkv_k<KernelsF64>(p, causal, stream);
     return hipErrorInvalidValue;
 }
 

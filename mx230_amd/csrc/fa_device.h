@@ -529,8 +529,14 @@ __device__ __forceinline__ void stage_kv(typename Pol::T *sk, typename Pol::T *s
     stage_rows<Pol, NT>(sv, V + (size_t)k0 * row_stride, N - k0, pl, wave, row_stride);
 }
 
-// Read by lanes past the end of a staged vector (see stage_vec64).
+// Read by lanes past the end of a staged vector (see stage_vec64). Device
+// variables and kernels are defined in the code object only (the device
+// pass); the host library, compiled for the host alone, sees declarations.
+#if defined(__HIP_DEVICE_COMPILE__)
 __device__ const float kPosInf = __builtin_inff();
+#else
+extern __device__ const float kPosInf;
+#endif
 
 // 64 fp32 values src[l] (l < nvalid, else *pad) -> dst[l], by one wave.
 __device__ __forceinline__ void stage_vec64(float *dst, const float *src, int nvalid, int lane, const float *pad) {

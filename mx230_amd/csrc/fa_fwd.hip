@@ -268,10 +268,11 @@ __device__ __forceinline__ void fwd_stage_lazy(f32x4 (&acc)[Pol::D / 16][QT], fl
     wave_priority<PRIO>(0);
 }
 
-// WPS: waves per SIMD the kernel is compiled for; QT: 16-query tiles per wave
-// (the work-group takes 64 QT queries).
-template <class Pol, bool CAUSAL, int WPS, int QT>
-__global__ __launch_bounds__(256, WPS) void fwd_kernel(Params p) {
+// One work-group of the forward, grid (B Hq, query blocks). QT: 16-query
+// tiles per wave (the work-group takes 64 QT queries); the kernels are
+// compiled for a number of waves per SIMD (the names' w*).
+template <class Pol, bool CAUSAL, int QT>
+__device__ __forceinline__ void fwd_entry(const Params &p) {
     using T = typename Pol::T;
     using Frag = typename Pol::Frag;
     constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
@@ -393,19 +394,50 @@ __global__ __launch_bounds__(256, WPS) void fwd_kernel(Params p) {
     }
 }
 
+// The code object's forward kernels (fa_kernels.h): policy, causal, waves
+// per SIMD, query tiles per wave.
+#if defined(__HIP_DEVICE_COMPILE__)
+#define MXFA_FWD(NAME, POL, CAUSAL, WPS, QT)                                                            \
+    extern "C" __global__ __launch_bounds__(256, WPS) void NAME(Params p) { fwd_entry<POL, CAUSAL, QT>(p); }
+MXFA_FWD(mxfa_fwd_b64_c_w3_q2, PolBF16<64>, true, 3, 2)
+MXFA_FWD(mxfa_fwd_b64_c_w2_q2, PolBF16<64>, true, 2, 2)
+MXFA_FWD(mxfa_fwd_b64_c_w3_q1, PolBF16<64>, true, 3, 1)
+MXFA_FWD(mxfa_fwd_b64_n_w2_q2, PolBF16<64>, false, 2, 2)
+MXFA_FWD(mxfa_fwd_b64_n_w3_q1, PolBF16<64>, false, 3, 1)
+MXFA_FWD(mxfa_fwd_b128_c_w2_q2, PolBF16<128>, true, 2, 2)
+MXFA_FWD(mxfa_fwd_b128_c_w2_q1, PolBF16<128>, true, 2, 1)
+MXFA_FWD(mxfa_fwd_b128_n_w2_q2, PolBF16<128>, false, 2, 2)
+MXFA_FWD(mxfa_fwd_f64_c_w1_q2, PolF32<64>, true, 1, 2)
+MXFA_FWD(mxfa_fwd_f64_n_w1_q2, PolF32<64>, false, 1, 2)
+#undef MXFA_FWD
+#endif
+
+// The kernel of (policy, causal) compiled for `wps` waves per SIMD with `qt`
+// query tiles per wave (one of the list above).
+template <class Pol, bool CAUSAL>
+static KernelId fwd_kernel_id(int wps, int qt) {
+    if constexpr (Pol::kExactScale && Pol::D == 64) {
+        if (CAUSAL) return qt == 1 ? k_mxfa_fwd_b64_c_w3_q1 : wps == 3 ? k_mxfa_fwd_b64_c_w3_q2 : k_mxfa_fwd_b64_c_w2_q2;
+        return qt == 1 ? k_mxfa_fwd_b64_n_w3_q1 : k_mxfa_fwd_b64_n_w2_q2;
+    } else if constexpr (Pol::kExactScale) {
+        if (CAUSAL) return qt == 1 ? k_mxfa_fwd_b128_c_w2_q1 : k_mxfa_fwd_b128_c_w2_q2;
+        return k_mxfa_fwd_b128_n_w2_q2;
+    } else {
+        return CAUSAL ? k_mxfa_fwd_f64_c_w1_q2 : k_mxfa_fwd_f64_n_w1_q2;
+    }
+}
+
 template <class Pol, bool CAUSAL, int QT>
-static hipError_t launch_fwd_qt(const Params &p, hipStream_t stream) {
+static hipError_t launch_fwd_qt(Params p, hipStream_t stream) {
     const dim3 grid(p.B * p.Hq, (p.N + 64 * QT - 1) / (64 * QT));
     constexpr int kHi = Pol::kWavesFwdCausal;
+    int wps = QT == 1 ? kHi : Pol::kWaves;
     if constexpr (CAUSAL && kHi > Pol::kWaves && QT > 1) {
         // enough causal work-groups to fill kHi per CU (256 CUs)
-        if ((long long)grid.x * grid.y >= 256LL * kHi) {
-            hipLaunchKernelGGL((fwd_kernel<Pol, CAUSAL, kHi, QT>), grid, dim3(256), 0, stream, p);
-            return hipGetLastError();
-        }
+        if ((long long)grid.x * grid.y >= 256LL * kHi) wps = kHi;
     }
-    hipLaunchKernelGGL((fwd_kernel<Pol, CAUSAL, QT == 1 ? kHi : Pol::kWaves, QT>), grid, dim3(256), 0, stream, p);
-    return hipGetLastError();
+    void *args[] = {&p};
+    return launch_kernel(fwd_kernel_id<Pol, CAUSAL>(wps, QT), grid, dim3(256), args, stream);
 }
 
 // bf16 launches whose 128-query work-groups would not fill every resident

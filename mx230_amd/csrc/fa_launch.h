@@ -6,8 +6,26 @@
 #include <hip/hip_runtime.h>
 
 #include "fa_device.h"
+#include "fa_kernels.h"
 
 namespace mxfa {
+
+// ---- the code object (module.cpp)
+enum class CodeObjectStatus { kOk, kMissing, kInvalid, kWrongArch };
+// Host-side check of a code object file (the current path when NULL): no
+// device access.
+CodeObjectStatus check_code_object(const char *path);
+// The code object later loads read (NULL: mxfa_gfx950.hsaco beside libmxfa.so).
+void set_code_object_path(const char *path);
+// Loads the code object on `device` (current on the calling thread) if it is
+// not loaded yet; hipErrorInvalidImage if it is missing, malformed or lacks
+// a kernel.
+hipError_t load_code_object(int device);
+// Unloads every device's code object (the next launch loads it again).
+void unload_code_objects();
+// Launches kernel `id` of the current device's code object (loading it on
+// first use). args: pointers to the kernel's arguments, in order.
+hipError_t launch_kernel(KernelId id, dim3 grid, dim3 block, void **args, hipStream_t stream);
 
 hipError_t launch_fwd(const Params &p, int dtype_bf16, int d, int causal, hipStream_t stream);
 hipError_t launch_preprocess(const Params &p, int dtype_bf16, int d, hipStream_t stream);

@@ -12,7 +12,7 @@ namespace mxfa {
 
 // S[bh][i][j] = scale * q_i . k_j, -inf above the diagonal when causal.
 template <int D>
-__global__ void naive_scores_kernel(Params p, float *S, int causal) {
+__device__ __forceinline__ void naive_scores_body(const Params &p, float *S, int causal) {
     const int j = blockIdx.x * 16 + threadIdx.x;
     const int i = blockIdx.y * 16 + threadIdx.y;
     const int bh = blockIdx.z;
@@ -28,7 +28,7 @@ __global__ void naive_scores_kernel(Params p, float *S, int causal) {
 }
 
 // In-place softmax of one row per workgroup (256 threads).
-__global__ __launch_bounds__(256) void naive_softmax_kernel(float *S, int N) {
+__device__ __forceinline__ void naive_softmax_body(float *S, int N) {
     __shared__ float red[256];
     float *row = S + ((size_t)blockIdx.y * N + blockIdx.x) * N;
     const int t = threadIdx.x;
@@ -60,7 +60,7 @@ __global__ __launch_bounds__(256) void naive_softmax_kernel(float *S, int N) {
 
 // O[bh][i][x] = sum_j S[bh][i][j] V[j][x]; block (D, 4) covers 4 rows.
 template <int D>
-__global__ void naive_av_kernel(Params p, const float *S) {
+__device__ __forceinline__ void naive_av_body(const Params &p, const float *S) {
     const int x = threadIdx.x;
     const int i = blockIdx.x * 4 + threadIdx.y;
     const int bh = blockIdx.y;
@@ -75,7 +75,7 @@ __global__ void naive_av_kernel(Params p, const float *S) {
 }
 
 template <int D>
-__global__ __launch_bounds__(256) void naive_bwd_kernel(Params p, int causal) {
+__device__ __forceinline__ void naive_bwd_body(const Params &p, int causal) {
     const int i = blockIdx.x * 256 + threadIdx.x;
     const int bh = blockIdx.y;
     const int N = p.N;
@@ -118,26 +118,41 @@ __global__ __launch_bounds__(256) void naive_bwd_kernel(Params p, int causal) {
     for (int x = 0; x < D; ++x) dQ[x] = dq[x];
 }
 
-hipError_t launch_naive_fwd(const Params &p, float *S, int d, int causal, hipStream_t stream) {
+// The code object's naive kernels (fa_kernels.h), d = 64.
+#if defined(__HIP_DEVICE_COMPILE__)
+extern "C" __global__ __launch_bounds__(256) void mxfa_naive_scores(Params p, float *S, int causal) {
+    naive_scores_body<64>(p, S, causal);
+}
+extern "C" __global__ __launch_bounds__(256) void mxfa_naive_softmax(float *S, int N) { naive_softmax_body(S, N); }
+extern "C" __global__ __launch_bounds__(256) void mxfa_naive_av(Params p, const float *S) { naive_av_body<64>(p, S); }
+extern "C" __global__ __launch_bounds__(256) void mxfa_naive_bwd(Params p, int causal) {
+    naive_bwd_body<64>(p, causal);
+}
+#endif
+
+hipError_t launch_naive_fwd(const Params &pin, float *S, int d, int causal, hipStream_t stream) {
     if (d != 64) return hipErrorInvalidValue;
+    Params p = pin;
+    int N = p.N;
     const unsigned BH = (unsigned)(p.B * p.Hq);
     const unsigned t16 = (unsigned)((p.N + 15) / 16);
-    hipLaunchKernelGGL((naive_scores_kernel<64>), dim3(t16, t16, BH), dim3(16, 16), 0, stream, p, S, causal);
-    hipError_t e = hipGetLastError();
+    void *sargs[] = {&p, &S, &causal};
+    hipError_t e = launch_kernel(k_mxfa_naive_scores, dim3(t16, t16, BH), dim3(16, 16), sargs, stream);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(naive_softmax_kernel, dim3((unsigned)p.N, BH), dim3(256), 0, stream, S, p.N);
-    e = hipGetLastError();
+    void *margs[] = {&S, &N};
+    e = launch_kernel(k_mxfa_naive_softmax, dim3((unsigned)p.N, BH), dim3(256), margs, stream);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((naive_av_kernel<64>), dim3((unsigned)((p.N + 3) / 4), BH), dim3(64, 4), 0, stream, p,
-                       (const float *)S);
-    return hipGetLastError();
+    const float *Sc = S;
+    void *aargs[] = {&p, &Sc};
+    return launch_kernel(k_mxfa_naive_av, dim3((unsigned)((p.N + 3) / 4), BH), dim3(64, 4), aargs, stream);
 }
 
-hipError_t launch_bwd_naive(const Params &p, int d, int causal, hipStream_t stream) {
+hipError_t launch_bwd_naive(const Params &pin, int d, int causal, hipStream_t stream) {
     if (d != 64) return hipErrorInvalidValue;
+    Params p = pin;
     const dim3 grid((unsigned)((p.N + 255) / 256), (unsigned)(p.B * p.Hq));
-    hipLaunchKernelGGL((naive_bwd_kernel<64>), grid, dim3(256), 0, stream, p, causal);
-    return hipGetLastError();
+    void *args[] = {&p, &causal};
+    return launch_kernel(k_mxfa_naive_bwd, grid, dim3(256), args, stream);
 }
 
 }  // namespace mxfa

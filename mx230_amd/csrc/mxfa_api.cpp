@@ -62,7 +62,11 @@ Params make_params(const mxfa_shape *s) {
     return p;
 }
 
-int from_hip(hipError_t e) { return e == hipSuccess ? MXFA_OK : MXFA_ERR_LAUNCH; }
+// hipErrorInvalidImage: the code object could not be loaded (module.cpp)
+int from_hip(hipError_t e) {
+    if (e == hipSuccess) return MXFA_OK;
+    return e == hipErrorInvalidImage ? MXFA_ERR_CODE_OBJECT : MXFA_ERR_LAUNCH;
+}
 
 int check_ptrs(std::initializer_list<const void *> ps) {
     for (const void *p : ps) {
@@ -128,6 +132,9 @@ const char *mxfa_strerror(int status) {
         case MXFA_ERR_LAUNCH: return "the HIP runtime rejected a kernel launch";
         case MXFA_ERR_DEVICE: return "no usable gfx950 device";
         case MXFA_ERR_WORKSPACE: return "the workspace is smaller than mxfa_bwd_workspace_bytes(shape)";
+        case MXFA_ERR_CODE_OBJECT:
+            return "the gfx950 code object (mxfa_gfx950.hsaco) is missing, malformed, for another processor or "
+                   "lacks a kernel";
         default: return "unknown status";
     }
 }
@@ -139,10 +146,22 @@ int mxfa_init(int device) {
     if (hipGetDeviceProperties(&prop, device) != hipSuccess) return MXFA_ERR_DEVICE;
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return MXFA_ERR_DEVICE;
     if (hipSetDevice(device) != hipSuccess) return MXFA_ERR_DEVICE;
+    return mxfa::load_code_object(device) == hipSuccess ? MXFA_OK : MXFA_ERR_CODE_OBJECT;
+}
+
+int mxfa_shutdown(void) {
+    mxfa::unload_code_objects();
     return MXFA_OK;
 }
 
-int mxfa_shutdown(void) { return MXFA_OK; }
+int mxfa_set_code_object(const char *path) {
+    mxfa::set_code_object_path(path);
+    return MXFA_OK;
+}
+
+int mxfa_check_code_object(const char *path) {
+    return mxfa::check_code_object(path) == mxfa::CodeObjectStatus::kOk ? MXFA_OK : MXFA_ERR_CODE_OBJECT;
+}
 
 int mxfa_check_shape(const mxfa_shape *shape) { return check_shape(shape); }
 
@@ -281,7 +300,9 @@ int mxfa_get_bwd_options(mxfa_bwd_options *options) {
 
 int mxfa_bwd_delta_fallbacks(unsigned long long *count) {
     if (count == nullptr) return MXFA_ERR_NULL;
-    return mxfa::read_delta_fallbacks(count) == hipSuccess ? MXFA_OK : MXFA_ERR_DEVICE;
+    const hipError_t e = mxfa::read_delta_fallbacks(count);
+    if (e == hipSuccess) return MXFA_OK;
+    return e == hipErrorInvalidImage ? MXFA_ERR_CODE_OBJECT : MXFA_ERR_DEVICE;
 }
 
 size_t mxfa_bwd_workspace_bytes(const mxfa_shape *shape) {

@@ -20,7 +20,7 @@ constexpr int kChains = 8;          // independent accumulators per wave
 // Each wave issues iters x kChains MFMAs whose accumulators do not depend on
 // each other, so the matrix pipe, not the dependent-issue latency, is the limit.
 template <bool BF16>
-__global__ __launch_bounds__(kProbeThreads) void probe_mfma_kernel(float *sink, int iters) {
+__device__ __forceinline__ void probe_mfma_body(float *sink, int iters) {
     const int tid = threadIdx.x;
     f32x4 acc[kChains];
 #pragma unroll
@@ -67,7 +67,7 @@ __global__ __launch_bounds__(kProbeThreads) void probe_mfma_kernel(float *sink, 
 // The same for v_mfma_f32_32x32x16_bf16 (the other bf16 MFMA shape):
 // 4 independent 16-register accumulators per wave.
 constexpr int kChains32 = 4;
-__global__ __launch_bounds__(kProbeThreads) void probe_mfma32_kernel(float *sink, int iters) {
+__device__ __forceinline__ void probe_mfma32_body(float *sink, int iters) {
     const int tid = threadIdx.x;
     f32x16 acc[kChains32];
 #pragma unroll
@@ -99,7 +99,7 @@ __global__ __launch_bounds__(kProbeThreads) void probe_mfma32_kernel(float *sink
 }
 
 // Streaming read of n16 16-byte vectors, grid-stride (the stream_f4 shape).
-__global__ __launch_bounds__(kProbeThreads) void probe_read_kernel(const float4 *x, size_t n16, float *sink) {
+__device__ __forceinline__ void probe_read_body(const float4 *x, size_t n16, float *sink) {
     float s = 0.f;
     for (size_t i = (size_t)blockIdx.x * kProbeThreads + threadIdx.x; i < n16; i += (size_t)gridDim.x * kProbeThreads) {
         const float4 v = x[i];
@@ -109,7 +109,7 @@ __global__ __launch_bounds__(kProbeThreads) void probe_read_kernel(const float4 
 }
 
 // Streaming copy of n16 16-byte vectors, grid-stride.
-__global__ __launch_bounds__(kProbeThreads) void probe_copy_kernel(const float4 *x, float4 *y, size_t n16) {
+__device__ __forceinline__ void probe_copy_body(const float4 *x, float4 *y, size_t n16) {
     for (size_t i = (size_t)blockIdx.x * kProbeThreads + threadIdx.x; i < n16; i += (size_t)gridDim.x * kProbeThreads)
         y[i] = x[i];
 }
@@ -121,7 +121,7 @@ __global__ __launch_bounds__(kProbeThreads) void probe_copy_kernel(const float4 
 // atomic adds of 1 (no return); else plain stores of the same bytes.
 // Key block 0 (the most stages) is dispatched first, as in the dK/dV pass.
 template <bool ATOMIC>
-__global__ __launch_bounds__(kProbeThreads) void probe_dq_atomic_kernel(float *acc, int n) {
+__device__ __forceinline__ void probe_dq_atomic_body(float *acc, int n) {
     const int h = blockIdx.x, kb = blockIdx.y;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int nqs = n / 64;
@@ -141,6 +141,31 @@ __global__ __launch_bounds__(kProbeThreads) void probe_dq_atomic_kernel(float *a
 
 }  // namespace
 
+// The code object's probe kernels (fa_kernels.h).
+#if defined(__HIP_DEVICE_COMPILE__)
+extern "C" __global__ __launch_bounds__(256) void mxfa_probe_mfma_bf16(float *sink, int iters) {
+    probe_mfma_body<true>(sink, iters);
+}
+extern "C" __global__ __launch_bounds__(256) void mxfa_probe_mfma_f32(float *sink, int iters) {
+    probe_mfma_body<false>(sink, iters);
+}
+extern "C" __global__ __launch_bounds__(256) void mxfa_probe_mfma32_bf16(float *sink, int iters) {
+    probe_mfma32_body(sink, iters);
+}
+extern "C" __global__ __launch_bounds__(256) void mxfa_probe_read_f4(const float4 *x, size_t n16, float *sink) {
+    probe_read_body(x, n16, sink);
+}
+extern "C" __global__ __launch_bounds__(256) void mxfa_probe_copy_f4(const float4 *x, float4 *y, size_t n16) {
+    probe_copy_body(x, y, n16);
+}
+extern "C" __global__ __launch_bounds__(256) void mxfa_probe_dq_atomic_add(float *acc, int n) {
+    probe_dq_atomic_body<true>(acc, n);
+}
+extern "C" __global__ __launch_bounds__(256) void mxfa_probe_dq_atomic_store(float *acc, int n) {
+    probe_dq_atomic_body<false>(acc, n);
+}
+#endif
+
 int probe_sink_len() { return kProbeBlocks * kProbeThreads; }
 
 double probe_dq_atomic_bytes(int bh, int n) {
@@ -152,12 +177,9 @@ double probe_dq_atomic_bytes(int bh, int n) {
 
 hipError_t launch_probe_dq_atomic(float *acc, int bh, int n, int atomic, hipStream_t stream) {
     const dim3 grid(bh, n / 128);
-    if (atomic) {
-        hipLaunchKernelGGL((probe_dq_atomic_kernel<true>), grid, dim3(kProbeThreads), 0, stream, acc, n);
-    } else {
-        hipLaunchKernelGGL((probe_dq_atomic_kernel<false>), grid, dim3(kProbeThreads), 0, stream, acc, n);
-    }
-    return hipGetLastError();
+    void *args[] = {&acc, &n};
+    return launch_kernel(atomic ? k_mxfa_probe_dq_atomic_add : k_mxfa_probe_dq_atomic_store, grid,
+                         dim3(kProbeThreads), args, stream);
 }
 
 double probe_mfma_flops(int bf16, int iters) {
@@ -168,12 +190,9 @@ double probe_mfma_flops(int bf16, int iters) {
 }
 
 hipError_t launch_probe_mfma(int bf16, int iters, float *sink, hipStream_t stream) {
-    if (bf16) {
-        hipLaunchKernelGGL((probe_mfma_kernel<true>), dim3(kProbeBlocks), dim3(kProbeThreads), 0, stream, sink, iters);
-    } else {
-        hipLaunchKernelGGL((probe_mfma_kernel<false>), dim3(kProbeBlocks), dim3(kProbeThreads), 0, stream, sink, iters);
-    }
-    return hipGetLastError();
+    void *args[] = {&sink, &iters};
+    return launch_kernel(bf16 ? k_mxfa_probe_mfma_bf16 : k_mxfa_probe_mfma_f32, dim3(kProbeBlocks),
+                         dim3(kProbeThreads), args, stream);
 }
 
 double probe_mfma32_flops(int iters) {
@@ -183,20 +202,20 @@ double probe_mfma32_flops(int iters) {
 }
 
 hipError_t launch_probe_mfma32(int iters, float *sink, hipStream_t stream) {
-    hipLaunchKernelGGL(probe_mfma32_kernel, dim3(kProbeBlocks), dim3(kProbeThreads), 0, stream, sink, iters);
-    return hipGetLastError();
+    void *args[] = {&sink, &iters};
+    return launch_kernel(k_mxfa_probe_mfma32_bf16, dim3(kProbeBlocks), dim3(kProbeThreads), args, stream);
 }
 
 hipError_t launch_probe_read(const void *x, size_t bytes, float *sink, hipStream_t stream) {
-    hipLaunchKernelGGL(probe_read_kernel, dim3(kProbeBlocks), dim3(kProbeThreads), 0, stream,
-                       static_cast<const float4 *>(x), bytes / 16, sink);
-    return hipGetLastError();
+    size_t n16 = bytes / 16;
+    void *args[] = {&x, &n16, &sink};
+    return launch_kernel(k_mxfa_probe_read_f4, dim3(kProbeBlocks), dim3(kProbeThreads), args, stream);
 }
 
 hipError_t launch_probe_copy(const void *x, void *y, size_t bytes, hipStream_t stream) {
-    hipLaunchKernelGGL(probe_copy_kernel, dim3(kProbeBlocks), dim3(kProbeThreads), 0, stream,
-                       static_cast<const float4 *>(x), static_cast<float4 *>(y), bytes / 16);
-    return hipGetLastError();
+    size_t n16 = bytes / 16;
+    void *args[] = {&x, &y, &n16};
+    return launch_kernel(k_mxfa_probe_copy_f4, dim3(kProbeBlocks), dim3(kProbeThreads), args, stream);
 }
 
 }  // namespace mxfa

@@ -146,6 +146,13 @@ int main(void) {
     EXPECT(mxfa_probe_copy(p, mis, 32, NULL), MXFA_ERR_ALIGN);
     EXPECT(mxfa_probe_dq_atomic(fp, 1, 192, 1, &d, NULL), MXFA_ERR_SHAPE);
 
+    /* code object checks (host only) */
+    EXPECT(mxfa_check_code_object("/nonexistent/mxfa_gfx950.hsaco"), MXFA_ERR_CODE_OBJECT);
+    EXPECT(mxfa_check_code_object("/proc/self/exe"), MXFA_ERR_CODE_OBJECT);
+    EXPECT(mxfa_set_code_object("/nonexistent/mxfa_gfx950.hsaco"), MXFA_OK);
+    EXPECT(mxfa_check_code_object(NULL), MXFA_ERR_CODE_OBJECT);
+    EXPECT(mxfa_set_code_object(NULL), MXFA_OK);
+
     /* device selection: an index that no machine has */
     EXPECT(mxfa_init(-1), MXFA_ERR_DEVICE);
     EXPECT(mxfa_shutdown(), MXFA_OK);

@@ -271,3 +271,56 @@ def test_product_never_touches_the_oracle():
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(ImportError, match="no fallback"):
         mx.load_library(str(tmp_path / "libmxfa.so"))
+
+
+# ------------------------------------------------------------- code object --
+
+def _patched(tmp_path, name, offset, data):
+    b = bytearray(open(mx.CODE_OBJECT_PATH, "rb").read())
+    b[offset:offset + len(data)] = data
+    p = tmp_path / name
+    p.write_bytes(bytes(b))
+    return str(p)
+
+
+def test_code_object_host_check(lib, tmp_path):
+    """mxfa_check_code_object, the counterpart of load_ptx's empty-stub guard
+    (common/src/lib.rs:11-18): the built code object passes; a missing file,
+    an empty one, non-ELF bytes, another machine, another OS/ABI and another
+    processor are MXFA_ERR_CODE_OBJECT, all without a device."""
+    bad = mx_status("MXFA_ERR_CODE_OBJECT")
+    assert mx.check_code_object() == 0
+    assert mx.check_code_object(mx.CODE_OBJECT_PATH) == 0
+    assert mx.check_code_object(str(tmp_path / "missing.hsaco")) == bad
+    (tmp_path / "empty.hsaco").write_bytes(b"")
+    assert mx.check_code_object(str(tmp_path / "empty.hsaco")) == bad
+    assert mx.check_code_object(mx.LIB_PATH) == bad  # an x86-64 ELF
+    assert mx.check_code_object(_patched(tmp_path, "magic.hsaco", 0, b"\x7fELG")) == bad
+    assert mx.check_code_object(_patched(tmp_path, "machine.hsaco", 18, b"\x3e\x00")) == bad
+    assert mx.check_code_object(_patched(tmp_path, "osabi.hsaco", 7, b"\x00")) == bad
+    assert mx.check_code_object(_patched(tmp_path, "gfx942.hsaco", 48, b"\x4c")) == bad
+    assert mx.check_code_object(_patched(tmp_path, "same.hsaco", 48, b"\x4f")) == 0
+
+
+def test_code_object_has_every_kernel():
+    """Every kernel fa_kernels.h names is a global function of the code object,
+    and the Delta fallback counter the library reads by name is there."""
+    readelf = "/opt/rocm/llvm/bin/llvm-readelf"
+    if not os.path.exists(readelf):
+        pytest.skip("llvm-readelf is not installed")
+    text = open(os.path.join(ROOT, "mx230_amd", "csrc", "fa_kernels.h")).read()
+    names = set(re.findall(r"X\((mxfa_\w+)\)", text))
+    assert len(names) > 40
+    out = subprocess.run([readelf, "-s", "--wide", mx.CODE_OBJECT_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    funcs = set(re.findall(r"FUNC\s+GLOBAL\s+\w+\s+\d+\s+(mxfa_\w+)", out))
+    objects = set(re.findall(r"OBJECT\s+GLOBAL\s+\w+\s+\d+\s+(mxfa_\w+)", out))
+    assert names <= funcs, sorted(names - funcs)
+    assert "mxfa_delta_fallbacks" in objects
+
+
+def test_library_has_no_device_code():
+    """libmxfa.so is host code only (the kernels live in the code object)."""
+    out = subprocess.run(["nm", "-D", mx.LIB_PATH], capture_output=True, text=True, check=True).stdout
+    assert "__hipRegisterFunction" not in out and "__hipRegisterFatBinary" not in out
+    assert "hipModuleLoadData" in out

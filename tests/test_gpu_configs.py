@@ -257,3 +257,34 @@ def test_runs_on_the_callers_stream():
     ref = oracle_fwd_bwd(q, k, v, do, True)
     errs, bad = parity(gpu, ref, TOL_BF16)
     assert not bad, errs
+
+
+def test_code_object_load_errors_and_reload(tmp_path):
+    """The kernels are a code object loaded per device: with it unloaded and
+    pointed at a missing or malformed file, launches return
+    MXFA_ERR_CODE_OBJECT (and nothing runs); pointed back at the built one, the
+    next launch loads it again and computes as before."""
+    import torch
+    import mx230_amd as mx
+    q, k, v, do = make_inputs(1, 2, 1, 100, 64, bf16=True)
+    tq, tk, tv = (to_dev(x, True) for x in (q, k, v))
+    o, lse = torch.empty_like(tq), torch.empty((1, 2, 100), dtype=torch.float32, device="cuda")
+    mx.run_flash_lse(tq, tk, tv, o, lse, True)
+    torch.cuda.synchronize()
+    want = to_np(o)
+    lib = mx.load_library()
+    (tmp_path / "bad.hsaco").write_bytes(b"\x7fELF" + bytes(200))
+    try:
+        for path in (str(tmp_path / "missing.hsaco"), str(tmp_path / "bad.hsaco")):
+            assert lib.mxfa_shutdown() == 0
+            mx.set_code_object(path)
+            with pytest.raises(mx.MxfaError, match="CODE_OBJECT"):
+                mx.run_flash_lse(tq, tk, tv, o, lse, True)
+            assert lib.mxfa_init(0) == -9
+    finally:
+        mx.set_code_object(None)
+    assert lib.mxfa_init(0) == 0
+    o.zero_()
+    mx.run_flash_lse(tq, tk, tv, o, lse, True)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_np(o), want)
