@@ -53,8 +53,10 @@ typedef enum {
     MXFA_ERR_LAUNCH = -6,      /* the HIP runtime rejected a launch */
     MXFA_ERR_DEVICE = -7,      /* no usable gfx950 device */
     MXFA_ERR_WORKSPACE = -8,   /* a workspace smaller than mxfa_bwd_workspace_bytes(shape) */
-    MXFA_ERR_CODE_OBJECT = -9  /* the gfx950 code object is missing, malformed, for another
+    MXFA_ERR_CODE_OBJECT = -9, /* the gfx950 code object is missing, malformed, for another
                                   processor, or lacks a kernel */
+    MXFA_ERR_SCRATCH = -10     /* mxfa_run_bwd_noalloc: the shape needs more than
+                                  mxfa_bwd_noalloc_scratch_bytes() */
 } mxfa_status;
 
 typedef enum { MXFA_F32 = 0, MXFA_BF16 = 1 } mxfa_dtype;
@@ -235,6 +237,24 @@ int mxfa_run_bwd_dkv_ws(const mxfa_shape *shape, const void *q, const void *k, c
 int mxfa_run_bwd_ws(const mxfa_shape *shape, const void *q, const void *k, const void *v, const void *o,
                     const void *dout, const float *lse, float *delta, void *dq, void *dk, void *dv,
                     void *workspace, size_t workspace_bytes, void *stream);
+
+/* mxfa_run_bwd_ws without a workspace argument and without allocating: the
+ * split dK/dV pass keeps its fp32 partial sums in a static device array of the
+ * library, mxfa_bwd_noalloc_scratch_bytes() (64 MiB) per device, held from the
+ * library's set-up on the device (mxfa_init, else this entry point's first
+ * call there) until the process ends. Shapes whose mxfa_bwd_workspace_bytes
+ * exceed it return MXFA_ERR_SCRATCH before any device work. No hipMalloc,
+ * hipFree or other allocating call; the array needs no clearing (every call
+ * overwrites what it reads). All calls on one device share the array and
+ * keep the last call's contents, so calls that overlap on one device race
+ * (serialise them, e.g. on one stream); results equal mxfa_run_bwd_ws's.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation). */
+int mxfa_run_bwd_noalloc(const mxfa_shape *shape, const void *q, const void *k, const void *v, const void *o,
+                         const void *dout, const float *lse, float *delta, void *dq, void *dk, void *dv,
+                         void *stream);
+size_t mxfa_bwd_noalloc_scratch_bytes(void);
 
 /* Naive backward baseline: one thread per query row, dK/dV scattered with
  * atomic adds. fp32 only. dQ, dK, dV MUST be zeroed by the caller.

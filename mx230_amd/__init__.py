@@ -41,6 +41,7 @@ STATUS = {
     -7: "MXFA_ERR_DEVICE",
     -8: "MXFA_ERR_WORKSPACE",
     -9: "MXFA_ERR_CODE_OBJECT",
+    -10: "MXFA_ERR_SCRATCH",
 }
 
 # Every symbol include/mxfa.h declares (the tests check the library exports them).
@@ -52,6 +53,7 @@ EXPORTS = (
     "mxfa_run_bwd_dkv_ws", "mxfa_run_bwd_ws", "mxfa_run_bwd_naive",
     "mxfa_naive_scratch_bytes", "mxfa_run_naive_fwd", "mxfa_check_prefill", "mxfa_run_prefill",
     "mxfa_set_bwd_options", "mxfa_get_bwd_options", "mxfa_bwd_delta_fallbacks",
+    "mxfa_run_bwd_noalloc", "mxfa_bwd_noalloc_scratch_bytes",
 )
 # Every symbol include/mxfa_probes.h declares.
 PROBE_EXPORTS = (
@@ -130,6 +132,9 @@ def load_library(path: str | None = None):
     lib.mxfa_bwd_workspace_bytes.restype = ctypes.c_size_t
     lib.mxfa_run_bwd_dkv_ws.argtypes = [sp, vp, vp, vp, vp, fp, fp, vp, vp, vp, ctypes.c_size_t, vp]
     lib.mxfa_run_bwd_ws.argtypes = [sp, vp, vp, vp, vp, vp, fp, fp, vp, vp, vp, vp, ctypes.c_size_t, vp]
+    lib.mxfa_run_bwd_noalloc.argtypes = [sp, vp, vp, vp, vp, vp, fp, fp, vp, vp, vp, vp]
+    lib.mxfa_bwd_noalloc_scratch_bytes.argtypes = []
+    lib.mxfa_bwd_noalloc_scratch_bytes.restype = ctypes.c_size_t
     lib.mxfa_naive_scratch_bytes.argtypes = [sp]
     lib.mxfa_naive_scratch_bytes.restype = ctypes.c_size_t
     lib.mxfa_run_naive_fwd.argtypes = [sp, vp, vp, vp, fp, vp, vp]
@@ -149,7 +154,7 @@ def load_library(path: str | None = None):
     lib.mxfa_bwd_delta_fallbacks.argtypes = [ctypes.POINTER(ctypes.c_ulonglong)]
     for name in EXPORTS + PROBE_EXPORTS:
         if name not in ("mxfa_version", "mxfa_strerror", "mxfa_bwd_workspace_bytes",
-                        "mxfa_naive_scratch_bytes"):
+                        "mxfa_naive_scratch_bytes", "mxfa_bwd_noalloc_scratch_bytes"):
             getattr(lib, name).restype = ctypes.c_int
     if path is None:
         _lib = lib
@@ -370,6 +375,19 @@ def run_bwd_ws(q, k, v, o, do, lse, delta, dq, dk, dv, workspace, causal: bool, 
             _expect(dq, "dq", qs, dt), _expect(dk, "dk", ks, dt), _expect(dv, "dv", ks, dt)]
     args += _ws_args(workspace)
     _check("mxfa_run_bwd_ws", load_library().mxfa_run_bwd_ws(ctypes.byref(sh.c()), *args, _stream(stream)))
+
+
+def run_bwd_noalloc(q, k, v, o, do, lse, delta, dq, dk, dv, causal: bool, scale: float = 0.0, stream=None):
+    """run_bwd_ws with the library's static scratch in place of a workspace
+    (mxfa_run_bwd_noalloc): allocates nothing; calls overlapping on one device
+    race on the scratch."""
+    sh = shape_of(q, k, causal, scale)
+    dt, qs, ks = _io(sh)
+    args = [_expect(q, "q", qs, dt), _expect(k, "k", ks, dt), _expect(v, "v", ks, dt), _expect(o, "o", qs, dt),
+            _expect(do, "do", qs, dt), _vec_ptr(lse, "lse", sh), _vec_ptr(delta, "delta", sh),
+            _expect(dq, "dq", qs, dt), _expect(dk, "dk", ks, dt), _expect(dv, "dv", ks, dt)]
+    _check("mxfa_run_bwd_noalloc", load_library().mxfa_run_bwd_noalloc(ctypes.byref(sh.c()), *args,
+                                                                        _stream(stream)))
 
 
 def run_bwd_dq_delta(q, k, v, o, do, lse, delta, dq, causal: bool, scale: float = 0.0, stream=None):

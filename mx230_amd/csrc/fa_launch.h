@@ -10,6 +10,11 @@
 
 namespace mxfa {
 
+// ---- the scratch of mxfa_run_bwd_noalloc (scratch.hip): a static device array
+size_t noalloc_scratch_bytes();
+// its device address on `device` (current on the calling thread)
+hipError_t noalloc_scratch(int device, void **ptr);
+
 // ---- the code object (module.cpp)
 enum class CodeObjectStatus { kOk, kMissing, kInvalid, kWrongArch };
 // Host-side check of a code object file (the current path when NULL): no

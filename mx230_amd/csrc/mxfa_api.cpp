@@ -132,6 +132,8 @@ const char *mxfa_strerror(int status) {
         case MXFA_ERR_LAUNCH: return "the HIP runtime rejected a kernel launch";
         case MXFA_ERR_DEVICE: return "no usable gfx950 device";
         case MXFA_ERR_WORKSPACE: return "the workspace is smaller than mxfa_bwd_workspace_bytes(shape)";
+        case MXFA_ERR_SCRATCH:
+            return "the shape needs more scratch than mxfa_bwd_noalloc_scratch_bytes() (use mxfa_run_bwd_ws)";
         case MXFA_ERR_CODE_OBJECT:
             return "the gfx950 code object (mxfa_gfx950.hsaco) is missing, malformed, for another processor or "
                    "lacks a kernel";
@@ -146,7 +148,10 @@ int mxfa_init(int device) {
     if (hipGetDeviceProperties(&prop, device) != hipSuccess) return MXFA_ERR_DEVICE;
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return MXFA_ERR_DEVICE;
     if (hipSetDevice(device) != hipSuccess) return MXFA_ERR_DEVICE;
-    return mxfa::load_code_object(device) == hipSuccess ? MXFA_OK : MXFA_ERR_CODE_OBJECT;
+    if (mxfa::load_code_object(device) != hipSuccess) return MXFA_ERR_CODE_OBJECT;
+    // set-up of mxfa_run_bwd_noalloc: the scratch array's address on this device
+    void *scratch = nullptr;
+    return mxfa::noalloc_scratch(device, &scratch) == hipSuccess ? MXFA_OK : MXFA_ERR_DEVICE;
 }
 
 int mxfa_shutdown(void) {
@@ -277,6 +282,26 @@ int mxfa_run_bwd_ws(const mxfa_shape *shape, const void *q, const void *k, const
     rc = mxfa_run_bwd_dq_delta(shape, q, k, v, o, dout, lse, delta, dq, stream);
     if (rc != MXFA_OK) return rc;
     return mxfa_run_bwd_dkv_ws(shape, q, k, v, dout, lse, delta, dk, dv, workspace, workspace_bytes, stream);
+}
+
+size_t mxfa_bwd_noalloc_scratch_bytes(void) { return mxfa::noalloc_scratch_bytes(); }
+
+int mxfa_run_bwd_noalloc(const mxfa_shape *shape, const void *q, const void *k, const void *v, const void *o,
+                         const void *dout, const float *lse, float *delta, void *dq, void *dk, void *dv,
+                         void *stream) {
+    int rc = check_shape(shape);
+    if (rc != MXFA_OK) return rc;
+    rc = check_ptrs({q, k, v, o, dout, lse, delta, dq, dk, dv});
+    if (rc != MXFA_OK) return rc;
+    const size_t need = mxfa_bwd_workspace_bytes(shape);
+    if (need > mxfa::noalloc_scratch_bytes()) return MXFA_ERR_SCRATCH;
+    void *scratch = nullptr;
+    if (need > 0) {
+        int device = -1;
+        if (hipGetDevice(&device) != hipSuccess) return MXFA_ERR_DEVICE;
+        if (mxfa::noalloc_scratch(device, &scratch) != hipSuccess) return MXFA_ERR_DEVICE;
+    }
+    return mxfa_run_bwd_ws(shape, q, k, v, o, dout, lse, delta, dq, dk, dv, scratch, need, stream);
 }
 
 int mxfa_bwd_one_launch(const mxfa_shape *shape) {

@@ -67,7 +67,7 @@ __device__ __forceinline__ void probe_mfma_body(float *sink, int iters) {
 // The same for v_mfma_f32_32x32x16_bf16 (the other bf16 MFMA shape):
 // 4 independent 16-register accumulators per wave.
 constexpr int kChains32 = 4;
-__device__ __forceinline__ void probe_mfma32_body(float *sink, int iters) {
+[[maybe_unused]] __device__ __forceinline__ void probe_mfma32_body(float *sink, int iters) {
     const int tid = threadIdx.x;
     f32x16 acc[kChains32];
 #pragma unroll
@@ -99,7 +99,7 @@ __device__ __forceinline__ void probe_mfma32_body(float *sink, int iters) {
 }
 
 // Streaming read of n16 16-byte vectors, grid-stride (the stream_f4 shape).
-__device__ __forceinline__ void probe_read_body(const float4 *x, size_t n16, float *sink) {
+[[maybe_unused]] __device__ __forceinline__ void probe_read_body(const float4 *x, size_t n16, float *sink) {
     float s = 0.f;
     for (size_t i = (size_t)blockIdx.x * kProbeThreads + threadIdx.x; i < n16; i += (size_t)gridDim.x * kProbeThreads) {
         const float4 v = x[i];
@@ -109,7 +109,7 @@ __device__ __forceinline__ void probe_read_body(const float4 *x, size_t n16, flo
 }
 
 // Streaming copy of n16 16-byte vectors, grid-stride.
-__device__ __forceinline__ void probe_copy_body(const float4 *x, float4 *y, size_t n16) {
+[[maybe_unused]] __device__ __forceinline__ void probe_copy_body(const float4 *x, float4 *y, size_t n16) {
     for (size_t i = (size_t)blockIdx.x * kProbeThreads + threadIdx.x; i < n16; i += (size_t)gridDim.x * kProbeThreads)
         y[i] = x[i];
 }

@@ -319,8 +319,24 @@ def test_code_object_has_every_kernel():
     assert "mxfa_delta_fallbacks" in objects
 
 
-def test_library_has_no_device_code():
-    """libmxfa.so is host code only (the kernels live in the code object)."""
+def test_library_has_no_kernels():
+    """libmxfa.so holds no kernels (they live in the code object): its only
+    device code is the scratch array of mxfa_run_bwd_noalloc."""
     out = subprocess.run(["nm", "-D", mx.LIB_PATH], capture_output=True, text=True, check=True).stdout
-    assert "__hipRegisterFunction" not in out and "__hipRegisterFatBinary" not in out
-    assert "hipModuleLoadData" in out
+    assert "__hipRegisterFunction" not in out
+    assert "__hipRegisterVar" in out and "hipModuleLoadData" in out
+
+
+def test_noalloc_rejects_shapes_beyond_its_scratch(lib):
+    """mxfa_run_bwd_noalloc: 64 MiB of scratch per device; a shape that needs
+    more is MXFA_ERR_SCRATCH before any device work (fake pointers, no GPU)."""
+    assert lib.mxfa_bwd_noalloc_scratch_bytes() == 64 << 20
+    p = ctypes.c_void_p(4096)
+    fits = _shape(B=1, Hq=32, Hkv=4, N=2048, d=128)  # cfg5 d = 128: exactly 64 MiB
+    assert lib.mxfa_bwd_workspace_bytes(ctypes.byref(fits)) == 64 << 20
+    big = _shape(B=1, Hq=64, Hkv=4, N=8192, d=64)  # 8 shares of 256 key blocks: 128 MiB
+    assert lib.mxfa_bwd_workspace_bytes(ctypes.byref(big)) == 2 * 8 * 4 * 8192 * 64 * 4
+    assert lib.mxfa_run_bwd_noalloc(ctypes.byref(big), p, p, p, p, p, p, p, p, p, p, None) == \
+        mx_status("MXFA_ERR_SCRATCH")
+    assert lib.mxfa_run_bwd_noalloc(ctypes.byref(big), p, p, p, p, p, p, p, p, p, None, None) == \
+        mx_status("MXFA_ERR_NULL")
