@@ -120,6 +120,12 @@ int main(void) {
     EXPECT(mxfa_run_naive_fwd(&ok, p, p, p, fp, p, NULL), MXFA_ERR_UNSUPPORTED);
     EXPECT(mxfa_run_naive_fwd(&s, p, p, p, NULL, p, NULL), MXFA_ERR_NULL);
 
+    /* the no-alloc backward: over its scratch, or missing pointers */
+    EXPECT(mxfa_bwd_noalloc_scratch_bytes(), 64LL << 20);
+    s = shape(1, 64, 4, 8192, 64, 1, MXFA_BF16, 0.0f);
+    EXPECT(mxfa_run_bwd_noalloc(&s, p, p, p, p, p, fp, fp, p, p, p, NULL), MXFA_ERR_SCRATCH);
+    EXPECT(mxfa_run_bwd_noalloc(&ok, p, p, p, p, p, fp, fp, p, NULL, p, NULL), MXFA_ERR_NULL);
+
     /* prefill */
     mxfa_prefill_shape pf = {16, 12, 4, 64, 100, 12 * 64 + 2 * 4 * 64, 4 * 64, 12 * 64, MXFA_BF16, 0.0f};
     EXPECT(mxfa_check_prefill(&pf), MXFA_OK);
