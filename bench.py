@@ -55,9 +55,9 @@ def parse():
                     help="time the two-launch backward (dQ pass with Delta, then dK/dV) even where one "
                          "launch is available (set_bwd_options(one_launch=False))")
     # the MI355X raises its clocks over the first ~30 ms of sustained load and
-    # drops them again within 0.5 s idle: before the --warmup steps, steps run
-    # for at least this long (reported as clock_warmup_ms / clock_warmup_steps,
-    # apart from "warmup")
+    # drops them again within 0.5 s idle: before the --warmup steps, forward
+    # launches run for at least this long (reported as clock_warmup_ms /
+    # clock_warmup_fwd_launches, apart from "warmup")
     ap.add_argument("--clock-warmup-ms", type=float, default=150.0)
     ap.add_argument("--separate-delta", action="store_true",
                     help="run the reference-shaped sequence (preprocess launch, then the dQ pass reading Delta)")
@@ -424,11 +424,14 @@ def main():
         torch.cuda.synchronize()
         return {n: sum(evs[j].elapsed_time(evs[j + 1]) for evs in evsets) / a.steps for j, (n, _) in enumerate(seq)}
 
-    # clock warm-up (reported on its own), then the requested warm-up steps
+    # clock warm-up, reported on its own: forward launches (the producer of O
+    # and LSE) for --clock-warmup-ms, so the clocks are up when the first
+    # backward runs and every backward dispatch in the run (the W warm-up
+    # steps and the timed ones) is a warm one; then the requested warm-up steps
     cw0 = time.perf_counter()
     cw_steps = 0
     while (time.perf_counter() - cw0) * 1e3 < a.clock_warmup_ms:
-        step(launches)
+        mx.run_flash_lse(q, k, v, o, lse, causal)
         cw_steps += 1
         if cw_steps % 8 == 0:
             torch.cuda.synchronize()
@@ -456,9 +459,12 @@ def main():
     ms_mean = evs[0].elapsed_time(evs[a.steps]) / a.steps
     ms_per_step = ms_median
 
-    # second timed region of K steps with events between the launches: each
-    # launch's average duration on the same stream (the roofline's basis)
-    kern = per_launch_ms(launches)
+    # the roofline's basis: each launch's duration from HIP events on the
+    # launch stream. With one launch per step that is the timed region itself
+    # (one event between consecutive launches; each interval also holds the
+    # ~6 us dispatch gap a kernel-trace duration leaves out); otherwise a second
+    # region of K steps with events around each launch
+    kern = {launches[0][0]: ms_median} if len(launches) == 1 else per_launch_ms(launches)
     # the two passes on their own (two launches), for the breakdown
     passes = None
     if one:
@@ -503,7 +509,7 @@ def main():
         "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_per_step, 4),
         "ms_per_step_mean": round(ms_mean, 4), "ms_per_step_min_max": [round(per_step[0], 4), round(per_step[-1], 4)],
         "timing": "median of the per-step event pairs of the timed region (mean beside it)",
-        "clock_warmup_ms": round(cw_ms, 1), "clock_warmup_steps": cw_steps,
+        "clock_warmup_ms": round(cw_ms, 1), "clock_warmup_fwd_launches": cw_steps,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": a.dtype,
         "data": "synthetic (seeded N(0,1) on the GPU)",
         "config": {"workload": ("flash-attention backward, one launch (dQ with Delta + dK/dV), fwd outside timing"
