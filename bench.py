@@ -69,6 +69,9 @@ def parse():
     ap.add_argument("--atomic-probe", action="store_true",
                     help="time the writes a dQ pass fused into the dK/dV pass would make (fp32 atomics "
                          "vs plain stores) at the bench shape, next to the separate dQ pass")
+    ap.add_argument("--mix-probe", action="store_true",
+                    help="instruction-mix ceilings (mxfa_probe_mix) beside the bf16 kernels' executed MFMA rates "
+                         "at the bench shape")
     ap.add_argument("--config-table", action="store_true",
                     help="forward and backward timings at every BASELINE config (one JSON line)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -272,6 +275,74 @@ def atomic_probe(a):
                                        "separate_dq_pass_us": round(dq_ms * 1e3, 1)}}), flush=True)
 
 
+def mix_probe(a):
+    """Each bf16 kernel's executed MFMA rate at the bench shape beside the
+    ceiling of its instruction mix (mxfa_probe_mix: the same per-MFMA counts
+    of exp / mul / cvt / LDS reads, issued with no dependencies) at two and
+    three waves per SIMD. Kernel times: median of 40 per-launch event pairs
+    after >= 150 ms of warm-up launches; ceilings: mean of 10 launches after
+    >= 150 ms of warm-up."""
+    import time
+    import torch
+    import mx230_amd as mx
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    mx.init(0)
+    stream = torch.cuda.current_stream()
+
+    def warm(fn):
+        t0 = time.perf_counter()
+        n = 0
+        while time.perf_counter() - t0 < 0.15:
+            fn()
+            n += 1
+            if n % 8 == 0:
+                torch.cuda.synchronize()
+        torch.cuda.synchronize()
+
+    def median_ms(fn, reps=40):
+        warm(fn)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+        for i in range(reps):
+            ev[i].record(stream)
+            fn()
+        ev[reps].record(stream)
+        torch.cuda.synchronize()
+        return sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(reps))[reps // 2]
+
+    B, H, N, d, causal = a.B, a.H, a.N, a.d, bool(a.causal)
+    hkv = a.Hkv or a.H
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1234)
+    q, do = (torch.randn((B, H, N, d), generator=gen, device=dev).to(torch.bfloat16) for _ in range(2))
+    k, v = (torch.randn((B, hkv, N, d), generator=gen, device=dev).to(torch.bfloat16) for _ in range(2))
+    o, dq = torch.empty_like(q), torch.empty_like(q)
+    dk, dv = torch.empty_like(k), torch.empty_like(v)
+    lse = torch.empty((B, H, N), device=dev)
+    delta = torch.empty_like(lse)
+    mx.run_flash_lse(q, k, v, o, lse, causal)
+    unit = N * N * d * B * H * (0.5 if causal else 1.0)  # x k N^2 d flops per (b, h)
+    kern = {"fwd": (4, lambda: mx.run_flash_lse(q, k, v, o, lse, causal)),
+            "dq": (6, lambda: mx.run_bwd_dq_delta(q, k, v, o, do, lse, delta, dq, causal)),
+            "dkv": (8, lambda: mx.run_bwd_dkv(q, k, v, do, lse, delta, dk, dv, causal)),
+            "bwd_one_launch": (14, lambda: mx.run_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, causal))}
+    kernels = {}
+    for name, (mult, fn) in kern.items():
+        ms = median_ms(fn)
+        kernels[name] = {"us": round(ms * 1e3, 1), "executed_tflops": round(mult * unit / (ms * 1e-3) / 1e12, 1)}
+    ceilings = {}
+    for mix in mx.PROBE_MIXES:
+        for w in (2, 3):
+            warm(lambda: mx.probe_mix_tflops(mix, w, iters=256, reps=1))
+            ceilings[f"{mix}_w{w}"] = round(mx.probe_mix_tflops(mix, w, iters=256, reps=10), 1)
+    of_ceiling = {name: round(kernels[name]["executed_tflops"] / ceilings[f"{mix}_w3"], 3)
+                  for name, mix in (("fwd", "fwd"), ("dq", "dq"), ("dkv", "dkv"))}
+    print(json.dumps({"mix_probe": {"shape": {"B": B, "Hq": H, "Hkv": hkv, "N": N, "d": d, "causal": causal},
+                                    "kernels": kernels, "ceilings_tflops": ceilings,
+                                    "kernel_over_its_mix_ceiling_w3": of_ceiling,
+                                    "peak_tflops": PEAK_TFLOPS["bf16"]}}), flush=True)
+
+
 def cpu_host():
     model = "unknown"
     try:
@@ -354,6 +425,9 @@ def main():
         return
     if a.atomic_probe:
         atomic_probe(a)
+        return
+    if a.mix_probe:
+        mix_probe(a)
         return
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {a.gpus}); the path shards "

@@ -27,8 +27,36 @@ int mxfa_probe_sink_len(void);
  * float[mxfa_probe_sink_len()] (written; the values are meaningless). */
 int mxfa_probe_mfma(int dtype, int iters, float *sink, double *flops, void *stream);
 /* The same with v_mfma_f32_32x32x16_bf16 (4 independent accumulators per
- * wave, iters x 4 MFMAs per wave): the MFMA of the bf16 d = 64 backward. */
+ * wave, iters x 4 MFMAs per wave), the other bf16 MFMA shape: its rate is the
+ * 16x16x32 one's (the kernels use 16x16x32). */
 int mxfa_probe_mfma32(int iters, float *sink, double *flops, void *stream);
+
+/* Instruction-mix ceilings. Each wave runs `iters` rounds of 32
+ * v_mfma_f32_16x16x32_bf16 (8 independent accumulators) with the mix's other
+ * instructions spread evenly over them, none waiting on another: the rate at
+ * which a SIMD issues that mix, with `waves_per_simd` waves per SIMD (1-8;
+ * 256 x waves_per_simd work-groups of 4 waves). The mixes replay, per 32
+ * MFMAs, the instruction counts rocprofv3 measures for the bf16 d = 64 causal
+ * kernels (SQ_INSTS_VALU less SQ_INSTS_MFMA, SQ_INSTS_VALU_TRANS_F32,
+ * SQ_INSTS_LDS, per SQ_INSTS_MFMA), as v_exp_f32 / v_mul_f32 /
+ * v_cvt_pk_bf16_f32 / ds_read_b128 / ds_read_b64_tr_b16:
+ *   MXFA_PROBE_MIX_MFMA      the MFMAs alone
+ *   MXFA_PROBE_MIX_DKV       dK/dV pass: 16 exp, 48 mul, 16 cvt, 12 b128, 16 tr
+ *   MXFA_PROBE_MIX_DKV_VALU  its VALU part alone
+ *   MXFA_PROBE_MIX_DKV_LDS   its LDS part alone
+ *   MXFA_PROBE_MIX_DQ        dQ pass: 21 exp, 60 mul, 11 cvt, 10 b128, 11 tr
+ *   MXFA_PROBE_MIX_FWD       forward: 32 exp, 113 mul, 16 cvt, 8 b128, 16 tr
+ * Writes the launch's MFMA flops to *flops. Not the reference's: its audit
+ * (isa.cu:11-63) times one instruction kind at a time. */
+enum {
+    MXFA_PROBE_MIX_MFMA = 0,
+    MXFA_PROBE_MIX_DKV = 1,
+    MXFA_PROBE_MIX_DKV_VALU = 2,
+    MXFA_PROBE_MIX_DKV_LDS = 3,
+    MXFA_PROBE_MIX_DQ = 4,
+    MXFA_PROBE_MIX_FWD = 5
+};
+int mxfa_probe_mix(int mix, int waves_per_simd, int iters, float *sink, double *flops, void *stream);
 /* Launches a grid-stride streaming read of `bytes` (a multiple of 16) at `x`,
  * the stream_f4 shape (isa.cu:55-63). */
 int mxfa_probe_read(const void *x, size_t bytes, float *sink, void *stream);

@@ -57,8 +57,8 @@ EXPORTS = (
 )
 # Every symbol include/mxfa_probes.h declares.
 PROBE_EXPORTS = (
-    "mxfa_probe_sink_len", "mxfa_probe_mfma", "mxfa_probe_mfma32", "mxfa_probe_read", "mxfa_probe_copy",
-    "mxfa_probe_dq_atomic",
+    "mxfa_probe_sink_len", "mxfa_probe_mfma", "mxfa_probe_mfma32", "mxfa_probe_mix", "mxfa_probe_read",
+    "mxfa_probe_copy", "mxfa_probe_dq_atomic",
 )
 
 
@@ -144,6 +144,7 @@ def load_library(path: str | None = None):
     lib.mxfa_probe_sink_len.argtypes = []
     lib.mxfa_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_int, fp, ctypes.POINTER(ctypes.c_double), vp]
     lib.mxfa_probe_mfma32.argtypes = [ctypes.c_int, fp, ctypes.POINTER(ctypes.c_double), vp]
+    lib.mxfa_probe_mix.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, fp, ctypes.POINTER(ctypes.c_double), vp]
     lib.mxfa_probe_read.argtypes = [vp, ctypes.c_size_t, fp, vp]
     lib.mxfa_probe_copy.argtypes = [vp, vp, ctypes.c_size_t, vp]
     lib.mxfa_probe_dq_atomic.argtypes = [fp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
@@ -556,6 +557,28 @@ def probe_mfma_tflops(bf16: bool = True, iters: int = 256, reps: int = 5, big: b
             _check("mxfa_probe_mfma32", lib.mxfa_probe_mfma32(iters, sp, ctypes.byref(flops), stream))
         else:
             _check("mxfa_probe_mfma", lib.mxfa_probe_mfma(dt, iters, sp, ctypes.byref(flops), stream))
+    ms = _time_ms(launch, reps)
+    return flops.value / (ms * 1e-3) / 1e12
+
+
+# The instruction mixes of mxfa_probe_mix (include/mxfa_probes.h, MXFA_PROBE_MIX_*).
+PROBE_MIXES = {"mfma": 0, "dkv": 1, "dkv_valu": 2, "dkv_lds": 3, "dq": 4, "fwd": 5}
+
+
+def probe_mix_tflops(mix: str, waves_per_simd: int = 3, iters: int = 64, reps: int = 5) -> float:
+    """MFMA throughput (TFLOP/s, whole device) of one of PROBE_MIXES issued with
+    no dependencies between its instructions, at waves_per_simd waves per SIMD
+    (mxfa_probe_mix): the instruction-issue ceiling of a kernel with that mix."""
+    torch = _torch()
+    lib = load_library()
+    sink = torch.empty(lib.mxfa_probe_sink_len(), dtype=torch.float32, device="cuda")
+    flops = ctypes.c_double(0.0)
+    stream = _stream(None)
+    mid = PROBE_MIXES[mix]
+
+    def launch():
+        _check("mxfa_probe_mix", lib.mxfa_probe_mix(mid, waves_per_simd, iters, _ptr(sink, "sink", torch.float32),
+                                                    ctypes.byref(flops), stream))
     ms = _time_ms(launch, reps)
     return flops.value / (ms * 1e-3) / 1e12
 

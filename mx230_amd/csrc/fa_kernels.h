@@ -29,7 +29,8 @@
     /* probes (probe.hip) */                                                                  \
     X(mxfa_probe_mfma_bf16) X(mxfa_probe_mfma_f32) X(mxfa_probe_mfma32_bf16)                  \
     X(mxfa_probe_read_f4) X(mxfa_probe_copy_f4) X(mxfa_probe_dq_atomic_add)                   \
-    X(mxfa_probe_dq_atomic_store)
+    X(mxfa_probe_dq_atomic_store) X(mxfa_probe_mix_mfma) X(mxfa_probe_mix_dkv)                  \
+    X(mxfa_probe_mix_dkv_valu) X(mxfa_probe_mix_dkv_lds) X(mxfa_probe_mix_dq) X(mxfa_probe_mix_fwd)
 
 namespace mxfa {
 

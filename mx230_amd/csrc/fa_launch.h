@@ -66,6 +66,9 @@ double probe_mfma32_flops(int iters);
 hipError_t launch_probe_mfma32(int iters, float *sink, hipStream_t stream);
 hipError_t launch_probe_read(const void *x, size_t bytes, float *sink, hipStream_t stream);
 hipError_t launch_probe_copy(const void *x, void *y, size_t bytes, hipStream_t stream);
+int probe_mix_count();
+double probe_mix_flops(int waves_per_simd, int iters);
+hipError_t launch_probe_mix(int mix, int waves_per_simd, int iters, float *sink, hipStream_t stream);
 double probe_dq_atomic_bytes(int bh, int n);
 hipError_t launch_probe_dq_atomic(float *acc, int bh, int n, int atomic, hipStream_t stream);
 

@@ -441,6 +441,15 @@ int mxfa_probe_mfma32(int iters, float *sink, double *flops, void *stream) {
     return from_hip(mxfa::launch_probe_mfma32(iters, sink, static_cast<hipStream_t>(stream)));
 }
 
+int mxfa_probe_mix(int mix, int waves_per_simd, int iters, float *sink, double *flops, void *stream) {
+    if (mix < 0 || mix >= mxfa::probe_mix_count() || waves_per_simd < 1 || waves_per_simd > 8 || iters < 1)
+        return MXFA_ERR_SHAPE;
+    if (sink == nullptr || flops == nullptr) return MXFA_ERR_NULL;
+    if (!aligned16(sink)) return MXFA_ERR_ALIGN;
+    *flops = mxfa::probe_mix_flops(waves_per_simd, iters);
+    return from_hip(mxfa::launch_probe_mix(mix, waves_per_simd, iters, sink, static_cast<hipStream_t>(stream)));
+}
+
 int mxfa_probe_read(const void *x, size_t bytes, float *sink, void *stream) {
     int rc = check_ptrs({x, sink});
     if (rc != MXFA_OK) return rc;

@@ -139,6 +139,94 @@ __device__ __forceinline__ void probe_dq_atomic_body(float *acc, int n) {
     }
 }
 
+// Instruction-mix ceilings: how fast a SIMD issues the instruction mix of a
+// flash-attention kernel when nothing in it waits on anything else. Each
+// iteration is 32 v_mfma_f32_16x16x32_bf16 on 8 independent accumulators,
+// with E v_exp_f32, M v_mul_f32, C v_cvt_pk_bf16_f32, B ds_read_b128 and
+// R ds_read_b64_tr_b16 spread evenly over them (instruction j of a kind with
+// count K after MFMA floor(32 j / K)); every 4 MFMAs the wave waits for the
+// LDS reads issued 4 MFMAs earlier, so at most one group's reads are in
+// flight. The counts replay the per-MFMA counts rocprofv3 measures for the
+// kernels (SQ_INSTS_VALU, SQ_INSTS_VALU_TRANS_F32, SQ_INSTS_LDS,
+// SQ_INSTS_MFMA), so a kernel's MFMA rate over its mix's rate is the share
+// of its instruction-issue ceiling that it reaches. The destinations are
+// read-write operands (each its own registers, kept live across the loop), so
+// the compiler does not fold the results of one kind into shared registers.
+constexpr int kMixSlots = 32;
+
+__device__ __forceinline__ constexpr int mix_first(int count, int slot) {
+    return (slot * count + kMixSlots - 1) / kMixSlots;  // first j with 32 j / count >= slot
+}
+__device__ __forceinline__ constexpr int mix_reads(int b, int r, int s0, int s1) {
+    return mix_first(b, s1) - mix_first(b, s0) + mix_first(r, s1) - mix_first(r, s0);
+}
+
+template <int E, int M, int C, int B, int R>
+__device__ __forceinline__ void probe_mix_body(float *sink, int iters) {
+    __shared__ __attribute__((aligned(16))) float lds[4096];  // 16 KB
+    const int tid = threadIdx.x, lane = tid & 63;
+    for (int i = tid; i < 4096; i += kProbeThreads) lds[i] = 0.001f * (float)(i & 255);
+    __syncthreads();
+    f32x4 acc[8];
+    float xe[8], xm[8];
+    uint32_t u[4];
+    f32x4 rb[4];
+    double rt[4];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        acc[j] = zero4();
+        xe[j] = 0.001f * (float)(tid + j);
+        xm[j] = 1.0f + 0.001f * (float)(tid ^ j);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        u[j] = 0;
+        rb[j] = zero4();
+        rt[j] = 0.0;
+    }
+    bf16x8 a, b;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        a[e] = (__bf16)(0.001f * (float)((tid + e) & 7));
+        b[e] = (__bf16)(0.002f * (float)((tid ^ e) & 7));
+    }
+    // byte address of this lane's 16 bytes in the first 1 KB (in bounds: the
+    // largest read ends at 8 KB)
+    const uint32_t la = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float *)lds + 16u * lane;
+    for (int i = 0; i < iters; ++i) {
+#pragma unroll
+        for (int s = 0; s < kMixSlots; ++s) {
+            asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(acc[s & 7]) : "v"(a), "v"(b));
+#pragma unroll
+            for (int j = mix_first(E, s); j < mix_first(E, s + 1); ++j) asm volatile("v_exp_f32 %0, %0" : "+v"(xe[j & 7]));
+#pragma unroll
+            for (int j = mix_first(M, s); j < mix_first(M, s + 1); ++j)
+                asm volatile("v_mul_f32 %0, %0, %1" : "+v"(xm[j & 7]) : "v"(xm[(j + 4) & 7]));
+#pragma unroll
+            for (int j = mix_first(C, s); j < mix_first(C, s + 1); ++j)
+                asm volatile("v_cvt_pk_bf16_f32 %0, %1, %2" : "+v"(u[j & 3]) : "v"(xe[(j + 1) & 7]), "v"(xm[(j + 2) & 7]));
+#pragma unroll
+            for (int j = mix_first(B, s); j < mix_first(B, s + 1); ++j)
+                asm volatile("ds_read_b128 %0, %1 offset:%2" : "+v"(rb[j & 3]) : "v"(la), "i"((j & 3) * 1024));
+#pragma unroll
+            for (int j = mix_first(R, s); j < mix_first(R, s + 1); ++j)
+                asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "+v"(rt[j & 3]) : "v"(la), "i"(4096 + (j & 3) * 1024));
+            if (s % 4 == 3) {
+                // the reads of this group of 4 MFMAs may stay in flight
+                const int n = mix_reads(B, R, s - 3, s + 1);
+                asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(n < 15 ? n : 15) : "memory");
+            }
+        }
+    }
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_waitcnt lgkmcnt(0)" ::: "memory");
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sum += acc[j][0] + xe[j] + xm[j];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sum += (float)u[j] + rb[j][0] + (float)rt[j];
+    sink[blockIdx.x * kProbeThreads + tid] = sum;
+}
+
 }  // namespace
 
 // The code object's probe kernels (fa_kernels.h).
@@ -158,6 +246,19 @@ extern "C" __global__ __launch_bounds__(256) void mxfa_probe_read_f4(const float
 extern "C" __global__ __launch_bounds__(256) void mxfa_probe_copy_f4(const float4 *x, float4 *y, size_t n16) {
     probe_copy_body(x, y, n16);
 }
+// instruction mixes (counts per 32 MFMAs; the rows of MXFA_PROBE_MIX_* in
+// mxfa_probes.h)
+#define MXFA_MIX(NAME, E, M, C, B, R)                                                                       \
+    extern "C" __global__ __launch_bounds__(256) void NAME(float *sink, int iters) {                        \
+        probe_mix_body<E, M, C, B, R>(sink, iters);                                                         \
+    }
+MXFA_MIX(mxfa_probe_mix_mfma, 0, 0, 0, 0, 0)
+MXFA_MIX(mxfa_probe_mix_dkv, 16, 48, 16, 12, 16)
+MXFA_MIX(mxfa_probe_mix_dkv_valu, 16, 48, 16, 0, 0)
+MXFA_MIX(mxfa_probe_mix_dkv_lds, 0, 0, 0, 12, 16)
+MXFA_MIX(mxfa_probe_mix_dq, 21, 60, 11, 10, 11)
+MXFA_MIX(mxfa_probe_mix_fwd, 32, 113, 16, 8, 16)
+#undef MXFA_MIX
 extern "C" __global__ __launch_bounds__(256) void mxfa_probe_dq_atomic_add(float *acc, int n) {
     probe_dq_atomic_body<true>(acc, n);
 }
@@ -204,6 +305,23 @@ double probe_mfma32_flops(int iters) {
 hipError_t launch_probe_mfma32(int iters, float *sink, hipStream_t stream) {
     void *args[] = {&sink, &iters};
     return launch_kernel(k_mxfa_probe_mfma32_bf16, dim3(kProbeBlocks), dim3(kProbeThreads), args, stream);
+}
+
+static const KernelId kMixKernels[] = {k_mxfa_probe_mix_mfma,     k_mxfa_probe_mix_dkv, k_mxfa_probe_mix_dkv_valu,
+                                       k_mxfa_probe_mix_dkv_lds, k_mxfa_probe_mix_dq,  k_mxfa_probe_mix_fwd};
+
+int probe_mix_count() { return (int)(sizeof(kMixKernels) / sizeof(kMixKernels[0])); }
+
+// One work-group (4 waves, one per SIMD) per CU per wave of occupancy.
+double probe_mix_flops(int waves_per_simd, int iters) {
+    return 256.0 * waves_per_simd * 4.0 * (double)iters * kMixSlots * (2.0 * 16 * 16 * 32);
+}
+
+hipError_t launch_probe_mix(int mix, int waves_per_simd, int iters, float *sink, hipStream_t stream) {
+    if (mix < 0 || mix >= probe_mix_count() || waves_per_simd < 1 || waves_per_simd > kProbeBlocks / 256)
+        return hipErrorInvalidValue;
+    void *args[] = {&sink, &iters};
+    return launch_kernel(kMixKernels[mix], dim3(256 * waves_per_simd), dim3(kProbeThreads), args, stream);
 }
 
 hipError_t launch_probe_read(const void *x, size_t bytes, float *sink, hipStream_t stream) {

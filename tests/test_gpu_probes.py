@@ -59,3 +59,19 @@ def test_probe_dq_atomic_counts_and_rates():
     # the 830 MB payload lands on 50 MB of addresses: repeated stores to a line
     # merge in the write-back caches, so the store rate has no HBM bound
     assert 0.05 < a["tbps"] < 10.0 and st["tbps"] > 0.05
+
+
+def test_probe_mix_ceilings_order():
+    """Instruction-mix ceilings: the MFMA-only mix runs at the MFMA probe's
+    rate (the same instruction, 8 independent chains); adding a kernel's VALU
+    or LDS work can only lower it, and the full mix is no faster than either
+    part alone."""
+    import mx230_amd as mx
+    mfma = mx.probe_mfma_tflops(bf16=True)
+    got = {m: mx.probe_mix_tflops(m, waves_per_simd=3, iters=128) for m in mx.PROBE_MIXES}
+    print("\n[probe] mix ceilings (3 waves/SIMD): " + " ".join(f"{m}={t:.0f}" for m, t in got.items())
+          + f" (MFMA probe {mfma:.0f}) TFLOP/s", flush=True)
+    assert 0.85 * mfma < got["mfma"] < 1.1 * mfma
+    for m in ("dkv", "dkv_valu", "dkv_lds", "dq", "fwd"):
+        assert 0.2 * mfma < got[m] < 1.05 * got["mfma"], m
+    assert got["dkv"] < 1.05 * min(got["dkv_valu"], got["dkv_lds"])
