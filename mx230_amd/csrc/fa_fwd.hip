@@ -27,6 +27,20 @@
 
 namespace mxfa {
 
+// Masking of a stage's scores, one compare per score: key k0 + 32 blk +
+// bidx(t, g, r) is masked when it is past the lane's query position (causal)
+// or past the last key, i.e. when its offset from the lane's first key of the
+// stage, 32 blk + bidx(t, g, r) - bidx(0, g, 0) (a compile-time constant), is
+// above the lane's limit below.
+template <class Pol, bool CAUSAL>
+__device__ __forceinline__ int fwd_mask_limit(int qpos, int k0, int Nk, int g) {
+    return (CAUSAL ? min(qpos, Nk - 1) : Nk - 1) - k0 - Pol::bidx(0, g, 0);
+}
+template <class Pol>
+__device__ __forceinline__ constexpr int fwd_mask_offset(int blk, int t, int g, int r) {
+    return 32 * blk + Pol::bidx(t, g, r) - Pol::bidx(0, g, 0);
+}
+
 // One 64-key stage for one wave: scores in log2 units (x xmul when Q is kept
 // exact, else qf holds Q scale log2(e)), online-softmax update,
 // O^T += V^T P^T. PRIO: the matrix products run at raised wave priority.
@@ -58,7 +72,7 @@ __device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][QT], float (
     wave_priority<PRIO>(0);
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-        const int qpos = qpos0 + 16 * qt + l16;
+        const int lim = fwd_mask_limit<Pol, CAUSAL>(qpos0 + 16 * qt + l16, k0, Nk, g);
         float mx = -INFINITY;
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
@@ -67,10 +81,7 @@ __device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][QT], float (
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     float v = Pol::kExactScale ? s[blk][t][qt][r] * xmul : s[blk][t][qt][r];
-                    if constexpr (MASK) {
-                        const int key = k0 + 32 * blk + Pol::bidx(t, g, r);
-                        v = (key >= Nk || (CAUSAL && key > qpos)) ? -INFINITY : v;
-                    }
+                    if constexpr (MASK) v = fwd_mask_offset<Pol>(blk, t, g, r) > lim ? -INFINITY : v;
                     s[blk][t][qt][r] = v;
                     mx = fmaxf(mx, v);
                 }
@@ -166,15 +177,14 @@ __device__ __forceinline__ void fwd_scores(f32x4 (&s)[2][2][QT], const float (&m
     if constexpr (MASK) {
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
-            const int qpos = qpos0 + 16 * qt + l16;
+            const int lim = fwd_mask_limit<Pol, CAUSAL>(qpos0 + 16 * qt + l16, k0, Nk, g);
 #pragma unroll
             for (int blk = 0; blk < 2; ++blk) {
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const int key = k0 + 32 * blk + Pol::bidx(t, g, r);
-                        if (key >= Nk || (CAUSAL && key > qpos)) s[blk][t][qt][r] = -INFINITY;
+                        if (fwd_mask_offset<Pol>(blk, t, g, r) > lim) s[blk][t][qt][r] = -INFINITY;
                     }
                 }
             }
