@@ -51,7 +51,7 @@ struct Params {
     // reduce launch adds them in split order.
     float *dkv_ws;
     int dkv_split;
-    // One-launch backward (bwd_fused_kernel): work-groups [0, fused_ndq) run
+    // One-launch backward (bwd_fused_entry, kernels mxfa_bwd_*): work-groups [0, fused_ndq) run
     // the dQ pass and publish Delta per 128-row query block with flag value
     // epoch in slot flag_slot of g_delta_flags; the rest run the dK/dV pass
     // and wait for those flags, at most delta_wait ticks of the 100 MHz

@@ -1,4 +1,4 @@
-"""The one-launch backward (bwd_fused_kernel, the default of mxfa_run_bwd for
+"""The one-launch backward (bwd_fused_entry, kernels mxfa_bwd_*: the default of mxfa_run_bwd for
 bf16): dQ work-groups publish Delta per 128-row block behind a flag, and the
 dK/dV work-groups of the same launch wait for it, or compute the rows
 themselves after a wait bounded in time.
