@@ -45,7 +45,7 @@ int mxfa_probe_mfma32(int iters, float *sink, double *flops, void *stream);
  *   MXFA_PROBE_MIX_DKV_VALU  its VALU part alone
  *   MXFA_PROBE_MIX_DKV_LDS   its LDS part alone
  *   MXFA_PROBE_MIX_DQ        dQ pass: 21 exp, 60 mul, 11 cvt, 10 b128, 11 tr
- *   MXFA_PROBE_MIX_FWD       forward: 32 exp, 113 mul, 16 cvt, 8 b128, 16 tr
+ *   MXFA_PROBE_MIX_FWD       forward: 32 exp, 106 mul, 16 cvt, 8 b128, 16 tr
  * Writes the launch's MFMA flops to *flops. Not the reference's: its audit
  * (isa.cu:11-63) times one instruction kind at a time. */
 enum {

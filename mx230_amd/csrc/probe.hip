@@ -257,7 +257,7 @@ MXFA_MIX(mxfa_probe_mix_dkv, 16, 48, 16, 12, 16)
 MXFA_MIX(mxfa_probe_mix_dkv_valu, 16, 48, 16, 0, 0)
 MXFA_MIX(mxfa_probe_mix_dkv_lds, 0, 0, 0, 12, 16)
 MXFA_MIX(mxfa_probe_mix_dq, 21, 60, 11, 10, 11)
-MXFA_MIX(mxfa_probe_mix_fwd, 32, 113, 16, 8, 16)
+MXFA_MIX(mxfa_probe_mix_fwd, 32, 106, 16, 8, 16)
 #undef MXFA_MIX
 extern "C" __global__ __launch_bounds__(256) void mxfa_probe_dq_atomic_add(float *acc, int n) {
     probe_dq_atomic_body<true>(acc, n);
