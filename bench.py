@@ -72,6 +72,9 @@ def parse():
     ap.add_argument("--mix-probe", action="store_true",
                     help="instruction-mix ceilings (mxfa_probe_mix) beside the bf16 kernels' executed MFMA rates "
                          "at the bench shape")
+    ap.add_argument("--timeline", action="store_true",
+                    help="per-work-group timeline of one one-launch backward at the bench shape (timeline build "
+                         "of the code object, mxfa_gfx950_timeline.hsaco)")
     ap.add_argument("--config-table", action="store_true",
                     help="forward and backward timings at every BASELINE config (one JSON line)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -343,6 +346,74 @@ def mix_probe(a):
                                     "peak_tflops": PEAK_TFLOPS["bf16"]}}), flush=True)
 
 
+def timeline(a):
+    """One one-launch backward at the bench shape (bf16, causal or not, no
+    GQA split) with the timeline build of the code object: each dQ and dK/dV
+    work-group's prologue (start until its first stage is staged), loop time
+    per stage and epilogue (until its stores are acknowledged), the number of
+    work-groups resident over the launch, and the work-groups' resident time
+    summed and divided by the resident slots (256 CUs x the kernel's
+    work-groups per CU) against the launch's span. After >= 150 ms of warm-up
+    backward steps."""
+    import numpy as np
+    import torch
+    import mx230_amd as mx
+    if not os.path.exists(mx.TIMELINE_CODE_OBJECT_PATH):
+        sys.exit(f"bench.py --timeline: {mx.TIMELINE_CODE_OBJECT_PATH} is missing (make -C mx230_amd/csrc timeline)")
+    mx.set_code_object(mx.TIMELINE_CODE_OBJECT_PATH)
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    mx.init(0)
+    B, H, N, d, causal = a.B, a.H, a.N, a.d, bool(a.causal)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1234)
+    q, k, v, do = (torch.randn((B, H, N, d), generator=gen, device=dev).to(torch.bfloat16) for _ in range(4))
+    o, dq, dk, dv = (torch.empty_like(q) for _ in range(4))
+    lse = torch.empty((B, H, N), device=dev)
+    delta = torch.empty_like(lse)
+    mx.run_flash_lse(q, k, v, o, lse, causal)
+    assert mx.bwd_one_launch(q, k, causal), "the timeline reads the one-launch backward"
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < 0.15:
+        mx.run_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, causal)
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    mx.run_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, causal)
+    torch.cuda.synchronize()
+    nbh, nqb = B * H, (N + 127) // 128
+    ndq, nkb = nbh * nqb, (N + 127) // 128
+    nwg = ndq + nbh * nkb
+    t = mx.probe_wg_times()[:nwg].astype(np.int64)
+    t = (t - t[:, 0].min()) * 0.01  # microseconds
+    span = float(t[:, 3].max())
+    # stages of each work-group: dQ (query block qb) walks keys to its diagonal,
+    # dK/dV (key block kb) walks queries from its diagonal
+    qb = np.arange(ndq) // nbh
+    kb = np.arange(nbh * nkb) // nbh
+    stages = np.concatenate([2 * (qb + 1) if causal else np.full(ndq, N // 64),
+                             (N - 128 * kb) // 64 if causal else np.full(nbh * nkb, N // 64)])
+    out = {"shape": {"B": B, "H": H, "N": N, "d": d, "causal": causal}, "span_us": round(span, 1)}
+    slots = 256 * 3
+    for name, sl in (("dq", slice(0, ndq)), ("dkv", slice(ndq, nwg))):
+        x, st = t[sl], stages[sl]
+        pro, loop, epi = x[:, 1] - x[:, 0], x[:, 2] - x[:, 1], x[:, 3] - x[:, 2]
+        busy = x[:, 3] - x[:, 0]
+        out[name] = {"work_groups": int(len(x)), "first_start_us": round(float(x[:, 0].min()), 1),
+                     "last_start_us": round(float(x[:, 0].max()), 1), "last_end_us": round(float(x[:, 3].max()), 1),
+                     "prologue_us_mean": round(float(pro.mean()), 2),
+                     "loop_us_per_stage_mean": round(float((loop / st).mean()), 3),
+                     "epilogue_us_mean": round(float(epi.mean()), 2),
+                     "prologue_share_of_resident_time": round(float(pro.sum() / busy.sum()), 3)}
+    out["resident_time_over_slots_us"] = round(float((t[:, 3] - t[:, 0]).sum() / slots), 1)
+    grid = np.linspace(0.0, span, 21)
+    out["resident_work_groups_every_5pct_of_span"] = [int(((t[:, 0] <= g) & (t[:, 3] > g)).sum()) for g in grid]
+    out["slots"] = slots
+    print(json.dumps({"timeline": out}), flush=True)
+
+
 def cpu_host():
     model = "unknown"
     try:
@@ -428,6 +499,9 @@ def main():
         return
     if a.mix_probe:
         mix_probe(a)
+        return
+    if a.timeline:
+        timeline(a)
         return
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {a.gpus}); the path shards "

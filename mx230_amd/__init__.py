@@ -27,6 +27,9 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmxfa.so")
 # the kernels: one gfx950 code object the library loads per device
 CODE_OBJECT_PATH = os.path.join(_HERE, "mxfa_gfx950.hsaco")
+# the same kernels with per-work-group timestamps in the backward bodies
+# (make -C mx230_amd/csrc timeline; read with probe_wg_times)
+TIMELINE_CODE_OBJECT_PATH = os.path.join(_HERE, "mxfa_gfx950_timeline.hsaco")
 
 MXFA_F32, MXFA_BF16 = 0, 1
 
@@ -58,7 +61,7 @@ EXPORTS = (
 # Every symbol include/mxfa_probes.h declares.
 PROBE_EXPORTS = (
     "mxfa_probe_sink_len", "mxfa_probe_mfma", "mxfa_probe_mfma32", "mxfa_probe_mix", "mxfa_probe_read",
-    "mxfa_probe_copy", "mxfa_probe_dq_atomic",
+    "mxfa_probe_copy", "mxfa_probe_dq_atomic", "mxfa_probe_wg_times",
 )
 
 
@@ -145,6 +148,7 @@ def load_library(path: str | None = None):
     lib.mxfa_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_int, fp, ctypes.POINTER(ctypes.c_double), vp]
     lib.mxfa_probe_mfma32.argtypes = [ctypes.c_int, fp, ctypes.POINTER(ctypes.c_double), vp]
     lib.mxfa_probe_mix.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, fp, ctypes.POINTER(ctypes.c_double), vp]
+    lib.mxfa_probe_wg_times.argtypes = [vp, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
     lib.mxfa_probe_read.argtypes = [vp, ctypes.c_size_t, fp, vp]
     lib.mxfa_probe_copy.argtypes = [vp, vp, ctypes.c_size_t, vp]
     lib.mxfa_probe_dq_atomic.argtypes = [fp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
@@ -583,6 +587,22 @@ def probe_mix_tflops(mix: str, waves_per_simd: int = 3, iters: int = 64, reps: i
     return flops.value / (ms * 1e-3) / 1e12
 
 
+def probe_wg_times():
+    """The per-work-group timestamps of the last backward launch (mxfa_probe_wg_times;
+    only with TIMELINE_CODE_OBJECT_PATH loaded): a uint64 numpy array [groups, 4]
+    of 100 MHz real-time counter values (start, first stage staged, end of
+    loop, stores acknowledged) by linear work-group index; zero rows for
+    indices the launch did not have (or an earlier launch's values)."""
+    import numpy as np
+    lib = load_library()
+    avail = ctypes.c_size_t(0)
+    _check("mxfa_probe_wg_times", lib.mxfa_probe_wg_times(None, 0, ctypes.byref(avail)))
+    buf = np.zeros(avail.value // 8, dtype=np.uint64)
+    _check("mxfa_probe_wg_times", lib.mxfa_probe_wg_times(buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes,
+                                                          ctypes.byref(avail)))
+    return buf.reshape(-1, 4)
+
+
 def probe_dq_atomic(bh: int = 48, n: int = 4096, atomic: bool = True, reps: int = 5) -> dict:
     """Time of the global writes a dQ pass fused into the dK/dV pass would make
     at a causal (bh heads, N = n, d = 64) shape (mxfa_probe_dq_atomic): fp32
@@ -631,6 +651,12 @@ def init(device: int = 0):
     """mxfa_init: checks that ``device`` is a gfx950, makes it current and
     loads the code object on it."""
     _check("mxfa_init", load_library().mxfa_init(device))
+
+
+def shutdown():
+    """mxfa_shutdown: unloads the code object from every device it was loaded
+    on (their work must have completed); the next launch loads it again."""
+    _check("mxfa_shutdown", load_library().mxfa_shutdown())
 
 
 def check_code_object(path: str | None = None) -> int:

@@ -107,6 +107,32 @@ extern "C" __device__ unsigned long long mxfa_delta_fallbacks;
 #endif
 constexpr int kFlagRows = 128;  // query rows per flag: one dQ work-group's block
 
+// Timeline build (-DMXFA_WG_TIMELINE: `make timeline`, mxfa_gfx950_timeline.hsaco):
+// thread 0 of every work-group of the dQ and dK/dV bodies stamps the 100 MHz
+// real-time counter at its start (0), once its first stage is staged (1), at
+// the end of its loop (2) and once its stores are acknowledged (3), into
+// mxfa_wg_times[4 g + i] for its linear work-group index g (read by
+// mxfa_probe_wg_times). In every other build these compile to nothing.
+#if defined(__HIP_DEVICE_COMPILE__) && defined(MXFA_WG_TIMELINE)
+constexpr unsigned kTimelineGroups = 1u << 16;
+extern "C" __device__ unsigned long long mxfa_wg_times[kTimelineGroups * 4];
+__device__ unsigned long long mxfa_wg_times[kTimelineGroups * 4];
+__device__ __forceinline__ void wg_time(int i) {
+    const unsigned g = blockIdx.y * gridDim.x + blockIdx.x;
+    if (threadIdx.x == 0 && g < kTimelineGroups) {
+        *reinterpret_cast<volatile unsigned long long *>(mxfa_wg_times + 4 * (size_t)g + i) =
+            __builtin_amdgcn_s_memrealtime();
+    }
+}
+__device__ __forceinline__ void wg_time_after_stores() {
+    wait_stores();
+    wg_time(3);
+}
+#else
+__device__ __forceinline__ void wg_time(int) {}
+__device__ __forceinline__ void wg_time_after_stores() {}
+#endif
+
 // ---------------------------------------------------------------- wave tiles
 //
 // dQ tiles hold ROWS queries of one wave: Q and -dO (registers), the LSE
@@ -464,6 +490,7 @@ __device__ __forceinline__ void dq_body(const Params &p, int bh, int qb, DqSmem<
     const T *K = static_cast<const T *>(p.k) + kvoff;
     const T *V = static_cast<const T *>(p.v) + kvoff;
     const int q0 = qb * BQ + wave * Tile::ROWS;
+    wg_time(0);
 
     Tile t;
     t.template load<DELTA, PUBLISH>(p, bh, q0, lane);
@@ -486,6 +513,7 @@ __device__ __forceinline__ void dq_body(const Params &p, int bh, int qb, DqSmem<
     stage_kv<Pol, NT>(sK[0], sV[0], K, V, 0, N, plan, wave);
     wait_stage();
     __syncthreads();
+    wg_time(1);
 
     // Every stage but the last kTail is unmasked for every wave (causal: its
     // keys all precede the workgroup's first query; otherwise: only the last
@@ -520,7 +548,9 @@ __device__ __forceinline__ void dq_body(const Params &p, int bh, int qb, DqSmem<
         wait_stage();
         __syncthreads();
     }
+    wg_time(2);
     t.store(p, bh, q0, lane);
+    wg_time_after_stores();
 }
 
 // The dQ pass as its own launch, grid (B Hq, query blocks). Causal: query
@@ -578,6 +608,7 @@ __device__ __forceinline__ void dkv_body(const Params &p, int bx, int kb, DkvSme
     const int h0 = sp * p.group / nsplit, nh = (sp + 1) * p.group / nsplit - h0;
     const size_t kvoff = (size_t)bkv * N * D;
     const int kw0 = kb * BKV + wave * Tile::ROWS;  // first key of this wave
+    wg_time(0);
 
     Tile t;
     t.load(p, static_cast<const T *>(p.k) + kvoff, static_cast<const T *>(p.v) + kvoff, kw0, lane);
@@ -640,6 +671,7 @@ __device__ __forceinline__ void dkv_body(const Params &p, int bx, int kb, DkvSme
     if (nsteps > 0) issue(0);
     wait_stage();
     __syncthreads();
+    wg_time(1);
 
     // One stage: prefetch stage st + 1, compute stage st, then wait for stage
     // st + 1 and barrier. Causal: the stages that straddle the diagonal are
@@ -684,15 +716,17 @@ __device__ __forceinline__ void dkv_body(const Params &p, int bx, int kb, DkvSme
         if (i < nqs) run_fixed(Buf0{}, st++, i);
     }
 
+    wg_time(2);
     if (nsplit > 1) {
         // this share's fp32 partial sums (unscaled); dkv_reduce_kernel adds
         // the shares and applies the scale
         const size_t plane = (size_t)p.B * p.Hkv * N * D;
         float *wK = p.dkv_ws + (size_t)sp * plane + kvoff;
         t.store(wK, wK + (size_t)nsplit * plane, kw0, N, 1.0f, lane);
-        return;
+    } else {
+        t.store(static_cast<T *>(p.dk) + kvoff, static_cast<T *>(p.dv) + kvoff, kw0, N, -p.scale, lane);
     }
-    t.store(static_cast<T *>(p.dk) + kvoff, static_cast<T *>(p.dv) + kvoff, kw0, N, -p.scale, lane);
+    wg_time_after_stores();
 }
 
 // The dK/dV pass as its own launch, grid (B Hkv split, key blocks). Causal:

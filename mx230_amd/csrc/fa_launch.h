@@ -55,6 +55,10 @@ void get_bwd_options(int *one_launch, int *delta_wait_us);
 // themselves on the current device since the library was loaded (a
 // synchronous copy).
 hipError_t read_delta_fallbacks(unsigned long long *count);
+// Timeline build only: copies up to `bytes` of the per-work-group timestamps
+// to host `dst` (none when dst is NULL) and reports their size in *avail;
+// hipErrorNotFound when the loaded code object is not the timeline build.
+hipError_t read_wg_times(void *dst, size_t bytes, size_t *avail);
 hipError_t launch_bwd_naive(const Params &p, int d, int causal, hipStream_t stream);
 hipError_t launch_naive_fwd(const Params &p, float *s, int d, int causal, hipStream_t stream);
 

@@ -106,13 +106,18 @@ DeviceModule *module_for(int device, hipError_t *err) {
         *err = hipErrorInvalidImage;
         return nullptr;
     }
+    // failed runtime calls below are reported as hipErrorInvalidImage (the
+    // caller's status); the runtime's own record of them is cleared, so the
+    // caller's next runtime call does not report it again
     if (hipModuleLoadData(&m.mod, bytes.data()) != hipSuccess) {
+        (void)hipGetLastError();
         m.mod = nullptr;
         *err = hipErrorInvalidImage;
         return nullptr;
     }
     for (int i = 0; i < kNumKernels; ++i) {
         if (hipModuleGetFunction(&m.fn[i], m.mod, kNames[i]) != hipSuccess) {
+            (void)hipGetLastError();
             unload(m);
             *err = hipErrorInvalidImage;
             return nullptr;
@@ -122,6 +127,7 @@ DeviceModule *module_for(int device, hipError_t *err) {
     size_t bytes_g = 0;
     if (hipModuleGetGlobal(&ptr, &bytes_g, m.mod, "mxfa_delta_fallbacks") != hipSuccess ||
         bytes_g != sizeof(unsigned long long)) {
+        (void)hipGetLastError();
         unload(m);
         *err = hipErrorInvalidImage;
         return nullptr;
@@ -175,6 +181,23 @@ hipError_t launch_kernel(KernelId id, dim3 grid, dim3 block, void **args, hipStr
     if (m == nullptr) return err;
     return hipModuleLaunchKernel(m->fn[id], grid.x, grid.y, grid.z, block.x, block.y, block.z, 0, stream, args,
                                  nullptr);
+}
+
+hipError_t read_wg_times(void *dst, size_t bytes, size_t *avail) {
+    hipError_t err = hipSuccess;
+    DeviceModule *m = current_module(&err);
+    if (m == nullptr) return err;
+    hipDeviceptr_t ptr = nullptr;
+    size_t n = 0;
+    // present only in the timeline build of the code object; the runtime's
+    // record of the failed lookup is cleared, the status reports it
+    if (hipModuleGetGlobal(&ptr, &n, m->mod, "mxfa_wg_times") != hipSuccess) {
+        (void)hipGetLastError();
+        return hipErrorNotFound;
+    }
+    *avail = n;
+    if (dst == nullptr || bytes == 0) return hipSuccess;
+    return hipMemcpyDtoH(dst, ptr, bytes < n ? bytes : n);
 }
 
 hipError_t read_delta_fallbacks(unsigned long long *count) {

@@ -450,6 +450,13 @@ int mxfa_probe_mix(int mix, int waves_per_simd, int iters, float *sink, double *
     return from_hip(mxfa::launch_probe_mix(mix, waves_per_simd, iters, sink, static_cast<hipStream_t>(stream)));
 }
 
+int mxfa_probe_wg_times(void *dst, size_t bytes, size_t *avail) {
+    if (avail == nullptr) return MXFA_ERR_NULL;
+    const hipError_t e = mxfa::read_wg_times(dst, bytes, avail);
+    if (e == hipErrorNotFound) return MXFA_ERR_UNSUPPORTED;
+    return from_hip(e);
+}
+
 int mxfa_probe_read(const void *x, size_t bytes, float *sink, void *stream) {
     int rc = check_ptrs({x, sink});
     if (rc != MXFA_OK) return rc;

@@ -75,3 +75,51 @@ def test_probe_mix_ceilings_order():
     for m in ("dkv", "dkv_valu", "dkv_lds", "dq", "fwd"):
         assert 0.2 * mfma < got[m] < 1.05 * got["mfma"], m
     assert got["dkv"] < 1.05 * min(got["dkv_valu"], got["dkv_lds"])
+
+
+def test_timeline_build():
+    """The timeline build of the code object stamps every work-group of a
+    one-launch backward in order (start <= first stage <= end of loop <= stores
+    acknowledged) and computes the same bits as the normal build; the normal
+    build has no timeline (MXFA_ERR_UNSUPPORTED). The normal code object is
+    loaded again at the end."""
+    import numpy as np
+    import torch
+    import mx230_amd as mx
+    B, H, N, d = 1, 4, 1024, 64
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    q, k, v, do = (torch.randn((B, H, N, d), generator=gen, device="cuda").to(torch.bfloat16) for _ in range(4))
+    o = torch.empty_like(q)
+    lse = torch.empty((B, H, N), device="cuda")
+    delta = torch.empty_like(lse)
+
+    def bwd():
+        mx.run_flash_lse(q, k, v, o, lse, True)
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        mx.run_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, True)
+        torch.cuda.synchronize()
+        return dq, dk, dv
+
+    ref = bwd()
+    with pytest.raises(mx.MxfaError):
+        mx.probe_wg_times()
+    try:
+        mx.shutdown()
+        mx.set_code_object(mx.TIMELINE_CODE_OBJECT_PATH)
+        mx.init(0)
+        got = bwd()
+        t = mx.probe_wg_times()
+    finally:
+        mx.shutdown()
+        mx.set_code_object(None)
+        mx.init(0)
+    for a_, b_ in zip(got, ref):
+        assert torch.equal(a_, b_)
+    nwg = 2 * B * H * (N // 128)
+    t = t[:nwg].astype(np.int64)
+    assert np.all(t[:, 0] > 0)
+    assert np.all(np.diff(t, axis=1) >= 0)
+    span_us = (t[:, 3].max() - t[:, 0].min()) * 0.01
+    print(f"\n[timeline] {nwg} work-groups over {span_us:.1f} us", flush=True)
+    assert 1.0 < span_us < 10000.0
