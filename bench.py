@@ -347,13 +347,14 @@ def mix_probe(a):
 
 
 def timeline(a):
-    """One one-launch backward at the bench shape (bf16, causal or not, no
-    GQA split) with the timeline build of the code object: each dQ and dK/dV
-    work-group's prologue (start until its first stage is staged), loop time
-    per stage and epilogue (until its stores are acknowledged), the number of
-    work-groups resident over the launch, and the work-groups' resident time
-    summed and divided by the resident slots (256 CUs x the kernel's
-    work-groups per CU) against the launch's span. After >= 150 ms of warm-up
+    """One one-launch backward at the bench shape (bf16, causal or not; with
+    --Hkv below --H, through the GQA split's workspace) with the timeline build
+    of the code object: each dQ and dK/dV work-group's prologue (start until
+    its first stage is staged), loop time per stage and epilogue (until its
+    stores are acknowledged), the number of work-groups resident over the
+    launch, the work-groups' resident time summed and divided by the resident
+    slots (256 CUs x the kernel's work-groups per CU) against the launch's
+    span, and the work-groups that end last. After >= 150 ms of warm-up
     backward steps."""
     import numpy as np
     import torch
@@ -365,38 +366,45 @@ def timeline(a):
     torch.cuda.set_device(dev)
     mx.init(0)
     B, H, N, d, causal = a.B, a.H, a.N, a.d, bool(a.causal)
+    Hkv = a.Hkv or H
     gen = torch.Generator(device=dev)
     gen.manual_seed(1234)
-    q, k, v, do = (torch.randn((B, H, N, d), generator=gen, device=dev).to(torch.bfloat16) for _ in range(4))
-    o, dq, dk, dv = (torch.empty_like(q) for _ in range(4))
+    q, do = (torch.randn((B, H, N, d), generator=gen, device=dev).to(torch.bfloat16) for _ in range(2))
+    k, v = (torch.randn((B, Hkv, N, d), generator=gen, device=dev).to(torch.bfloat16) for _ in range(2))
+    o, dq = torch.empty_like(q), torch.empty_like(q)
+    dk, dv = torch.empty_like(k), torch.empty_like(k)
     lse = torch.empty((B, H, N), device=dev)
     delta = torch.empty_like(lse)
+    nws = mx.bwd_workspace_bytes(q, k, causal)
+    ws = torch.empty(nws, dtype=torch.uint8, device=dev) if nws else None
     mx.run_flash_lse(q, k, v, o, lse, causal)
     assert mx.bwd_one_launch(q, k, causal), "the timeline reads the one-launch backward"
     t0 = time.perf_counter()
     n = 0
     while time.perf_counter() - t0 < 0.15:
-        mx.run_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, causal)
+        mx.run_bwd_ws(q, k, v, o, do, lse, delta, dq, dk, dv, ws, causal)
         n += 1
         if n % 8 == 0:
             torch.cuda.synchronize()
     torch.cuda.synchronize()
-    mx.run_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, causal)
+    mx.run_bwd_ws(q, k, v, o, do, lse, delta, dq, dk, dv, ws, causal)
     torch.cuda.synchronize()
-    nbh, nqb = B * H, (N + 127) // 128
-    ndq, nkb = nbh * nqb, (N + 127) // 128
-    nwg = ndq + nbh * nkb
-    t = mx.probe_wg_times()[:nwg].astype(np.int64)
-    t = (t - t[:, 0].min()) * 0.01  # microseconds
+    # the launch's work-groups: dQ, then dK/dV; each recorded its kind, block
+    # and stages
+    split = mx.bwd_workspace_bytes(q, k, causal) // (8 * B * Hkv * N * d)
+    full = mx.probe_wg_times().astype(np.int64)
+    # rows past the launch's work-groups are zero or an earlier launch's
+    ndq = B * H * ((N + 127) // 128)
+    cur = full[:, 0] >= full[:ndq, 0].min()
+    nwg = len(full) if cur[ndq:].all() else ndq + int(np.argmin(cur[ndq:]))
+    full = full[:nwg]
+    kind, blk, stages = full[:, 4] >> 32, full[:, 4] & 0xffffffff, full[:, 5]
+    assert np.all(kind[:ndq] == 0) and np.all(kind[ndq:] == 1)
+    t = (full[:, :4] - full[:, 0].min()) * 0.01  # microseconds
     span = float(t[:, 3].max())
-    # stages of each work-group: dQ (query block qb) walks keys to its diagonal,
-    # dK/dV (key block kb) walks queries from its diagonal
-    qb = np.arange(ndq) // nbh
-    kb = np.arange(nbh * nkb) // nbh
-    stages = np.concatenate([2 * (qb + 1) if causal else np.full(ndq, N // 64),
-                             (N - 128 * kb) // 64 if causal else np.full(nbh * nkb, N // 64)])
-    out = {"shape": {"B": B, "H": H, "N": N, "d": d, "causal": causal}, "span_us": round(span, 1)}
-    slots = 256 * 3
+    out = {"shape": {"B": B, "Hq": H, "Hkv": Hkv, "N": N, "d": d, "causal": causal},
+           "dkv_partial_planes": int(max(split, 1)), "span_us": round(span, 1)}
+    slots = 256 * (3 if d == 64 else 2)
     for name, sl in (("dq", slice(0, ndq)), ("dkv", slice(ndq, nwg))):
         x, st = t[sl], stages[sl]
         pro, loop, epi = x[:, 1] - x[:, 0], x[:, 2] - x[:, 1], x[:, 3] - x[:, 2]
@@ -411,6 +419,12 @@ def timeline(a):
     grid = np.linspace(0.0, span, 21)
     out["resident_work_groups_every_5pct_of_span"] = [int(((t[:, 0] <= g) & (t[:, 3] > g)).sum()) for g in grid]
     out["slots"] = slots
+    last = []
+    for i in np.argsort(-t[:, 3])[:5]:
+        last.append({"kind": "dq" if i < ndq else "dkv", "block": int(blk[i]),
+                     "stages": int(stages[i]), "start_us": round(float(t[i, 0]), 1),
+                     "loop_start_us": round(float(t[i, 1]), 1), "end_us": round(float(t[i, 3]), 1)})
+    out["last_to_end"] = last
     print(json.dumps({"timeline": out}), flush=True)
 
 

@@ -209,11 +209,13 @@ int mxfa_bwd_delta_fallbacks(unsigned long long *count);
 /* Bytes of device workspace the _ws entry points below can use (0 for an
  * invalid shape). dQ is a separate atomic-free pass and needs none. With GQA
  * (Hq > Hkv), when the key blocks alone would leave the GPU underfilled, the
- * dK/dV pass splits each group's query heads over several work-groups per key
- * block: each writes fp32 partial dK/dV sums to the workspace and a second
- * launch adds them in a fixed order (deterministic, atomic-free). The size is
- * 2 * split * B * Hkv * N * d * 4 bytes, where split divides Hq / Hkv; 0 when
- * no split helps (always without GQA).
+ * dK/dV pass splits the work of each key block (its group's query heads, each
+ * from the diagonal) over several work-groups, a causal block with more
+ * queries over more of them: each writes fp32 partial dK/dV sums to the
+ * workspace and a second launch adds them in a fixed order (deterministic,
+ * atomic-free). The size is 2 * planes * B * Hkv * N * d * 4 bytes, planes
+ * being the most work-groups any key block takes; 0 when no split helps
+ * (always without GQA).
  * The reference has no GQA (d = 64, one head, attention_bwd.cu:165-243); this
  * sizes the scratch of its dK/dV pass generalised to GQA groups. */
 size_t mxfa_bwd_workspace_bytes(const mxfa_shape *shape);

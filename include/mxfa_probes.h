@@ -62,11 +62,13 @@ int mxfa_probe_mix(int mix, int waves_per_simd, int iters, float *sink, double *
  * mxfa_set_code_object before the device loads it), thread 0 of every dQ and
  * dK/dV work-group stamps the 100 MHz real-time counter at its start, once its
  * first stage is staged, at the end of its loop and once its stores are
- * acknowledged: four uint64 per linear work-group index (blockIdx.y *
- * gridDim.x + blockIdx.x), for the first 65536 work-groups of each launch,
- * each launch overwriting the last one's. Copies up to `bytes` of them to host
- * `dst` (a synchronous device-to-host copy; dst may be NULL) and writes their
- * size to *avail. MXFA_ERR_UNSUPPORTED with the normal code object. */
+ * acknowledged, and records its kind and block ((kind << 32) | block; kind 0
+ * = dQ, query block; 1 = dK/dV, key block) and its stages: eight uint64 per
+ * linear work-group index (blockIdx.y * gridDim.x + blockIdx.x; the last two
+ * zero), for the first 65536 work-groups of each launch, each launch
+ * overwriting the last one's. Copies up to `bytes` of them to host `dst` (a
+ * synchronous device-to-host copy; dst may be NULL) and writes their size to
+ * *avail. MXFA_ERR_UNSUPPORTED with the normal code object. */
 int mxfa_probe_wg_times(void *dst, size_t bytes, size_t *avail);
 /* Launches a grid-stride streaming read of `bytes` (a multiple of 16) at `x`,
  * the stream_f4 shape (isa.cu:55-63). */

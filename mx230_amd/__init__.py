@@ -588,11 +588,13 @@ def probe_mix_tflops(mix: str, waves_per_simd: int = 3, iters: int = 64, reps: i
 
 
 def probe_wg_times():
-    """The per-work-group timestamps of the last backward launch (mxfa_probe_wg_times;
-    only with TIMELINE_CODE_OBJECT_PATH loaded): a uint64 numpy array [groups, 4]
-    of 100 MHz real-time counter values (start, first stage staged, end of
-    loop, stores acknowledged) by linear work-group index; zero rows for
-    indices the launch did not have (or an earlier launch's values)."""
+    """The per-work-group timeline of the last backward launch (mxfa_probe_wg_times;
+    only with TIMELINE_CODE_OBJECT_PATH loaded): a uint64 numpy array [groups, 8]
+    by linear work-group index. Columns 0-3: 100 MHz real-time counter values
+    (start, first stage staged, end of loop, stores acknowledged); 4: (kind
+    << 32) | block (kind 0 = dQ and its query block, 1 = dK/dV and its key
+    block); 5: its stages; 6-7: zero. Zero rows for indices the launch did
+    not have (or an earlier launch's values)."""
     import numpy as np
     lib = load_library()
     avail = ctypes.c_size_t(0)
@@ -600,7 +602,7 @@ def probe_wg_times():
     buf = np.zeros(avail.value // 8, dtype=np.uint64)
     _check("mxfa_probe_wg_times", lib.mxfa_probe_wg_times(buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes,
                                                           ctypes.byref(avail)))
-    return buf.reshape(-1, 4)
+    return buf.reshape(-1, 8)
 
 
 def probe_dq_atomic(bh: int = 48, n: int = 4096, atomic: bool = True, reps: int = 5) -> dict:

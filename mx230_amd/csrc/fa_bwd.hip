@@ -111,18 +111,24 @@ constexpr int kFlagRows = 128;  // query rows per flag: one dQ work-group's bloc
 // thread 0 of every work-group of the dQ and dK/dV bodies stamps the 100 MHz
 // real-time counter at its start (0), once its first stage is staged (1), at
 // the end of its loop (2) and once its stores are acknowledged (3), into
-// mxfa_wg_times[4 g + i] for its linear work-group index g (read by
+// mxfa_wg_times[8 g + i] for its linear work-group index g, and records what
+// it ran: (kind << 32) | block at 8 g + 4 (kind 0 = dQ, block = query block;
+// 1 = dK/dV, block = key block) and its stages at 8 g + 5 (read by
 // mxfa_probe_wg_times). In every other build these compile to nothing.
 #if defined(__HIP_DEVICE_COMPILE__) && defined(MXFA_WG_TIMELINE)
 constexpr unsigned kTimelineGroups = 1u << 16;
-extern "C" __device__ unsigned long long mxfa_wg_times[kTimelineGroups * 4];
-__device__ unsigned long long mxfa_wg_times[kTimelineGroups * 4];
-__device__ __forceinline__ void wg_time(int i) {
+extern "C" __device__ unsigned long long mxfa_wg_times[kTimelineGroups * 8];
+__device__ unsigned long long mxfa_wg_times[kTimelineGroups * 8];
+__device__ __forceinline__ void wg_put(int i, unsigned long long v) {
     const unsigned g = blockIdx.y * gridDim.x + blockIdx.x;
     if (threadIdx.x == 0 && g < kTimelineGroups) {
-        *reinterpret_cast<volatile unsigned long long *>(mxfa_wg_times + 4 * (size_t)g + i) =
-            __builtin_amdgcn_s_memrealtime();
+        *reinterpret_cast<volatile unsigned long long *>(mxfa_wg_times + 8 * (size_t)g + i) = v;
     }
+}
+__device__ __forceinline__ void wg_time(int i) { wg_put(i, __builtin_amdgcn_s_memrealtime()); }
+__device__ __forceinline__ void wg_info(unsigned kind, int block, int stages) {
+    wg_put(4, ((unsigned long long)kind << 32) | (unsigned)block);
+    wg_put(5, (unsigned)stages);
 }
 __device__ __forceinline__ void wg_time_after_stores() {
     wait_stores();
@@ -130,6 +136,7 @@ __device__ __forceinline__ void wg_time_after_stores() {
 }
 #else
 __device__ __forceinline__ void wg_time(int) {}
+__device__ __forceinline__ void wg_info(unsigned, int, int) {}
 __device__ __forceinline__ void wg_time_after_stores() {}
 #endif
 
@@ -508,6 +515,7 @@ __device__ __forceinline__ void dq_body(const Params &p, int bh, int qb, DqSmem<
 
     const int kend = CAUSAL ? min(N, qb * BQ + BQ) : N;
     const int nsteps = (kend + BK - 1) / BK;
+    wg_info(0, qb, nsteps);
 
     const RowPlan<Pol, NT> plan(tid);
     stage_kv<Pol, NT>(sK[0], sV[0], K, V, 0, N, plan, wave);
@@ -577,13 +585,14 @@ struct DkvSmem {
     uint32_t sF[2];  // one-launch backward: the flags of the next stages' Delta blocks
 };
 
-// The dK/dV work of key block kb (4 Tile::ROWS keys) of grid column bx =
-// (batch, KV head) * dkv_split + share. WAIT (one-launch backward): Delta
-// comes from the dQ work-groups of the same launch; wave 1 stages a stage's
-// Delta rows only once their block's flag reads p.epoch (see issue below),
-// else computes them as DqTile does.
+// The dK/dV work wk (dkv_work): key block wk.kb (4 Tile::ROWS keys) of
+// (batch, KV head) wk.bkv, share wk.sp of wk.ns, i.e. the share's run of the
+// group's query heads' stages (head-major, each head's from the diagonal).
+// WAIT (one-launch backward): Delta comes from the dQ work-groups of the same
+// launch; wave 1 stages a stage's Delta rows only once their block's flag
+// reads p.epoch (see issue below), else computes them as DqTile does.
 template <class Tile, bool CAUSAL, bool WAIT = false, class DqTile = void>
-__device__ __forceinline__ void dkv_body(const Params &p, int bx, int kb, DkvSmem<typename Tile::Pol> &sm) {
+__device__ __forceinline__ void dkv_body(const Params &p, const DkvWork wk, DkvSmem<typename Tile::Pol> &sm) {
     using Pol = typename Tile::Pol;
     using T = typename Pol::T;
     constexpr int D = Pol::D;
@@ -601,11 +610,8 @@ __device__ __forceinline__ void dkv_body(const Params &p, int bx, int kb, DkvSme
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int N = p.N;
-    const int nsplit = p.dkv_split;
-    const int bkv = bx / nsplit;       // b * Hkv + kvh
-    const int sp = bx - bkv * nsplit;  // which share of the group's query heads
+    const int kb = wk.kb, bkv = wk.bkv;  // bkv = b * Hkv + kvh
     const int b = bkv / p.Hkv, kvh = bkv % p.Hkv;
-    const int h0 = sp * p.group / nsplit, nh = (sp + 1) * p.group / nsplit - h0;
     const size_t kvoff = (size_t)bkv * N * D;
     const int kw0 = kb * BKV + wave * Tile::ROWS;  // first key of this wave
     wg_time(0);
@@ -615,21 +621,32 @@ __device__ __forceinline__ void dkv_body(const Params &p, int bx, int kb, DkvSme
 
     const int qstart = CAUSAL ? kb * BKV : 0;
     const int nqs = (N - qstart + BQ - 1) / BQ;  // stages per query head
-    const int nsteps = nqs * nh;
-    const size_t bh0 = (size_t)b * p.Hq + (size_t)kvh * p.group + h0;
+    // the share's stages [g0, g0 + nsteps) of the group's p.group * nqs
+    int g0 = 0, nsteps = p.group * nqs;
+    if (wk.ns > 1) {
+        g0 = (int)((long long)wk.sp * nsteps / wk.ns);
+        nsteps = (int)((long long)(wk.sp + 1) * nsteps / wk.ns) - g0;
+    }
+    const size_t bh0 = (size_t)b * p.Hq + (size_t)kvh * p.group;  // the group's first query head
+    wg_info(1, kb, nsteps);
 
     // Stages are loaded strictly in order; (ld_h, ld_i) = query head and stage
     // within it of the next one (kept incrementally: no division per stage).
     const RowPlan<Pol, NT> plan(tid);
     int ld_h = 0, ld_i = 0;
+    if (g0 > 0) {
+        ld_h = g0 / nqs;
+        ld_i = g0 - ld_h * nqs;
+    }
+    const int i_first = ld_i;  // the first stage's place in its query head
     // WAIT: the flag of each stage's Delta block is fetched into sm.sF one
     // issue ahead, with a load that misses the caches (as are the Delta rows
     // themselves: the dQ work-group that wrote them may sit on another XCD).
     // It is checked before the Delta rows are staged; a flag not yet set is
     // polled for at most p.delta_wait ticks of the real-time counter, and then
     // the wave computes the rows itself, in the dQ tile's order (the same
-    // bits), and counts the event in g_delta_fallbacks. The first stage, with
-    // nothing fetched ahead, is polled directly.
+    // bits), and counts the event in mxfa_delta_fallbacks. The first stage,
+    // with nothing fetched ahead, is polled directly.
     const int nfb = (N + kFlagRows - 1) / kFlagRows;
     const uint32_t *flags = g_delta_flags + (size_t)p.flag_slot * kMaxFlagBlocks;
     auto issue = [&](int st) __attribute__((always_inline)) {
@@ -660,11 +677,12 @@ __device__ __forceinline__ void dkv_body(const Params &p, int bx, int kb, DkvSme
                     DqTile::delta_fallback(sD[bf], p, bh, qs, N, lane);
                     if (lane == 0) atomicAdd(&mxfa_delta_fallbacks, 1ull);
                 }
-                // one lane: the DMA writes each active lane's dword at base + 4 lane
-                if (ld_h < nh && lane == 0) {
-                    const int qs_next = qstart + ld_i * BQ;
-                    lds_dma4_uc(lds_addr(&sm.sF[(st + 1) & 1]), flags + (bh0 + ld_h) * nfb + qs_next / kFlagRows);
-                }
+            }
+            // the next stage's flag; one lane: the DMA writes each active
+            // lane's dword at base + 4 lane
+            if (wave == 1 && st + 1 < nsteps && lane == 0) {
+                const int qs_next = qstart + ld_i * BQ;
+                lds_dma4_uc(lds_addr(&sm.sF[(st + 1) & 1]), flags + (bh0 + ld_h) * nfb + qs_next / kFlagRows);
             }
         }
     };
@@ -704,37 +722,45 @@ __device__ __forceinline__ void dkv_body(const Params &p, int bx, int kb, DkvSme
     using Buf0 = std::integral_constant<int, 0>;
     using Buf1 = std::integral_constant<int, 1>;
     // rows past N get p = 0 from LSE = +inf, so only the causal diagonal masks
+    // each query head of the share's run: stages [i, iend) of its nqs
     const int ndiag = CAUSAL ? min(nqs, BKV / BQ) : 0;
-    for (int hh = 0, st = 0; hh < nh; ++hh) {
-        for (int i = 0; i < ndiag; ++i, ++st) run(st, i);
-        int i = ndiag;
-        if (i < nqs && (st & 1)) run_fixed(Buf1{}, st++, i++);
-        for (; i + 1 < nqs; i += 2, st += 2) {
+    for (int st = 0, i = i_first; st < nsteps; i = 0) {
+        const int iend = min(nqs, i + (nsteps - st));
+        // the diagonal stages (at most BKV / BQ: a loop of known length)
+        const int dend = min(ndiag, iend);
+#pragma unroll
+        for (int j = 0; j < BKV / BQ; ++j) {
+            if (i < dend) run(st++, i++);
+        }
+        if (i < iend && (st & 1)) run_fixed(Buf1{}, st++, i++);
+        for (; i + 1 < iend; i += 2, st += 2) {
             run_fixed(Buf0{}, st, i);
             run_fixed(Buf1{}, st + 1, i + 1);
         }
-        if (i < nqs) run_fixed(Buf0{}, st++, i);
+        if (i < iend) run_fixed(Buf0{}, st++, i);
     }
 
     wg_time(2);
-    if (nsplit > 1) {
-        // this share's fp32 partial sums (unscaled); dkv_reduce_kernel adds
-        // the shares and applies the scale
+    if (p.dkv_split > 1) {
+        // this share's fp32 partial sums (unscaled); dkv_reduce_body adds the
+        // block's shares and applies the scale
         const size_t plane = (size_t)p.B * p.Hkv * N * D;
-        float *wK = p.dkv_ws + (size_t)sp * plane + kvoff;
-        t.store(wK, wK + (size_t)nsplit * plane, kw0, N, 1.0f, lane);
+        float *wK = p.dkv_ws + (size_t)wk.sp * plane + kvoff;
+        t.store(wK, wK + (size_t)p.dkv_split * plane, kw0, N, 1.0f, lane);
     } else {
         t.store(static_cast<T *>(p.dk) + kvoff, static_cast<T *>(p.dv) + kvoff, kw0, N, -p.scale, lane);
     }
     wg_time_after_stores();
 }
 
-// The dK/dV pass as its own launch, grid (B Hkv split, key blocks). Causal:
-// key block 0 (the most queries) is dispatched first.
+// The dK/dV pass as its own launch, a 1-D grid of dkv_work's work-groups.
+// Causal: key block 0 (the most queries) is dispatched first.
 template <class Tile, bool CAUSAL>
 __device__ __forceinline__ void dkv_entry(const Params &p) {
     __shared__ DkvSmem<typename Tile::Pol> sm;
-    dkv_body<Tile, CAUSAL>(p, blockIdx.x, blockIdx.y, sm);
+    const DkvWork wk = dkv_work(p, blockIdx.x, 4 * Tile::ROWS, Tile::Pol::ROWS, CAUSAL);
+    if (wk.kb * 4 * Tile::ROWS >= p.N) return;
+    dkv_body<Tile, CAUSAL>(p, wk, sm);
 }
 
 // The whole backward from O in one launch (bf16): work-groups [0, fused_ndq)
@@ -760,28 +786,35 @@ __device__ __forceinline__ void bwd_fused_entry(const Params &p) {
         const int nbh = p.B * p.Hq;
         dq_body<DqT, CAUSAL, true, true>(p, bid % nbh, bid / nbh, sm.dq);
     } else {
-        const int w = bid - p.fused_ndq, nbk = p.B * p.Hkv * p.dkv_split;
-        dkv_body<DkvT, CAUSAL, true, DqT>(p, w % nbk, w / nbk, sm.dkv);
+        const DkvWork wk = dkv_work(p, bid - p.fused_ndq, 4 * DkvT::ROWS, DkvT::Pol::ROWS, CAUSAL);
+        if (wk.kb * 4 * DkvT::ROWS >= p.N) return;
+        dkv_body<DkvT, CAUSAL, true, DqT>(p, wk, sm.dkv);
     }
 }
 
-// dK / dV of a split dK/dV pass: the sum of the nsplit fp32 partial planes in
-// split order (so the result is deterministic), times -scale for dK. n4 =
-// float4 groups per plane; the dV planes follow the dK planes.
+// dK / dV of a split dK/dV pass: for each key row, the sum of its key block's
+// shares' fp32 partial planes in share order (so the result is
+// deterministic), times -scale for dK. n4 = float4 groups per plane
+// ([B Hkv][N][d]), d4 = d / 4; keys in blocks of bkv_rows, queries in stages
+// of bq; the dV planes follow the dK planes.
 template <class T>
-__device__ __forceinline__ void dkv_reduce_body(const float *ws, T *dk, T *dv, size_t n4, int nsplit, float kscale) {
-    const f32x4 *w = reinterpret_cast<const f32x4 *>(ws);
-    const size_t stride = (size_t)gridDim.x * 256;
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < 2 * n4; i += stride) {
+__device__ __forceinline__ void dkv_reduce_body(const Params &p, unsigned n4, int d4, int bkv_rows, int bq,
+                                                int causal) {
+    const f32x4 *w = reinterpret_cast<const f32x4 *>(p.dkv_ws);
+    T *dk = static_cast<T *>(p.dk), *dv = static_cast<T *>(p.dv);
+    const unsigned stride = gridDim.x * 256u;
+    for (unsigned i = blockIdx.x * 256u + threadIdx.x; i < 2 * n4; i += stride) {
         const bool isv = i >= n4;
-        const size_t j = isv ? i - n4 : i;
-        const f32x4 *src = w + (isv ? (size_t)nsplit * n4 : 0) + j;
+        const unsigned j = isv ? i - n4 : i;
+        const int kb = (int)((j / (unsigned)d4) % (unsigned)p.N) / bkv_rows;
+        const int ns = dkv_block_shares(p, (p.N - (causal ? kb * bkv_rows : 0) + bq - 1) / bq);
+        const f32x4 *src = w + (isv ? (size_t)p.dkv_split * n4 : 0) + j;
         f32x4 a = src[0];
-        for (int s = 1; s < nsplit; ++s) a += src[(size_t)s * n4];
+        for (int s = 1; s < ns; ++s) a += src[(size_t)s * n4];
         if (isv) {
-            store4<T>(dv + 4 * j, a, 1.0f);
+            store4<T>(dv + 4 * (size_t)j, a, 1.0f);
         } else {
-            store4<T>(dk + 4 * j, a, kscale);
+            store4<T>(dk + 4 * (size_t)j, a, -p.scale);
         }
     }
 }
@@ -814,9 +847,9 @@ using DkvB128 = DkvTile16<PolBF16<128>, 1>;
         bwd_fused_entry<DQT, DKVT, CAUSAL>(p);                                                           \
     }
 #define MXFA_REDUCE(NAME, T)                                                                             \
-    extern "C" __global__ __launch_bounds__(256) void NAME(const float *ws, T *dk, T *dv, size_t n4, int nsplit, \
-                                                           float kscale) {                               \
-        dkv_reduce_body<T>(ws, dk, dv, n4, nsplit, kscale);                                              \
+    extern "C" __global__ __launch_bounds__(256) void NAME(Params p, unsigned n4, int d4, int bkv_rows, int bq, \
+                                                           int causal) {                                 \
+        dkv_reduce_body<T>(p, n4, d4, bkv_rows, bq, causal);                                             \
     }
 MXFA_PREPROCESS(mxfa_preprocess_b64, u16, 64)
 MXFA_PREPROCESS(mxfa_preprocess_b128, u16, 128)
@@ -944,58 +977,104 @@ bool bwd_fused_available(const Params &p, int dtype_bf16, int d, hipStream_t str
 }
 
 template <class K>
-static hipError_t launch_dkv_reduce(const Params &p, hipStream_t stream) {
-    using T = typename K::Dkv::T;
-    size_t n4 = (size_t)p.B * p.Hkv * p.N * (K::Dkv::D / 4);
+static hipError_t launch_dkv_reduce(const Params &p, int causal, hipStream_t stream) {
+    using Tile = typename K::Dkv;
+    const size_t n4 = (size_t)p.B * p.Hkv * p.N * (Tile::D / 4);
+    if (2 * n4 >= 0xffffffffULL) return hipErrorInvalidValue;
     const size_t blocks = std::min<size_t>((2 * n4 + 255) / 256, 4096);
-    const float *ws = p.dkv_ws;
-    T *dk = static_cast<T *>(p.dk), *dv = static_cast<T *>(p.dv);
-    int nsplit = p.dkv_split;
-    float kscale = -p.scale;
-    void *args[] = {&ws, &dk, &dv, &n4, &nsplit, &kscale};
+    unsigned n4u = (unsigned)n4;
+    int d4 = Tile::D / 4, bkv_rows = 4 * Tile::ROWS, bq = Tile::Pol::ROWS;
+    void *args[] = {const_cast<Params *>(&p), &n4u, &d4, &bkv_rows, &bq, &causal};
     return launch_kernel(K::reduce, dim3((unsigned)blocks), dim3(256), args, stream);
 }
 
-// How many work-groups share the query heads of a key block's GQA group: the
-// smallest divisor of the group that gives the launch at least two
-// work-groups per resident slot (256 CUs x the kernel's work-groups per CU),
-// else the whole group (one query head per work-group). 1 without GQA or when
-// the key blocks alone fill the GPU twice over. A share's heads run one after
-// another, so its causal key block 0 is the launch's critical path: at cfg5
-// d = 128 (128 key blocks, 512 slots) 8 shares ran 144 us against 157 us for
-// the 4 that one slot each would give.
+// The split of a dK/dV pass over its GQA group's query heads (Params::
+// dkv_split and the two fields after it), for the pass's tile:
+//  * none (dkv_split = 1) without GQA or when the key blocks alone give the
+//    launch at least two work-groups per resident slot (256 CUs x the kernel's
+//    work-groups per CU);
+//  * else every key block gets at least dkv_min_shares shares: the smallest
+//    divisor of the group that gives two work-groups per slot, else the whole
+//    group (one query head per share);
+//  * and a causal block with more stages gets more shares, about
+//    dkv_share_stages stages each: the stages one slot runs on average over a
+//    one-launch backward (dK/dV stages plus half the dQ stages, which cost
+//    about half as much, over the slots), but at least 8 (a work-group's
+//    prologue and epilogue take about as long as 3-4 stages) and no more than
+//    twice the minimum shares per block. A share's stages run one after
+//    another, so the heaviest share is the launch's critical path: at cfg5
+//    d = 64 (B1 Hq32 Hkv4 N2048), one query head per share left key block 0's
+//    32 stages per share as the last work-groups to end, with most slots idle.
 template <class Tile>
-static int dkv_split_t(const Params &p) {
-    if (p.group <= 1) return 1;
-    constexpr int BKV = 4 * Tile::ROWS;
+static void dkv_plan_t(Params &p, bool causal) {
+    p.dkv_split = p.dkv_min_shares = 1;
+    p.dkv_share_stages = 1 << 30;
+    if (p.group <= 1) return;
+    constexpr int BKV = 4 * Tile::ROWS, BQ = Tile::Pol::ROWS;
     constexpr long long kSlots = 256LL * Tile::kWaves;
-    const long long base = (long long)p.B * p.Hkv * ((p.N + BKV - 1) / BKV);
-    for (int s = 1; s < p.group; ++s) {
-        if (p.group % s == 0 && base * s >= 2 * kSlots) return s;
+    const long long nbkv = (long long)p.B * p.Hkv, nkb = (p.N + BKV - 1) / BKV;
+    int s = p.group;
+    for (int c = 1; c < p.group; ++c) {
+        if (p.group % c == 0 && nbkv * nkb * c >= 2 * kSlots) {
+            s = c;
+            break;
+        }
     }
-    return p.group;
+    if (s == 1) return;
+    // stages of the dK/dV work (every query head of every key block) and of
+    // the dQ work (128-query blocks over 64-key stages)
+    long long dkv_stages = 0, dq_stages = 0;
+    for (long long kb = 0; kb < nkb; ++kb) dkv_stages += (p.N - (causal ? kb * BKV : 0) + BQ - 1) / BQ;
+    for (long long qb = 0; qb < (p.N + 127) / 128; ++qb) {
+        dq_stages += ((causal ? std::min<long long>(p.N, 128 * (qb + 1)) : p.N) + 63) / 64;
+    }
+    const long long per_slot = (dkv_stages * p.group * nbkv + dq_stages * p.B * p.Hq / 2 + kSlots - 1) / kSlots;
+    const long long most_stages = (long long)p.group * ((p.N + BQ - 1) / BQ);  // key block 0's
+    const long long w = std::max({per_slot, 8LL, (most_stages + 2 * s - 1) / (2 * s)});
+    p.dkv_split = 2;  // marks the split for dkv_block_shares
+    p.dkv_min_shares = s;
+    p.dkv_share_stages = (int)std::min<long long>(w, 1 << 30);
+    int most = 1;
+    for (long long kb = 0; kb < nkb; ++kb) {
+        most = std::max(most, dkv_block_shares(p, (int)((p.N - (causal ? kb * BKV : 0) + BQ - 1) / BQ)));
+    }
+    p.dkv_split = most;
 }
 
-int dkv_split(const Params &p, int dtype_bf16, int d) {
-    if (dtype_bf16) {
-        if (d == 64) return dkv_split_t<DkvB64>(p);
-        if (d == 128) return dkv_split_t<DkvB128>(p);
-    } else if (d == 64) {
-        return dkv_split_t<DkvF32>(p);
+// The work-groups of a dK/dV pass (dkv_work's order) with p's split.
+template <class Tile>
+static long long dkv_work_groups(const Params &p, bool causal) {
+    constexpr int BKV = 4 * Tile::ROWS, BQ = Tile::Pol::ROWS;
+    const long long nbkv = (long long)p.B * p.Hkv, nkb = (p.N + BKV - 1) / BKV;
+    if (p.dkv_split <= 1) return nbkv * nkb;
+    long long n = 0;
+    for (long long kb = 0; kb < nkb; ++kb) {
+        n += nbkv * dkv_block_shares(p, (int)((p.N - (causal ? kb * BKV : 0) + BQ - 1) / BQ));
     }
-    return 1;
+    return n;
+}
+
+int dkv_split(const Params &p, int dtype_bf16, int d, int causal) {
+    Params q = p;
+    if (dtype_bf16) {
+        if (d == 64) dkv_plan_t<DkvB64>(q, causal != 0);
+        if (d == 128) dkv_plan_t<DkvB128>(q, causal != 0);
+    } else if (d == 64) {
+        dkv_plan_t<DkvF32>(q, causal != 0);
+    }
+    return q.dkv_split;
 }
 
 template <class K>
 static hipError_t launch_fused_k(Params p, int causal, hipStream_t stream) {
-    constexpr int BKV = 4 * K::Dkv::ROWS;
     // with a workspace, GQA shapes split each group's query heads as in the
     // dK/dV pass; the shares' partial sums are added by a second launch
-    p.dkv_split = p.dkv_ws != nullptr ? dkv_split_t<typename K::Dkv>(p) : 1;
+    dkv_plan_t<typename K::Dkv>(p, causal != 0);
+    if (p.dkv_ws == nullptr) p.dkv_split = 1;
     if (p.dkv_split == 1) p.dkv_ws = nullptr;
     const long long nfb = (p.N + kFlagRows - 1) / kFlagRows;
     const long long ndq = (long long)p.B * p.Hq * nfb;
-    const long long ndkv = (long long)p.B * p.Hkv * p.dkv_split * ((p.N + BKV - 1) / BKV);
+    const long long ndkv = dkv_work_groups<typename K::Dkv>(p, causal != 0);
     if (ndq + ndkv > 0x7fffffffLL) return hipErrorInvalidValue;
     unsigned e = ++g_epoch;
     if (e == 0) e = ++g_epoch;  // 0 is the flags' initial value
@@ -1009,7 +1088,7 @@ static hipError_t launch_fused_k(Params p, int causal, hipStream_t stream) {
     const hipError_t err = launch_kernel(K::fused[causal ? 1 : 0], dim3((unsigned)(ndq + ndkv)), dim3(256), args,
                                          stream);
     if (err != hipSuccess || p.dkv_split == 1) return err;
-    return launch_dkv_reduce<K>(p, stream);
+    return launch_dkv_reduce<K>(p, causal, stream);
 }
 
 hipError_t launch_bwd_fused(const Params &p, int d, int causal, hipStream_t stream) {
@@ -1023,13 +1102,15 @@ static hipError_t launch_dkv_k(Params p, int causal, hipStream_t stream) {
     using Tile = typename K::Dkv;
     // with a workspace, GQA shapes whose key blocks alone underfill the GPU
     // split each group's query heads over several work-groups
-    p.dkv_split = p.dkv_ws != nullptr ? dkv_split_t<Tile>(p) : 1;
+    dkv_plan_t<Tile>(p, causal != 0);
+    if (p.dkv_ws == nullptr) p.dkv_split = 1;
     if (p.dkv_split == 1) p.dkv_ws = nullptr;
-    const dim3 grid(p.B * p.Hkv * p.dkv_split, (p.N + 4 * Tile::ROWS - 1) / (4 * Tile::ROWS));
+    const long long n = dkv_work_groups<Tile>(p, causal != 0);
+    if (n > 0x7fffffffLL) return hipErrorInvalidValue;
     void *args[] = {&p};
-    const hipError_t e = launch_kernel(K::dkv[causal ? 1 : 0], grid, dim3(256), args, stream);
+    const hipError_t e = launch_kernel(K::dkv[causal ? 1 : 0], dim3((unsigned)n), dim3(256), args, stream);
     if (e != hipSuccess || p.dkv_split == 1) return e;
-    return launch_dkv_reduce<K>(p, stream);
+    return launch_dkv_reduce<K>(p, causal, stream);
 }
 
 hipError_t launch_bwd_dkv(const Params &p, int dtype_bf16, int d, int causal, hipStream_t stream) {

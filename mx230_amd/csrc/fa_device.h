@@ -45,12 +45,14 @@ struct Params {
     // kernels assume it.
     long long q_bs, q_hs, kv_bs, kv_hs, o_bs, o_hs;
     int q_rs, kv_rs, o_rs, Nk, pos0;
-    // dK/dV pass: the query heads of a GQA group split over dkv_split
-    // work-groups per key block; with dkv_split > 1 each writes fp32 partial
-    // sums to dkv_ws ([split][B*Hkv][N][d] for dK, then the same for dV) and a
-    // reduce launch adds them in split order.
+    // dK/dV pass with dkv_split > 1: the group's query heads' stages of a
+    // key block (group x its stages per head, in head order) are split into
+    // dkv_block_shares(...) contiguous runs, one work-group each; share s
+    // writes fp32 partial sums to plane s of dkv_ws ([dkv_split][B*Hkv][N][d]
+    // for dK, then the same for dV; dkv_split = the most shares of any block)
+    // and a reduce launch adds each block's planes in share order.
     float *dkv_ws;
-    int dkv_split;
+    int dkv_split, dkv_min_shares, dkv_share_stages;
     // One-launch backward (bwd_fused_entry, kernels mxfa_bwd_*): work-groups [0, fused_ndq) run
     // the dQ pass and publish Delta per 128-row query block with flag value
     // epoch in slot flag_slot of g_delta_flags; the rest run the dK/dV pass
@@ -66,6 +68,39 @@ struct Params {
 // flags) of kMaxFlagBlocks flags, one per (batch, query head, 128-row block).
 constexpr int kFlagSlots = 4;
 constexpr int kMaxFlagBlocks = 1 << 18;
+
+// Shares of a dK/dV key block whose queries take nqs stages per query head:
+// its group x nqs stages in runs of about dkv_share_stages, never fewer than
+// dkv_min_shares runs nor more runs than stages (1 without a split).
+__host__ __device__ inline int dkv_block_shares(const Params &p, int nqs) {
+    if (p.dkv_split <= 1) return 1;
+    const int t = p.group * nqs;
+    const int n = t / p.dkv_share_stages + (t % p.dkv_share_stages != 0 ? 1 : 0);
+    const int s = n > p.dkv_min_shares ? n : p.dkv_min_shares;
+    return s < t ? s : t;
+}
+
+// The work of work-group w of a dK/dV pass (keys in blocks of bkv_rows,
+// queries in stages of bq): key block kb, causal key block 0 (the most
+// queries) first, then (batch, KV head) bkv, then share sp of the block's ns.
+// kb is the number of key blocks when w is past the pass's last work-group.
+struct DkvWork {
+    int bkv, kb, sp, ns;
+};
+__host__ __device__ inline DkvWork dkv_work(const Params &p, int w, int bkv_rows, int bq, bool causal) {
+    const int nbkv = p.B * p.Hkv, nkb = (p.N + bkv_rows - 1) / bkv_rows;
+    if (p.dkv_split <= 1) return {w % nbkv, w / nbkv, 0, 1};
+    if (!causal) {
+        const int ns = dkv_block_shares(p, (p.N + bq - 1) / bq), per = nbkv * ns, r = w % per;
+        return {r / ns, w / per, r % ns, ns};
+    }
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int ns = dkv_block_shares(p, (p.N - kb * bkv_rows + bq - 1) / bq);
+        if (w < nbkv * ns) return {w / ns, kb, w % ns, ns};
+        w -= nbkv * ns;
+    }
+    return {0, nkb, 0, 1};
+}
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 

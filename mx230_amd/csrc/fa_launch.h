@@ -36,11 +36,12 @@ hipError_t launch_fwd(const Params &p, int dtype_bf16, int d, int causal, hipStr
 hipError_t launch_preprocess(const Params &p, int dtype_bf16, int d, hipStream_t stream);
 // delta != 0: the dQ pass computes Delta from p.o_in and writes it to p.delta
 hipError_t launch_bwd_dq(const Params &p, int dtype_bf16, int d, int causal, int delta, hipStream_t stream);
-// p.dkv_ws != nullptr: GQA shapes may split each group's query heads over
-// dkv_split(p, ...) work-groups, with fp32 partials in p.dkv_ws (2 * split *
-// B * Hkv * N * d floats) and a second, reducing launch
+// p.dkv_ws != nullptr: GQA shapes may split each key block's query heads'
+// stages over several work-groups, with fp32 partials in p.dkv_ws (2 *
+// dkv_split(p, ...) * B * Hkv * N * d floats) and a second, reducing launch
 hipError_t launch_bwd_dkv(const Params &p, int dtype_bf16, int d, int causal, hipStream_t stream);
-int dkv_split(const Params &p, int dtype_bf16, int d);
+// partial planes of the split (the most shares of any key block; 1: none)
+int dkv_split(const Params &p, int dtype_bf16, int d, int causal);
 // The one-launch backward from O (dQ pass with Delta + dK/dV pass, bf16;
 // with p.dkv_ws a GQA split as launch_bwd_dkv, whose reduce then follows as a
 // second launch): available for the shape, and launched with its own epoch.

@@ -58,7 +58,8 @@ Params make_params(const mxfa_shape *s) {
     p.Nk = s->N;
     p.pos0 = 0;
     p.dkv_ws = nullptr;
-    p.dkv_split = 1;
+    p.dkv_split = p.dkv_min_shares = 1;
+    p.dkv_share_stages = 1 << 30;
     return p;
 }
 
@@ -333,9 +334,9 @@ int mxfa_bwd_delta_fallbacks(unsigned long long *count) {
 size_t mxfa_bwd_workspace_bytes(const mxfa_shape *shape) {
     if (check_shape(shape) != MXFA_OK) return 0;
     const Params p = make_params(shape);
-    const int split = mxfa::dkv_split(p, shape->dtype == MXFA_BF16, shape->d);
+    const int split = mxfa::dkv_split(p, shape->dtype == MXFA_BF16, shape->d, shape->causal);
     if (split <= 1) return 0;
-    // fp32 partial dK and dV planes, one pair per share of the query heads
+    // fp32 partial dK and dV planes, one pair per share of a key block
     return 2 * (size_t)split * shape->B * shape->Hkv * shape->N * shape->d * sizeof(float);
 }
 

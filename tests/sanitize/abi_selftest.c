@@ -78,7 +78,7 @@ int main(void) {
     EXPECT(mxfa_bwd_workspace_bytes(NULL), 0);
     EXPECT(mxfa_bwd_workspace_bytes(&ok), 0);
     s = shape(2, 14, 2, 4096, 64, 1, MXFA_BF16, 0.0f);
-    EXPECT(mxfa_bwd_workspace_bytes(&s), 2LL * 7 * 2 * 2 * 4096 * 64 * 4);
+    EXPECT(mxfa_bwd_workspace_bytes(&s), 2LL * 8 * 2 * 2 * 4096 * 64 * 4); /* cfg4: 8 planes */
     EXPECT(mxfa_naive_scratch_bytes(&ok), 4LL * 12 * 4096 * 4096 * 4);
     EXPECT(mxfa_naive_scratch_bytes(NULL), 0);
     EXPECT(mxfa_bwd_one_launch(&ok), 1);

@@ -106,10 +106,12 @@ def test_sizes_and_strings(lib):
     # no GQA: nothing to split
     (dict(B=4, Hq=12, Hkv=12, N=4096, d=64), 0),
     # cfg4 (Qwen2.5, 7:1): 2*2 (b, kv head) x 32 key blocks = 128 work-groups
-    # for 2 x 768 slots; 7 is prime, so one query head per work-group
-    (dict(B=2, Hq=14, Hkv=2, N=4096, d=64), 2 * 7 * 2 * 2 * 4096 * 64 * 4),
-    # cfg5 d=64 (TinyLlama, 8:1): 64 work-groups; 4 shares give 256 < 1536, so 8
-    (dict(B=1, Hq=32, Hkv=4, N=2048, d=64), 2 * 8 * 1 * 4 * 2048 * 64 * 4),
+    # for 2 x 768 slots; 7 is prime, so one query head per share at least;
+    # about 58 stages per share gives key blocks 0-2 (7 x 64-60 stages) 8
+    (dict(B=2, Hq=14, Hkv=2, N=4096, d=64), 2 * 8 * 2 * 2 * 4096 * 64 * 4),
+    # cfg5 d=64 (TinyLlama, 8:1): 64 work-groups; 4 shares give 256 < 1536, so
+    # 8 at least; about 17 stages per share gives key block 0 (8 x 32 stages) 16
+    (dict(B=1, Hq=32, Hkv=4, N=2048, d=64), 2 * 16 * 1 * 4 * 2048 * 64 * 4),
     # cfg5 d=128: 64-key blocks, 128 work-groups for 2 x 512 slots: 8 shares
     (dict(B=1, Hq=32, Hkv=4, N=2048, d=128), 2 * 8 * 1 * 4 * 2048 * 128 * 4),
     # 8 * 8 (b, kv head) x 32 key blocks = 2048 work-groups, twice 768 slots: no split
@@ -332,7 +334,7 @@ def test_noalloc_rejects_shapes_beyond_its_scratch(lib):
     more is MXFA_ERR_SCRATCH before any device work (fake pointers, no GPU)."""
     assert lib.mxfa_bwd_noalloc_scratch_bytes() == 64 << 20
     p = ctypes.c_void_p(4096)
-    fits = _shape(B=1, Hq=32, Hkv=4, N=2048, d=128)  # cfg5 d = 128: exactly 64 MiB
+    fits = _shape(B=1, Hq=32, Hkv=4, N=2048, d=128)  # cfg5 d = 128: exactly 64 MiB (8 planes)
     assert lib.mxfa_bwd_workspace_bytes(ctypes.byref(fits)) == 64 << 20
     big = _shape(B=1, Hq=64, Hkv=4, N=8192, d=64)  # 8 shares of 256 key blocks: 128 MiB
     assert lib.mxfa_bwd_workspace_bytes(ctypes.byref(big)) == 2 * 8 * 4 * 8192 * 64 * 4

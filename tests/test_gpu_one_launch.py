@@ -113,10 +113,14 @@ def test_one_launch_fallback(opts, name, shape, causal):
     n1 = mx.bwd_delta_fallbacks()
     for n, a, b in zip(("Delta", "dQ", "dK", "dV"), got, ref):
         assert torch.equal(a, b), f"{name}: {n} of the fallback differs from the two-launch backward"
-    # one fallback per stage of every dK/dV work-group: at least one per
-    # (KV head, key block), and none when the waits are allowed
+    # one fallback per stage of every dK/dV work-group (a work-group per
+    # (batch, KV head, key block of 4 x 32 keys, 4 x 16 at d = 128) walks
+    # every query head of its group from its diagonal in 64-query stages),
+    # and none when the waits are allowed
     B, H, Hkv, N, d = shape
-    assert n1 - n0 >= B * Hkv * ((N + 127) // 128) // 2, (n0, n1)
+    bkv = 128 if d == 64 else 64
+    want = B * Hkv * sum((H // Hkv) * -(-(N - (kb * bkv if causal else 0)) // 64) for kb in range(-(-N // bkv)))
+    assert n1 - n0 == want, (n0, n1, want)
     opts(delta_wait_us=200)
     _sync(_bwd(t, causal))
     print(f"[{name}] fallbacks forced {n1 - n0}, then {mx.bwd_delta_fallbacks() - n1}", flush=True)

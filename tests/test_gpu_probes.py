@@ -117,9 +117,19 @@ def test_timeline_build():
     for a_, b_ in zip(got, ref):
         assert torch.equal(a_, b_)
     nwg = 2 * B * H * (N // 128)
-    t = t[:nwg].astype(np.int64)
+    info = t[:nwg, 4:6].astype(np.int64)
+    t = t[:nwg, :4].astype(np.int64)
     assert np.all(t[:, 0] > 0)
     assert np.all(np.diff(t, axis=1) >= 0)
+    # dQ work-groups first (query blocks in increasing order), then dK/dV
+    # (key block 0 first); causal stages: 2 (qb + 1) and N / 64 - 2 kb
+    ndq = nwg // 2
+    kind, block = info[:, 0] >> 32, info[:, 0] & 0xffffffff
+    assert np.all(kind[:ndq] == 0) and np.all(kind[ndq:] == 1)
+    assert np.array_equal(block[:ndq], np.arange(ndq) // (B * H))
+    assert np.array_equal(block[ndq:], np.arange(ndq) // (B * H))
+    assert np.array_equal(info[:ndq, 1], 2 * (block[:ndq] + 1))
+    assert np.array_equal(info[ndq:, 1], N // 64 - 2 * block[ndq:])
     span_us = (t[:, 3].max() - t[:, 0].min()) * 0.01
     print(f"\n[timeline] {nwg} work-groups over {span_us:.1f} us", flush=True)
     assert 1.0 < span_us < 10000.0
