@@ -346,16 +346,58 @@ def mix_probe(a):
                                     "peak_tflops": PEAK_TFLOPS["bf16"]}}), flush=True)
 
 
+def _timeline_pass(t, stages, slots):
+    """Summary of one kernel's work-groups (t: [groups, 4] microseconds from
+    the launch's first start)."""
+    pro, loop, epi = t[:, 1] - t[:, 0], t[:, 2] - t[:, 1], t[:, 3] - t[:, 2]
+    busy = t[:, 3] - t[:, 0]
+    return {"work_groups": int(len(t)), "first_start_us": round(float(t[:, 0].min()), 1),
+            "last_start_us": round(float(t[:, 0].max()), 1), "last_end_us": round(float(t[:, 3].max()), 1),
+            "prologue_us_mean": round(float(pro.mean()), 2),
+            "loop_us_per_stage_mean": round(float((loop / stages).mean()), 3),
+            "epilogue_us_mean": round(float(epi.mean()), 2),
+            "prologue_share_of_resident_time": round(float(pro.sum() / busy.sum()), 3)}
+
+
+def _timeline_launch(full, kinds, names):
+    """Summary of one launch from its rows of the timeline build's array:
+    span, the work-groups resident at once (the most of them is the slots the
+    launch had: CUs x work-groups per CU), the work-groups' resident time over
+    those slots, per pass (kind) prologue / loop per stage / epilogue, and the
+    five work-groups that end last."""
+    import numpy as np
+    kind, blk, stages = full[:, 4] >> 32, full[:, 4] & 0xffffffff, full[:, 5]
+    t = (full[:, :4] - full[:, 0].min()) * 0.01  # microseconds
+    span = float(t[:, 3].max())
+    ev = np.concatenate([np.stack([t[:, 0], np.ones(len(t))], 1), np.stack([t[:, 3], -np.ones(len(t))], 1)])
+    ev = ev[np.lexsort((ev[:, 1], ev[:, 0]))]  # ends before starts at equal times
+    slots = int(np.cumsum(ev[:, 1]).max())
+    g = np.arange(len(t))
+    out = {"span_us": round(span, 1), "slots_observed": slots,
+           "resident_time_over_slots_us": round(float((t[:, 3] - t[:, 0]).sum() / slots), 1),
+           # work-groups go to the 8 XCDs round robin in dispatch order
+           "first_start_by_xcd_us": [round(float(t[g % 8 == x, 0].min()), 1) for x in range(8)]}
+    for k, name in zip(kinds, names):
+        sel = kind == k
+        out[name] = _timeline_pass(t[sel], stages[sel], slots)
+    grid = np.linspace(0.0, span, 21)
+    out["resident_work_groups_every_5pct_of_span"] = [int(((t[:, 0] <= g) & (t[:, 3] > g)).sum()) for g in grid]
+    out["last_to_end"] = [{"kind": names[kinds.index(int(kind[i]))], "block": int(blk[i]), "stages": int(stages[i]),
+                           "start_us": round(float(t[i, 0]), 1), "loop_start_us": round(float(t[i, 1]), 1),
+                           "end_us": round(float(t[i, 3]), 1)} for i in np.argsort(-t[:, 3])[:5]]
+    return out
+
+
 def timeline(a):
-    """One one-launch backward at the bench shape (bf16, causal or not; with
-    --Hkv below --H, through the GQA split's workspace) with the timeline build
-    of the code object: each dQ and dK/dV work-group's prologue (start until
-    its first stage is staged), loop time per stage and epilogue (until its
-    stores are acknowledged), the number of work-groups resident over the
-    launch, the work-groups' resident time summed and divided by the resident
-    slots (256 CUs x the kernel's work-groups per CU) against the launch's
-    span, and the work-groups that end last. After >= 150 ms of warm-up
-    backward steps."""
+    """One one-launch backward and one forward at the bench shape (bf16,
+    causal or not; with --Hkv below --H, the backward through the GQA split's
+    workspace) with the timeline build of the code object: for each kernel
+    its span, the work-groups resident over the launch, their resident time
+    summed over the slots it had (the most resident at once), each pass's
+    prologue (start until its first stage is staged), loop time per stage and
+    epilogue (until its stores are acknowledged), and the work-groups that end
+    last. Each measured launch follows >= 150 ms of calls of the same kind,
+    the last eight of them queued back to back with it."""
     import numpy as np
     import torch
     import mx230_amd as mx
@@ -377,54 +419,43 @@ def timeline(a):
     delta = torch.empty_like(lse)
     nws = mx.bwd_workspace_bytes(q, k, causal)
     ws = torch.empty(nws, dtype=torch.uint8, device=dev) if nws else None
-    mx.run_flash_lse(q, k, v, o, lse, causal)
     assert mx.bwd_one_launch(q, k, causal), "the timeline reads the one-launch backward"
-    t0 = time.perf_counter()
-    n = 0
-    while time.perf_counter() - t0 < 0.15:
-        mx.run_bwd_ws(q, k, v, o, do, lse, delta, dq, dk, dv, ws, causal)
-        n += 1
-        if n % 8 == 0:
-            torch.cuda.synchronize()
-    torch.cuda.synchronize()
+
+    def warm(fn):
+        # >= 150 ms of calls, the last 8 queued back to back with the measured
+        # one: after an idle gap (a synchronisation) the first launch has been
+        # seen to start on some XCDs up to ~30 us after the others
+        t0 = time.perf_counter()
+        n = 0
+        while n % 8 != 7 or time.perf_counter() - t0 < 0.15:
+            fn()
+            n += 1
+            if n % 8 == 0:
+                torch.cuda.synchronize()
+
+    out = {"shape": {"B": B, "Hq": H, "Hkv": Hkv, "N": N, "d": d, "causal": causal},
+           "dkv_partial_planes": int(max(nws // (8 * B * Hkv * N * d), 1))}
+    mx.run_flash_lse(q, k, v, o, lse, causal)
+    # the backward's work-groups: dQ, then dK/dV; rows past them are zero, an
+    # earlier launch's (older stamps) or the forward's
+    warm(lambda: mx.run_bwd_ws(q, k, v, o, do, lse, delta, dq, dk, dv, ws, causal))
     mx.run_bwd_ws(q, k, v, o, do, lse, delta, dq, dk, dv, ws, causal)
     torch.cuda.synchronize()
-    # the launch's work-groups: dQ, then dK/dV; each recorded its kind, block
-    # and stages
-    split = mx.bwd_workspace_bytes(q, k, causal) // (8 * B * Hkv * N * d)
     full = mx.probe_wg_times().astype(np.int64)
-    # rows past the launch's work-groups are zero or an earlier launch's
-    ndq = B * H * ((N + 127) // 128)
-    cur = full[:, 0] >= full[:ndq, 0].min()
-    nwg = len(full) if cur[ndq:].all() else ndq + int(np.argmin(cur[ndq:]))
+    kind = full[:, 4] >> 32
+    ndq = int(np.argmin(kind == 0))
+    cur = (kind[ndq:] == 1) & (full[ndq:, 0] >= full[:ndq, 0].min())
+    nwg = len(full) if cur.all() else ndq + int(np.argmin(cur))
     full = full[:nwg]
-    kind, blk, stages = full[:, 4] >> 32, full[:, 4] & 0xffffffff, full[:, 5]
-    assert np.all(kind[:ndq] == 0) and np.all(kind[ndq:] == 1)
-    t = (full[:, :4] - full[:, 0].min()) * 0.01  # microseconds
-    span = float(t[:, 3].max())
-    out = {"shape": {"B": B, "Hq": H, "Hkv": Hkv, "N": N, "d": d, "causal": causal},
-           "dkv_partial_planes": int(max(split, 1)), "span_us": round(span, 1)}
-    slots = 256 * (3 if d == 64 else 2)
-    for name, sl in (("dq", slice(0, ndq)), ("dkv", slice(ndq, nwg))):
-        x, st = t[sl], stages[sl]
-        pro, loop, epi = x[:, 1] - x[:, 0], x[:, 2] - x[:, 1], x[:, 3] - x[:, 2]
-        busy = x[:, 3] - x[:, 0]
-        out[name] = {"work_groups": int(len(x)), "first_start_us": round(float(x[:, 0].min()), 1),
-                     "last_start_us": round(float(x[:, 0].max()), 1), "last_end_us": round(float(x[:, 3].max()), 1),
-                     "prologue_us_mean": round(float(pro.mean()), 2),
-                     "loop_us_per_stage_mean": round(float((loop / st).mean()), 3),
-                     "epilogue_us_mean": round(float(epi.mean()), 2),
-                     "prologue_share_of_resident_time": round(float(pro.sum() / busy.sum()), 3)}
-    out["resident_time_over_slots_us"] = round(float((t[:, 3] - t[:, 0]).sum() / slots), 1)
-    grid = np.linspace(0.0, span, 21)
-    out["resident_work_groups_every_5pct_of_span"] = [int(((t[:, 0] <= g) & (t[:, 3] > g)).sum()) for g in grid]
-    out["slots"] = slots
-    last = []
-    for i in np.argsort(-t[:, 3])[:5]:
-        last.append({"kind": "dq" if i < ndq else "dkv", "block": int(blk[i]),
-                     "stages": int(stages[i]), "start_us": round(float(t[i, 0]), 1),
-                     "loop_start_us": round(float(t[i, 1]), 1), "end_us": round(float(t[i, 3]), 1)})
-    out["last_to_end"] = last
+    out["backward"] = _timeline_launch(full, [0, 1], ["dq", "dkv"])
+    # the forward's work-groups: the leading rows it stamped (kind 2)
+    warm(lambda: mx.run_flash_lse(q, k, v, o, lse, causal))
+    mx.run_flash_lse(q, k, v, o, lse, causal)
+    torch.cuda.synchronize()
+    full = mx.probe_wg_times().astype(np.int64)
+    kind = full[:, 4] >> 32
+    nwg = len(full) if np.all(kind == 2) else int(np.argmin(kind == 2))
+    out["forward"] = _timeline_launch(full[:nwg], [2], ["fwd"])
     print(json.dumps({"timeline": out}), flush=True)
 
 

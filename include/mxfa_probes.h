@@ -57,13 +57,14 @@ enum {
     MXFA_PROBE_MIX_FWD = 5
 };
 int mxfa_probe_mix(int mix, int waves_per_simd, int iters, float *sink, double *flops, void *stream);
-/* Work-group timeline of the backward. With the timeline build of the code
- * object loaded (mxfa_gfx950_timeline.hsaco beside libmxfa.so, selected with
- * mxfa_set_code_object before the device loads it), thread 0 of every dQ and
- * dK/dV work-group stamps the 100 MHz real-time counter at its start, once its
- * first stage is staged, at the end of its loop and once its stores are
- * acknowledged, and records its kind and block ((kind << 32) | block; kind 0
- * = dQ, query block; 1 = dK/dV, key block) and its stages: eight uint64 per
+/* Work-group timeline of the forward and the backward. With the timeline
+ * build of the code object loaded (mxfa_gfx950_timeline.hsaco beside
+ * libmxfa.so, selected with mxfa_set_code_object before the device loads it),
+ * thread 0 of every forward, dQ and dK/dV work-group stamps the 100 MHz
+ * real-time counter at its start, once its first stage is staged, at the end
+ * of its loop and once its stores are acknowledged, and records its kind and
+ * block ((kind << 32) | block; kind 0 = dQ, query block; 1 = dK/dV, key block;
+ * 2 = forward, query block) and its stages: eight uint64 per
  * linear work-group index (blockIdx.y * gridDim.x + blockIdx.x; the last two
  * zero), for the first 65536 work-groups of each launch, each launch
  * overwriting the last one's. Copies up to `bytes` of them to host `dst` (a

@@ -588,13 +588,14 @@ def probe_mix_tflops(mix: str, waves_per_simd: int = 3, iters: int = 64, reps: i
 
 
 def probe_wg_times():
-    """The per-work-group timeline of the last backward launch (mxfa_probe_wg_times;
-    only with TIMELINE_CODE_OBJECT_PATH loaded): a uint64 numpy array [groups, 8]
-    by linear work-group index. Columns 0-3: 100 MHz real-time counter values
-    (start, first stage staged, end of loop, stores acknowledged); 4: (kind
-    << 32) | block (kind 0 = dQ and its query block, 1 = dK/dV and its key
-    block); 5: its stages; 6-7: zero. Zero rows for indices the launch did
-    not have (or an earlier launch's values)."""
+    """The per-work-group timeline of the last forward or backward launch
+    (mxfa_probe_wg_times; only with TIMELINE_CODE_OBJECT_PATH loaded): a uint64
+    numpy array [groups, 8] by linear work-group index. Columns 0-3: 100 MHz
+    real-time counter values (start, first stage staged, end of loop, stores
+    acknowledged); 4: (kind << 32) | block (kind 0 = dQ and its query block,
+    1 = dK/dV and its key block, 2 = forward and its query block); 5: its
+    stages; 6-7: zero. Zero rows for indices the launch did not have (or an
+    earlier launch's values)."""
     import numpy as np
     lib = load_library()
     avail = ctypes.c_size_t(0)

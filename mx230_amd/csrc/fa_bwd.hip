@@ -107,39 +107,6 @@ extern "C" __device__ unsigned long long mxfa_delta_fallbacks;
 #endif
 constexpr int kFlagRows = 128;  // query rows per flag: one dQ work-group's block
 
-// Timeline build (-DMXFA_WG_TIMELINE: `make timeline`, mxfa_gfx950_timeline.hsaco):
-// thread 0 of every work-group of the dQ and dK/dV bodies stamps the 100 MHz
-// real-time counter at its start (0), once its first stage is staged (1), at
-// the end of its loop (2) and once its stores are acknowledged (3), into
-// mxfa_wg_times[8 g + i] for its linear work-group index g, and records what
-// it ran: (kind << 32) | block at 8 g + 4 (kind 0 = dQ, block = query block;
-// 1 = dK/dV, block = key block) and its stages at 8 g + 5 (read by
-// mxfa_probe_wg_times). In every other build these compile to nothing.
-#if defined(__HIP_DEVICE_COMPILE__) && defined(MXFA_WG_TIMELINE)
-constexpr unsigned kTimelineGroups = 1u << 16;
-extern "C" __device__ unsigned long long mxfa_wg_times[kTimelineGroups * 8];
-__device__ unsigned long long mxfa_wg_times[kTimelineGroups * 8];
-__device__ __forceinline__ void wg_put(int i, unsigned long long v) {
-    const unsigned g = blockIdx.y * gridDim.x + blockIdx.x;
-    if (threadIdx.x == 0 && g < kTimelineGroups) {
-        *reinterpret_cast<volatile unsigned long long *>(mxfa_wg_times + 8 * (size_t)g + i) = v;
-    }
-}
-__device__ __forceinline__ void wg_time(int i) { wg_put(i, __builtin_amdgcn_s_memrealtime()); }
-__device__ __forceinline__ void wg_info(unsigned kind, int block, int stages) {
-    wg_put(4, ((unsigned long long)kind << 32) | (unsigned)block);
-    wg_put(5, (unsigned)stages);
-}
-__device__ __forceinline__ void wg_time_after_stores() {
-    wait_stores();
-    wg_time(3);
-}
-#else
-__device__ __forceinline__ void wg_time(int) {}
-__device__ __forceinline__ void wg_info(unsigned, int, int) {}
-__device__ __forceinline__ void wg_time_after_stores() {}
-#endif
-
 // ---------------------------------------------------------------- wave tiles
 //
 // dQ tiles hold ROWS queries of one wave: Q and -dO (registers), the LSE

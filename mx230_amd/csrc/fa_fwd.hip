@@ -310,6 +310,7 @@ __device__ __forceinline__ void fwd_entry(const Params &p) {
     const T *V = static_cast<const T *>(p.v) + kvoff;
     const int q0 = qb * BQ + wave * 16 * QT;
     const int qpos0 = pos0 + q0;  // position of the wave's first query row
+    wg_time(0);
 
     Frag qf[QT][NC];
 #pragma unroll
@@ -335,11 +336,13 @@ __device__ __forceinline__ void fwd_entry(const Params &p) {
 
     const int kend = CAUSAL ? min(Nk, pos0 + qb * BQ + BQ) : Nk;
     const int nsteps = (kend + BK - 1) / BK;
+    wg_info(2, qb, nsteps);
 
     const RowPlan<Pol> plan(tid);
     stage_kv<Pol>(sK[0], sV[0], K, V, 0, Nk, plan, wave, p.kv_rs);
     wait_stage();
     __syncthreads();
+    wg_time(1);
 
     // Leading stages that no wave masks (all their keys exist and precede the
     // workgroup's first query position) run in pairs with the LDS buffer a
@@ -390,6 +393,7 @@ __device__ __forceinline__ void fwd_entry(const Params &p) {
         __syncthreads();
     }
 
+    wg_time(2);
     T *O = static_cast<T *>(p.o) + b * p.o_bs + h * p.o_hs;
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
@@ -402,6 +406,7 @@ __device__ __forceinline__ void fwd_entry(const Params &p) {
             if (p.lse != nullptr && g == 0) p.lse[(size_t)bh * N + qi] = (m[qt] + fast_log2(ltot)) * kLn2;
         }
     }
+    wg_time_after_stores();
 }
 
 // The code object's forward kernels (fa_kernels.h): policy, causal, waves

@@ -110,6 +110,9 @@ def test_timeline_build():
         mx.init(0)
         got = bwd()
         t = mx.probe_wg_times()
+        mx.run_flash_lse(q, k, v, o, lse, True)
+        torch.cuda.synchronize()
+        tf = mx.probe_wg_times()
     finally:
         mx.shutdown()
         mx.set_code_object(None)
@@ -130,6 +133,16 @@ def test_timeline_build():
     assert np.array_equal(block[ndq:], np.arange(ndq) // (B * H))
     assert np.array_equal(info[:ndq, 1], 2 * (block[:ndq] + 1))
     assert np.array_equal(info[ndq:, 1], N // 64 - 2 * block[ndq:])
+    # the forward (64-query work-groups at this size, heaviest query block
+    # first): kind 2, its query block, one 64-key stage per 64 queries to the
+    # diagonal
+    nfw = B * H * (N // 64)
+    tf = tf[:nfw].astype(np.int64)
+    assert np.all(np.diff(tf[:, :4], axis=1) >= 0)
+    assert np.all(tf[:, 4] >> 32 == 2)
+    fblock = tf[:, 4] & 0xffffffff
+    assert np.array_equal(fblock, N // 64 - 1 - np.arange(nfw) // (B * H))
+    assert np.array_equal(tf[:, 5], fblock + 1)
     span_us = (t[:, 3].max() - t[:, 0].min()) * 0.01
     print(f"\n[timeline] {nwg} work-groups over {span_us:.1f} us", flush=True)
     assert 1.0 < span_us < 10000.0
