@@ -64,9 +64,10 @@ int mxfa_probe_mix(int mix, int waves_per_simd, int iters, float *sink, double *
  * real-time counter at its start, once its first stage is staged, at the end
  * of its loop and once its stores are acknowledged, and records its kind and
  * block ((kind << 32) | block; kind 0 = dQ, query block; 1 = dK/dV, key block;
- * 2 = forward, query block) and its stages: eight uint64 per
- * linear work-group index (blockIdx.y * gridDim.x + blockIdx.x; the last two
- * zero), for the first 65536 work-groups of each launch, each launch
+ * 2 = forward, query block), its stages and where it ran ((XCC_ID << 32) |
+ * HW_ID): eight uint64 per linear work-group index (blockIdx.y * gridDim.x +
+ * blockIdx.x; the last one zero), for the first 65536 work-groups of each
+ * launch, each launch
  * overwriting the last one's. Copies up to `bytes` of them to host `dst` (a
  * synchronous device-to-host copy; dst may be NULL) and writes their size to
  * *avail. MXFA_ERR_UNSUPPORTED with the normal code object. */

@@ -594,8 +594,9 @@ def probe_wg_times():
     real-time counter values (start, first stage staged, end of loop, stores
     acknowledged); 4: (kind << 32) | block (kind 0 = dQ and its query block,
     1 = dK/dV and its key block, 2 = forward and its query block); 5: its
-    stages; 6-7: zero. Zero rows for indices the launch did not have (or an
-    earlier launch's values)."""
+    stages; 6: (XCC_ID << 32) | HW_ID, the XCD and the CU (HW_ID bits 8-11),
+    shader engine (13-15) it ran on; 7: zero. Zero rows for indices the launch
+    did not have (or an earlier launch's values)."""
     import numpy as np
     lib = load_library()
     avail = ctypes.c_size_t(0)

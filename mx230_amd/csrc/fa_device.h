@@ -468,8 +468,9 @@ __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)
 // acknowledged (3), into mxfa_wg_times[8 g + i] for its linear work-group
 // index g, and records what it ran: (kind << 32) | block at 8 g + 4 (kind 0 =
 // dQ, block = query block; 1 = dK/dV, block = key block; 2 = forward, block =
-// query block) and its stages at 8 g + 5 (read by mxfa_probe_wg_times). In
-// every other build these compile to nothing.
+// query block), its stages at 8 g + 5 and where it ran at 8 g + 6 ((XCC_ID
+// << 32) | HW_ID; read by mxfa_probe_wg_times). In every other build these
+// compile to nothing.
 #if defined(__HIP_DEVICE_COMPILE__) && defined(MXFA_WG_TIMELINE)
 constexpr unsigned kTimelineGroups = 1u << 16;
 extern "C" __device__ unsigned long long mxfa_wg_times[kTimelineGroups * 8];
@@ -484,6 +485,10 @@ __device__ __forceinline__ void wg_time(int i) { wg_put(i, __builtin_amdgcn_s_me
 __device__ __forceinline__ void wg_info(unsigned kind, int block, int stages) {
     wg_put(4, ((unsigned long long)kind << 32) | (unsigned)block);
     wg_put(5, (unsigned)stages);
+    // where it runs: the HW_ID register (CU, shader array and engine fields)
+    // and the XCC_ID register (the XCD)
+    wg_put(6, ((unsigned long long)__builtin_amdgcn_s_getreg(20 | (15 << 11)) << 32) |
+                  (unsigned)__builtin_amdgcn_s_getreg(4 | (31 << 11)));
 }
 __device__ __forceinline__ void wg_time_after_stores() {
     wait_stores();
