@@ -96,6 +96,15 @@ def test_split_ragged(causal, n):
     _check(f"split-n{n}", q, k, v, do, causal, True, kvh=1)
 
 
+@pytest.mark.parametrize("hq,n", [(8, 643), (10, 836)], ids=["g4-n643", "g5-n836"])
+def test_split_share_starts_inside_the_diagonal(hq, n):
+    """Shares are runs of a key block's (query head, stage) list: at these
+    shapes some run starts at the second stage of a head, inside the two
+    masked stages at its diagonal (group 5 also splits heads unevenly)."""
+    q, k, v, do = make_inputs(1, hq, 2, n, 64, bf16=True, seeds=(61, 62, 63, 64))
+    _check(f"split-g{hq // 2}-n{n}", q, k, v, do, True, True, kvh=1)
+
+
 def test_split_fp32():
     """The fp32 parity path, 2:1 group, causal."""
     q, k, v, do = make_inputs(1, 4, 2, 300, 64, seeds=(41, 42, 43, 44))

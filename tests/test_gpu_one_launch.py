@@ -147,8 +147,8 @@ def test_one_launch_concurrent_streams(opts):
 
 
 @pytest.mark.parametrize("shape", [(2, 14, 2, 4096, 64), (1, 32, 4, 2048, 64), (1, 32, 4, 2048, 128),
-                                   (1, 8, 2, 300, 64)],
-                         ids=["cfg4", "cfg5-d64", "cfg5-d128", "ragged"])
+                                   (1, 8, 2, 300, 64), (1, 10, 2, 836, 64)],
+                         ids=["cfg4", "cfg5-d64", "cfg5-d128", "ragged", "g5-mid-diagonal"])
 def test_one_launch_with_gqa_split(opts, shape):
     import torch
     import mx230_amd as mx
