@@ -117,19 +117,10 @@ def naive_table():
     import mx230_amd as mx
     dev = torch.device("cuda", 0)
     mx.init(0)
-    stream = torch.cuda.current_stream()
 
     def median_ms(fn):
-        fn()
-        times = []
-        for _ in range(5):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            fn()
-            e1.record(stream)
-            e1.synchronize()
-            times.append(e0.elapsed_time(e1))
-        return sorted(times)[2]
+        # the reference's WARMUP = 1, ITERS = 5 (main.rs:15-16)
+        return mx.time_median_ms(fn, warmup=mx.WARMUP, iters=mx.ITERS)
 
     gen = torch.Generator(device=dev)
     rows = []

@@ -676,6 +676,37 @@ def set_code_object(path: str | None):
     _check("mxfa_set_code_object", load_library().mxfa_set_code_object(path.encode() if path else None))
 
 
+# The reference's benchmark counts (02-flash-attention/src/main.rs:15-16).
+WARMUP = 1
+ITERS = 5
+
+
+def time_median_ms(fn, warmup: int = WARMUP, iters: int = ITERS, stream=None) -> float:
+    """Median time of one invocation of `fn` in milliseconds, as
+    common/src/lib.rs:22-43 (time_median_ms) measures it: `warmup` calls, a
+    synchronisation of the stream, then `iters` calls each bracketed by a pair
+    of HIP events on the stream and waited for; the median is the sorted
+    times' element iters // 2. `fn` enqueues its work on `stream` (default:
+    torch's current stream)."""
+    torch = _torch()
+    if iters < 1:
+        raise ValueError(f"iters must be at least 1 (got {iters})")
+    s = stream if stream is not None else torch.cuda.current_stream()
+    for _ in range(warmup):
+        fn()
+    s.synchronize()
+    times = []
+    for _ in range(iters):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(s)
+        fn()
+        end.record(s)
+        end.synchronize()
+        times.append(start.elapsed_time(end))
+    times.sort()
+    return times[len(times) // 2]
+
+
 def fwd_flops(B, Hq, N, d, causal) -> float:
     """Algorithmic forward flops: 4 N^2 d per (batch, query head), halved if causal."""
     return 4.0 * N * N * d * B * Hq * (0.5 if causal else 1.0)

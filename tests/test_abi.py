@@ -342,3 +342,9 @@ def test_noalloc_rejects_shapes_beyond_its_scratch(lib):
         mx_status("MXFA_ERR_SCRATCH")
     assert lib.mxfa_run_bwd_noalloc(ctypes.byref(big), p, p, p, p, p, p, p, p, p, None, None) == \
         mx_status("MXFA_ERR_NULL")
+
+
+def test_time_median_ms_needs_an_iteration():
+    """mx.time_median_ms rejects iters < 1 before touching a device."""
+    with pytest.raises(ValueError):
+        mx.time_median_ms(lambda: None, warmup=0, iters=0)

@@ -146,3 +146,30 @@ def test_timeline_build():
     span_us = (t[:, 3].max() - t[:, 0].min()) * 0.01
     print(f"\n[timeline] {nwg} work-groups over {span_us:.1f} us", flush=True)
     assert 1.0 < span_us < 10000.0
+
+
+def test_time_median_ms():
+    """mx.time_median_ms, the counterpart of common/src/lib.rs:22-43: the
+    median of per-call event times after the warm-up calls; two backward
+    calls per invocation take about twice as long as one."""
+    import torch
+    import mx230_amd as mx
+    B, H, N, d = 2, 12, 2048, 64
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(9)
+    q, k, v, do = (torch.randn((B, H, N, d), generator=gen, device="cuda").to(torch.bfloat16) for _ in range(4))
+    o, dq, dk, dv = (torch.empty_like(q) for _ in range(4))
+    lse = torch.empty((B, H, N), device="cuda")
+    delta = torch.empty_like(lse)
+    mx.run_flash_lse(q, k, v, o, lse, True)
+
+    def bwd():
+        mx.run_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, True)
+
+    calls = []
+    one = mx.time_median_ms(lambda: (calls.append(1), bwd()), warmup=3, iters=9)
+    assert len(calls) == 3 + 9
+    two = mx.time_median_ms(lambda: (bwd(), bwd()), warmup=3, iters=9)
+    print(f"\n[time_median_ms] one backward {one * 1e3:.1f} us, two {two * 1e3:.1f} us", flush=True)
+    assert 0.0 < one < 10.0
+    assert 1.5 < two / one < 2.3
