@@ -111,9 +111,9 @@ constexpr int kFlagRows = 128;  // query rows per flag: one dQ work-group's bloc
 //
 // dQ tiles hold ROWS queries of one wave: Q and -dO (registers), the LSE
 // offset and Delta of each query, and the dQ accumulators. load() fills them
-// (DELTA: computing Delta = rowsum(dO * O) from O and writing it to p.delta,
-// write-through when PUBLISH), stage() runs one 64-key stage of K and V from
-// LDS, store() writes dQ. delta_fallback() computes Delta of 64 rows on one
+// (DELTA: computing Delta = rowsum(dO * O) from O, which store_delta() writes
+// to p.delta, write-through when PUBLISH), stage() runs one 64-key stage of K
+// and V from LDS, store() writes dQ. delta_fallback() computes Delta of 64 rows on one
 // wave with exactly the arithmetic of load(), so both give the same bits.
 //
 // dK/dV tiles hold ROWS keys of one wave: K and -V (registers) and the dK/dV
@@ -149,46 +149,70 @@ struct DqTile16 {
         return t;
     }
 
-    template <bool DELTA, bool PUBLISH>
+    // The wave's rows: every load is issued first (branch-free), so they are
+    // in flight together. DELTA: Delta = rowsum(dO * O) from O, which
+    // store_delta() writes; otherwise Delta is read from p.delta.
+    template <bool DELTA>
     __device__ __forceinline__ void load(const Params &p, int bh, int q0, int lane) {
         const int g = lane >> 4, l16 = lane & 15;
         const int N = p.N;
-        const T *Q = static_cast<const T *>(p.q) + (size_t)bh * N * D;
-        const T *dO = static_cast<const T *>(p.dout) + (size_t)bh * N * D;
+        const size_t hrow = (size_t)bh * N;
+        const T *Q = static_cast<const T *>(p.q) + hrow * D;
+        const T *dO = static_cast<const T *>(p.dout) + hrow * D;
+        Frag of[DELTA ? QT : 1][NC];
+        float lse[QT];
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
-            const int qi = q0 + 16 * qt + l16;
-            const bool ok = qi < N;
-            Pol::gmem_row_frags(qf[qt], Q + (size_t)qi * D, g, ok);
-            Pol::gmem_row_frags(dof[qt], dO + (size_t)qi * D, g, ok);
+            const int qi = q0 + 16 * qt + l16, qc = min(qi, N - 1);
+            Pol::gmem_row_frags(qf[qt], Q, qi, N, D, g);
+            Pol::gmem_row_frags(dof[qt], dO, qi, N, D, g);
+            if constexpr (DELTA) {
+                Pol::gmem_row_frags(of[qt], static_cast<const T *>(p.o_in) + hrow * D, qi, N, D, g);
+            } else {
+                Dl[qt] = p.delta[hrow + qc];
+            }
+            lse[qt] = p.lse[hrow + qc];
+        }
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+            const bool ok = q0 + 16 * qt + l16 < N;
             if constexpr (DELTA) {
                 // the lane holds 16 of the row's d elements; the 4 lane groups
-                // g = 0..3 together hold the row
-                Frag of[NC];
-                Pol::gmem_row_frags(of, static_cast<const T *>(p.o_in) + (size_t)bh * N * D + (size_t)qi * D, g,
-                                    ok);
-                Dl[qt] = xg_sum(group_part(dof[qt], of));
-                if (ok && g == 0) {
-                    if constexpr (PUBLISH) {
-                        store_wt(p.delta + (size_t)bh * N + qi, __float_as_uint(Dl[qt]));
-                    } else {
-                        p.delta[(size_t)bh * N + qi] = Dl[qt];
-                    }
-                }
+                // g = 0..3 together hold the row (rows past N: zeros, Delta 0)
+                Dl[qt] = xg_sum(group_part(dof[qt], of[qt]));
             } else {
-                Dl[qt] = ok ? p.delta[(size_t)bh * N + qi] : 0.f;
+                Dl[qt] = ok ? Dl[qt] : 0.f;
             }
 #pragma unroll
             for (int kc = 0; kc < NC; ++kc) {
                 if (!Pol::kExactScale) qf[qt][kc] = Pol::scaled(qf[qt][kc], p.scale_log2);
                 dof[qt][kc] = Pol::neg(dof[qt][kc]);
             }
-            nL2[qt] = ok ? p.lse[(size_t)bh * N + qi] * (Pol::kExactScale ? -1.0f / p.scale : -kLog2e) : 0.f;
+            nL2[qt] = ok ? lse[qt] * (Pol::kExactScale ? -1.0f / p.scale : -kLog2e) : 0.f;
         }
 #pragma unroll
         for (int xt = 0; xt < XT; ++xt) {
 #pragma unroll
             for (int qt = 0; qt < QT; ++qt) acc[xt][qt] = zero4();
+        }
+    }
+
+    // Writes the Delta rows load<true>() computed to p.delta; PUBLISH: written
+    // through to memory.
+    template <bool PUBLISH>
+    __device__ __forceinline__ void store_delta(const Params &p, int bh, int q0, int lane) const {
+        const int g = lane >> 4, l16 = lane & 15;
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+            const int qi = q0 + 16 * qt + l16;
+            if (qi < p.N && g == 0) {
+                float *dst = p.delta + (size_t)bh * p.N + qi;
+                if constexpr (PUBLISH) {
+                    store_wt(dst, __float_as_uint(Dl[qt]));
+                } else {
+                    *dst = Dl[qt];
+                }
+            }
         }
     }
 
@@ -314,14 +338,18 @@ struct DkvTile16 {
     f32x4 accK[XT][KT], accV[XT][KT];
     float lmul, xmul;
 
+    // K and V rows under a branch per row (gmem_row_frags_if): the branch-free
+    // form issues the loads together, but measured no faster here (they
+    // overlap the first stage's loads either way) and made the register
+    // allocator spill inside the two-launch dK/dV kernel's stage loops
     __device__ __forceinline__ void load(const Params &p, const T *K, const T *V, int kw0, int lane) {
         const int g = lane >> 4, l16 = lane & 15;
         const int N = p.N;
 #pragma unroll
         for (int kt = 0; kt < KT; ++kt) {
             const int key = kw0 + 16 * kt + l16;
-            Pol::gmem_row_frags(kf[kt], K + (size_t)key * D, g, key < N);
-            Pol::gmem_row_frags(vf[kt], V + (size_t)key * D, g, key < N);
+            Pol::gmem_row_frags_if(kf[kt], K + (size_t)key * D, g, key < N);
+            Pol::gmem_row_frags_if(vf[kt], V + (size_t)key * D, g, key < N);
 #pragma unroll
             for (int kc = 0; kc < NC; ++kc) {
                 if (!Pol::kExactScale) kf[kt][kc] = Pol::scaled(kf[kt][kc], p.scale_log2);
@@ -444,7 +472,8 @@ struct DqSmem {
 // DELTA: compute Delta_i = sum_x dO[i,x] O[i,x] here (O from p.o_in) and write
 // it to p.delta for the dK/dV pass, instead of reading it from there.
 // PUBLISH (with DELTA, in the one-launch backward): Delta is written through
-// to memory and then the block's flag set to p.epoch, before the main loop.
+// to memory once the first stage is staged, and the block's flag set to
+// p.epoch after the first stage, whose wait sees those stores acknowledged.
 template <class Tile, bool CAUSAL, bool DELTA, bool PUBLISH = false>
 __device__ __forceinline__ void dq_body(const Params &p, int bh, int qb, DqSmem<typename Tile::Pol> &sm) {
     using Pol = typename Tile::Pol;
@@ -466,29 +495,33 @@ __device__ __forceinline__ void dq_body(const Params &p, int bh, int qb, DqSmem<
     const int q0 = qb * BQ + wave * Tile::ROWS;
     wg_time(0);
 
+    // the first stage's K/V loads and the tile's loads are in flight together
+    const RowPlan<Pol, NT> plan(tid);
+    stage_kv<Pol, NT>(sK[0], sV[0], K, V, 0, N, plan, wave);
     Tile t;
-    t.template load<DELTA, PUBLISH>(p, bh, q0, lane);
-
-    if constexpr (PUBLISH) {
-        static_assert(DELTA && BQ == kFlagRows, "a published block is one work-group's Delta rows");
-        // every wave's Delta stores acknowledged (written through), then the flag
-        wait_stores();
-        __syncthreads();
-        if (tid == 0) {
-            const int nfb = (N + kFlagRows - 1) / kFlagRows;
-            store_wt(g_delta_flags + (size_t)p.flag_slot * kMaxFlagBlocks + (size_t)bh * nfb + qb, p.epoch);
-        }
-    }
+    t.template load<DELTA>(p, bh, q0, lane);
+    if constexpr (DELTA && !PUBLISH) t.template store_delta<false>(p, bh, q0, lane);
 
     const int kend = CAUSAL ? min(N, qb * BQ + BQ) : N;
     const int nsteps = (kend + BK - 1) / BK;
     wg_info(0, qb, nsteps);
 
-    const RowPlan<Pol, NT> plan(tid);
-    stage_kv<Pol, NT>(sK[0], sV[0], K, V, 0, N, plan, wave);
     wait_stage();
     __syncthreads();
     wg_time(1);
+    // PUBLISH: the Delta stores go out now, and stage 0's wait (every wave's
+    // s_waitcnt, then the barrier) sees them acknowledged before thread 0 sets
+    // the flag; so no wave waits for a write-through on its own
+    static_assert(!PUBLISH || (DELTA && BQ == kFlagRows), "a published block is one work-group's Delta rows");
+    if constexpr (PUBLISH) t.template store_delta<true>(p, bh, q0, lane);
+    auto publish = [&](int st) __attribute__((always_inline)) {
+        if constexpr (PUBLISH) {
+            if (st == 0 && tid == 0) {
+                const int nfb = (N + kFlagRows - 1) / kFlagRows;
+                store_wt(g_delta_flags + (size_t)p.flag_slot * kMaxFlagBlocks + (size_t)bh * nfb + qb, p.epoch);
+            }
+        }
+    };
 
     // Every stage but the last kTail is unmasked for every wave (causal: its
     // keys all precede the workgroup's first query; otherwise: only the last
@@ -502,6 +535,7 @@ __device__ __forceinline__ void dq_body(const Params &p, int bh, int qb, DqSmem<
         t.template stage<CAUSAL, false, kPrio>(sK[B], sV[B], st * BK, q0, N, lane, p.scale_log2);
         wait_stage();
         __syncthreads();
+        publish(st);
     };
     constexpr int kTail = BQ / BK > 2 ? BQ / BK : 2;
     const int nmain = nsteps - min(nsteps, kTail);
@@ -522,6 +556,7 @@ __device__ __forceinline__ void dq_body(const Params &p, int bh, int qb, DqSmem<
         }
         wait_stage();
         __syncthreads();
+        publish(st);
     }
     wg_time(2);
     t.store(p, bh, q0, lane);
@@ -582,9 +617,6 @@ __device__ __forceinline__ void dkv_body(const Params &p, const DkvWork wk, DkvS
     const size_t kvoff = (size_t)bkv * N * D;
     const int kw0 = kb * BKV + wave * Tile::ROWS;  // first key of this wave
     wg_time(0);
-
-    Tile t;
-    t.load(p, static_cast<const T *>(p.k) + kvoff, static_cast<const T *>(p.v) + kvoff, kw0, lane);
 
     const int qstart = CAUSAL ? kb * BKV : 0;
     const int nqs = (N - qstart + BQ - 1) / BQ;  // stages per query head
@@ -653,7 +685,11 @@ __device__ __forceinline__ void dkv_body(const Params &p, const DkvWork wk, DkvS
             }
         }
     };
+    // the first stage's loads (and its flag poll) go out before the tile's
+    // own, so both are in flight together
     if (nsteps > 0) issue(0);
+    Tile t;
+    t.load(p, static_cast<const T *>(p.k) + kvoff, static_cast<const T *>(p.v) + kvoff, kw0, lane);
     wait_stage();
     __syncthreads();
     wg_time(1);

@@ -240,7 +240,8 @@ struct PolBF16 {
 #pragma unroll
         for (int c = 0; c < NC; ++c) f[c] = *reinterpret_cast<const Frag *>(base + chunk_off(n, 4 * c + g));
     }
-    __device__ static __forceinline__ void gmem_row_frags(Frag (&f)[NC], const T *row, int g, bool valid) {
+    // the row's fragments if valid, else zeros (the loads under a branch)
+    __device__ static __forceinline__ void gmem_row_frags_if(Frag (&f)[NC], const T *row, int g, bool valid) {
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             if (valid) {
@@ -248,6 +249,19 @@ struct PolBF16 {
             } else {
                 f[c] = Frag{};
             }
+        }
+    }
+    // row i of n rows (row stride rs elements), zeros for i >= n (n >= 1): the
+    // loads read row min(i, n - 1), so they take no branch and a tile's loads
+    // issue together
+    __device__ static __forceinline__ void gmem_row_frags(Frag (&f)[NC], const T *rows, int i, int n, size_t rs,
+                                                          int g) {
+        const bool valid = i < n;
+        const T *row = rows + (size_t)(valid ? i : n - 1) * rs;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const Frag v = *reinterpret_cast<const Frag *>(row + 32 * c + 8 * g);
+            f[c] = valid ? v : Frag{};
         }
     }
     // sum of the element products, in fp32
@@ -352,15 +366,30 @@ struct PolF32 {
             f[4 * i + 3] = v.w;
         }
     }
-    __device__ static __forceinline__ void gmem_row_frags(Frag (&f)[NC], const T *row, int g, bool valid) {
+    __device__ static __forceinline__ void gmem_row_frags_if(Frag (&f)[NC], const T *row, int g, bool valid) {
 #pragma unroll
-        for (int i = 0; i < NC / 4; ++i) {
+        for (int j = 0; j < NC / 4; ++j) {
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (valid) v = *reinterpret_cast<const float4 *>(row + NC * g + 4 * i);
-            f[4 * i + 0] = v.x;
-            f[4 * i + 1] = v.y;
-            f[4 * i + 2] = v.z;
-            f[4 * i + 3] = v.w;
+            if (valid) v = *reinterpret_cast<const float4 *>(row + NC * g + 4 * j);
+            f[4 * j + 0] = v.x;
+            f[4 * j + 1] = v.y;
+            f[4 * j + 2] = v.z;
+            f[4 * j + 3] = v.w;
+        }
+    }
+    // row i of n rows (row stride rs elements), zeros for i >= n (n >= 1),
+    // branch-free as in PolBF16
+    __device__ static __forceinline__ void gmem_row_frags(Frag (&f)[NC], const T *rows, int i, int n, size_t rs,
+                                                          int g) {
+        const bool valid = i < n;
+        const T *row = rows + (size_t)(valid ? i : n - 1) * rs;
+#pragma unroll
+        for (int j = 0; j < NC / 4; ++j) {
+            const float4 v = *reinterpret_cast<const float4 *>(row + NC * g + 4 * j);
+            f[4 * j + 0] = valid ? v.x : 0.f;
+            f[4 * j + 1] = valid ? v.y : 0.f;
+            f[4 * j + 2] = valid ? v.z : 0.f;
+            f[4 * j + 3] = valid ? v.w : 0.f;
         }
     }
     __device__ static __forceinline__ Frag neg(Frag f) { return -f; }

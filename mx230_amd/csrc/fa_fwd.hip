@@ -314,11 +314,11 @@ __device__ __forceinline__ void fwd_entry(const Params &p) {
 
     Frag qf[QT][NC];
 #pragma unroll
+    for (int qt = 0; qt < QT; ++qt) Pol::gmem_row_frags(qf[qt], Q, q0 + 16 * qt + l16, N, p.q_rs, g);
+    // fp32: Q scale log2(e), so the scores come out of the MFMAs in log2
+    // units; bf16 keeps Q exact and scales the fp32 scores instead
+#pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-        const int qi = q0 + 16 * qt + l16;
-        Pol::gmem_row_frags(qf[qt], Q + (size_t)qi * p.q_rs, g, qi < N);
-        // fp32: Q scale log2(e), so the scores come out of the MFMAs in log2
-        // units; bf16 keeps Q exact and scales the fp32 scores instead
 #pragma unroll
         for (int kc = 0; kc < NC; ++kc) {
             if (!Pol::kExactScale) qf[qt][kc] = Pol::scaled(qf[qt][kc], p.scale_log2);
