@@ -315,7 +315,13 @@ struct DqTile16 {
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
             const int qi = q0 + 16 * qt + l16;
-            if (qi < N) {
+            if constexpr (std::is_same<T, u16>::value) {
+                // bf16 rows, 16 bytes per lane
+                const size_t row = (size_t)min(qi, N - 1) * D;
+#pragma unroll
+                for (int xt = 0; xt < XT; xt += 2)
+                    store8_pair_bf16(dQ + row, 16 * xt, g, acc[xt][qt], acc[xt + 1][qt], -p.scale, qi < N);
+            } else if (qi < N) {
 #pragma unroll
                 for (int xt = 0; xt < XT; ++xt)
                     store4<T>(dQ + (size_t)qi * D + 16 * xt + 4 * g, acc[xt][qt], -p.scale);
@@ -448,7 +454,15 @@ struct DkvTile16 {
 #pragma unroll
         for (int kt = 0; kt < KT; ++kt) {
             const int key = kw0 + 16 * kt + l16;
-            if (key < N) {
+            if constexpr (std::is_same<U, u16>::value) {
+                // bf16 rows, 16 bytes per lane
+                const size_t row = (size_t)min(key, N - 1) * D;
+#pragma unroll
+                for (int xt = 0; xt < XT; xt += 2) {
+                    store8_pair_bf16(dK + row, 16 * xt, g, accK[xt][kt], accK[xt + 1][kt], kmul, key < N);
+                    store8_pair_bf16(dV + row, 16 * xt, g, accV[xt][kt], accV[xt + 1][kt], 1.0f, key < N);
+                }
+            } else if (key < N) {
 #pragma unroll
                 for (int xt = 0; xt < XT; ++xt) {
                     store4<U>(dK + (size_t)key * D + 16 * xt + 4 * g, accK[xt][kt], kmul);

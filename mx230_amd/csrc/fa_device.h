@@ -699,4 +699,28 @@ __device__ __forceinline__ void store4<u16>(u16 *dst, f32x4 v, float mul) {
     *reinterpret_cast<uint2 *>(dst) = make_uint2(a, b);
 }
 
+// Two C tiles of one output row in bf16, 16 bytes per lane: in the 16x16 C
+// layout a holds elements x0 + 4g .. +3 of the lane's row and b elements
+// x0 + 16 + 4g .. +3 (g = lane / 16). Lanes of lane groups g and g + 1 (g
+// even; the same row) swap halves with v_permlane16_swap, so a lane of an even
+// group writes elements x0 + 4g .. +7 and one of an odd group x0 + 12 + 4g ..
+// +7: a store instruction covers 64 bytes of each of its 16 rows instead of
+// 32. Every lane takes part in the swap; only the store is predicated (both
+// lanes of a pair have the same row, so the same `valid`).
+__device__ __forceinline__ void store8_pair_bf16(u16 *row, int x0, int g, f32x4 a, f32x4 b, float mul,
+                                                 bool valid) {
+    const uint32_t a0 = (uint32_t)to_bf16_bits(a[0] * mul) | ((uint32_t)to_bf16_bits(a[1] * mul) << 16);
+    const uint32_t a1 = (uint32_t)to_bf16_bits(a[2] * mul) | ((uint32_t)to_bf16_bits(a[3] * mul) << 16);
+    const uint32_t b0 = (uint32_t)to_bf16_bits(b[0] * mul) | ((uint32_t)to_bf16_bits(b[1] * mul) << 16);
+    const uint32_t b1 = (uint32_t)to_bf16_bits(b[2] * mul) | ((uint32_t)to_bf16_bits(b[3] * mul) << 16);
+    // even groups keep their own a and take the odd partner's; odd groups
+    // take the even partner's b and keep their own
+    const auto s0 = __builtin_amdgcn_permlane16_swap(a0, b0, false, false);
+    const auto s1 = __builtin_amdgcn_permlane16_swap(a1, b1, false, false);
+    if (valid) {
+        const int off = x0 + ((g & 1) ? 12 + 4 * g : 4 * g);
+        *reinterpret_cast<uint4 *>(row + off) = make_uint4(s0[0], s1[0], s0[1], s1[1]);
+    }
+}
+
 }  // namespace mxfa

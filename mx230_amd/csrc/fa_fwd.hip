@@ -400,11 +400,17 @@ __device__ __forceinline__ void fwd_entry(const Params &p) {
         const int qi = q0 + 16 * qt + l16;
         const float ltot = xg_sum(lsum[qt]);
         const float inv = 1.0f / ltot;
-        if (qi < N) {
+        if constexpr (std::is_same<T, u16>::value) {
+            // bf16 rows, 16 bytes per lane (rows start on 16-byte boundaries)
+            T *row = O + (size_t)min(qi, N - 1) * p.o_rs;
+#pragma unroll
+            for (int xt = 0; xt < XT; xt += 2)
+                store8_pair_bf16(row, 16 * xt, g, acc[xt][qt], acc[xt + 1][qt], inv, qi < N);
+        } else if (qi < N) {
 #pragma unroll
             for (int xt = 0; xt < XT; ++xt) store4<T>(O + (size_t)qi * p.o_rs + 16 * xt + 4 * g, acc[xt][qt], inv);
-            if (p.lse != nullptr && g == 0) p.lse[(size_t)bh * N + qi] = (m[qt] + fast_log2(ltot)) * kLn2;
         }
+        if (qi < N && p.lse != nullptr && g == 0) p.lse[(size_t)bh * N + qi] = (m[qt] + fast_log2(ltot)) * kLn2;
     }
     wg_time_after_stores();
 }
