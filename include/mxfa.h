@@ -310,6 +310,21 @@ int mxfa_check_prefill(const mxfa_prefill_shape *shape);
 int mxfa_run_prefill(const mxfa_prefill_shape *shape, const void *q, const void *kcache, const void *vcache,
                      void *out, void *stream);
 
+/* The prefill over a paged KV cache. Replaces `attn_prefill_paged`
+ * (03-llm-engine/kernels/llm.cu:3827-3836, body :3674-3804 with
+ * PAGED = true; launched by gpu.rs:3270-3289): the same as mxfa_run_prefill,
+ * except that logical cache position t sits in cache row
+ * block_table[t / block_size] * block_size + t % block_size (kv_row<true>,
+ * llm.cu:959-963), rows kv_stride elements apart from kcache / vcache.
+ * block_table: int32 on the device, entries for positions 0 .. pos0 + n_tok - 1,
+ * each a physical block inside the caches (not checked: a bad entry reads
+ * outside them, as in the reference). block_size: a power of two (the
+ * reference engine's KV_BLOCK is 16, gpu.rs:209); others give
+ * MXFA_ERR_UNSUPPORTED. Outputs are bitwise those of mxfa_run_prefill over the
+ * gathered, contiguous cache. */
+int mxfa_run_prefill_paged(const mxfa_prefill_shape *shape, const void *q, const void *kcache, const void *vcache,
+                           void *out, const int *block_table, int block_size, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

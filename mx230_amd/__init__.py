@@ -55,6 +55,7 @@ EXPORTS = (
     "mxfa_run_bwd_dkv", "mxfa_run_bwd_flash", "mxfa_run_bwd_dq_delta", "mxfa_run_bwd", "mxfa_bwd_one_launch", "mxfa_bwd_workspace_bytes",
     "mxfa_run_bwd_dkv_ws", "mxfa_run_bwd_ws", "mxfa_run_bwd_naive",
     "mxfa_naive_scratch_bytes", "mxfa_run_naive_fwd", "mxfa_check_prefill", "mxfa_run_prefill",
+    "mxfa_run_prefill_paged",
     "mxfa_set_bwd_options", "mxfa_get_bwd_options", "mxfa_bwd_delta_fallbacks",
     "mxfa_run_bwd_noalloc", "mxfa_bwd_noalloc_scratch_bytes",
 )
@@ -144,6 +145,7 @@ def load_library(path: str | None = None):
     pp = ctypes.POINTER(MxfaPrefillShape)
     lib.mxfa_check_prefill.argtypes = [pp]
     lib.mxfa_run_prefill.argtypes = [pp, vp, vp, vp, vp, vp]
+    lib.mxfa_run_prefill_paged.argtypes = [pp, vp, vp, vp, vp, vp, ctypes.c_int, vp]
     lib.mxfa_probe_sink_len.argtypes = []
     lib.mxfa_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_int, fp, ctypes.POINTER(ctypes.c_double), vp]
     lib.mxfa_probe_mfma32.argtypes = [ctypes.c_int, fp, ctypes.POINTER(ctypes.c_double), vp]
@@ -500,6 +502,44 @@ def run_prefill(q, kcache, vcache, out, pos0: int, n_head: int, n_kv_head: int, 
     sh = MxfaPrefillShape(n_tok, n_head, n_kv_head, head_dim, pos0, qs, ks, os_,
                           MXFA_BF16 if q.dtype == torch.bfloat16 else MXFA_F32, scale)
     _check("mxfa_run_prefill", load_library().mxfa_run_prefill(ctypes.byref(sh), qp, kp, vp, op, _stream(stream)))
+
+
+def run_prefill_paged(q, kcache, vcache, out, block_table, block_size: int, pos0: int, n_head: int,
+                      n_kv_head: int, head_dim: int = 64, scale: float = 0.0, stream=None):
+    """mxfa_run_prefill_paged, run_prefill over a paged KV cache
+    (attn_prefill_paged, 03-llm-engine/kernels/llm.cu:3827-3836): logical
+    position t sits in cache row block_table[t // block_size] * block_size +
+    t % block_size (kv_row<true>, llm.cu:959-963).
+
+    kcache, vcache: [pool rows, >= n_kv_head*head_dim], same row stride, the
+    pool holding every block the table names; block_table: int32 device tensor
+    with at least ceil((pos0 + n_tok) / block_size) entries; block_size: a power
+    of two. The rest as run_prefill; the outputs equal run_prefill's over the
+    gathered cache bit for bit."""
+    torch = _torch()
+    if q.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"q: dtype {q.dtype}; bf16 or float32 expected")
+    n_tok = q.shape[0] if q.dim() == 2 else -1
+    qp, qs = _rows(q, "q", q.dtype, 1, n_head * head_dim)
+    kp, ks = _rows(kcache, "kcache", q.dtype, 1, n_kv_head * head_dim)
+    vp, vs = _rows(vcache, "vcache", q.dtype, 1, n_kv_head * head_dim)
+    if ks != vs:
+        raise ValueError(f"kcache and vcache must share a row stride ({ks} != {vs})")
+    op, os_ = _rows(out, "out", q.dtype, n_tok, n_head * head_dim)
+    if not isinstance(block_table, torch.Tensor) or block_table.device.type != "cuda" or \
+            block_table.dtype != torch.int32 or block_table.dim() != 1 or block_table.stride(0) != 1:
+        raise ValueError("block_table: expected a contiguous 1-D int32 device tensor")
+    if block_size < 1:
+        raise ValueError(f"block_size {block_size}: must be positive")
+    need = -(-(pos0 + n_tok) // block_size)
+    if block_table.numel() < need:
+        raise ValueError(f"block_table: {block_table.numel()} entries, positions 0..{pos0 + n_tok - 1} need {need}")
+    sh = MxfaPrefillShape(n_tok, n_head, n_kv_head, head_dim, pos0, qs, ks, os_,
+                          MXFA_BF16 if q.dtype == torch.bfloat16 else MXFA_F32, scale)
+    _check("mxfa_run_prefill_paged",
+           load_library().mxfa_run_prefill_paged(ctypes.byref(sh), qp, kp, vp, op,
+                                                 ctypes.c_void_p(block_table.data_ptr()), int(block_size),
+                                                 _stream(stream)))
 
 
 # ------------------------------------------------------------ conveniences --

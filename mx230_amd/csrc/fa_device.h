@@ -45,6 +45,12 @@ struct Params {
     // kernels assume it.
     long long q_bs, q_hs, kv_bs, kv_hs, o_bs, o_hs;
     int q_rs, kv_rs, o_rs, Nk, pos0;
+    // Paged K/V (the prefill over a block-table cache): with block_table set,
+    // key row t of K and V is cache row (block_table[t >> bs_shift] <<
+    // bs_shift) + (t & (2^bs_shift - 1)), counted in rows of kv_rs elements
+    // from the K/V base of the head; null: cache row t.
+    const int *block_table;
+    int bs_shift;
     // dK/dV pass with dkv_split > 1: the group's query heads' stages of a
     // key block (group x its stages per head, in head order) are split into
     // dkv_block_shares(...) contiguous runs, one work-group each; share s
@@ -631,6 +637,42 @@ __device__ __forceinline__ void stage_kv(typename Pol::T *sk, typename Pol::T *s
     stage_rows<Pol, NT>(sk, K + (size_t)k0 * row_stride, N - k0, pl, wave, row_stride);
     stage_rows<Pol, NT>(sv, V + (size_t)k0 * row_stride, N - k0, pl, wave, row_stride);
 }
+
+// A paged K/V stage (Params::block_table): per staging load of the thread,
+// the block-table entry of its row in the next stage to be staged. fetch()
+// loads them for the stage at k0 (rows past N take row N - 1, as stage_rows
+// does); stage() issues that stage's loads from them. A caller fetches one
+// stage ahead of the loads, so the table loads complete within the stage
+// before and the staging loads never wait for them.
+template <class Pol, int NT = 256>
+struct PagedRows {
+    static constexpr int NK = RowPlan<Pol, NT>::NK;
+    int blk[NK];
+
+    __device__ __forceinline__ void fetch(const int *bt, int shift, int k0, int N, const RowPlan<Pol, NT> &pl) {
+#pragma unroll
+        for (int k = 0; k < NK; ++k) {
+            const int t = min(k0 + (int)(pl.rc[k] & 255u), N - 1);
+            blk[k] = bt[t >> shift];
+        }
+    }
+    // rows k0 .. k0 + Pol::ROWS - 1 of K and V (cache rows row_stride
+    // elements apart) into the LDS tiles, as stage_kv does for a contiguous cache
+    __device__ __forceinline__ void stage(typename Pol::T *sk, typename Pol::T *sv, const typename Pol::T *K,
+                                          const typename Pol::T *V, int k0, int N, int shift,
+                                          const RowPlan<Pol, NT> &pl, int wave, int row_stride) const {
+        const uint32_t bk = lds_addr(sk) + wave * 64 * 16, bv = lds_addr(sv) + wave * 64 * 16;
+        const int mask = (1 << shift) - 1;
+#pragma unroll
+        for (int k = 0; k < NK; ++k) {
+            const int t = min(k0 + (int)(pl.rc[k] & 255u), N - 1);
+            const size_t off = (((size_t)blk[k] << shift) + (size_t)(t & mask)) * (size_t)row_stride +
+                               (pl.rc[k] >> 8) / sizeof(typename Pol::T);
+            lds_dma16(bk + k * NT * 16, K + off);
+            lds_dma16(bv + k * NT * 16, V + off);
+        }
+    }
+};
 
 // Read by lanes past the end of a staged vector (see stage_vec64). Device
 // variables and kernels are defined in the code object only (the device

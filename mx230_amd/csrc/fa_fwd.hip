@@ -280,8 +280,9 @@ __device__ __forceinline__ void fwd_stage_lazy(f32x4 (&acc)[Pol::D / 16][QT], fl
 
 // One work-group of the forward, grid (B Hq, query blocks). QT: 16-query
 // tiles per wave (the work-group takes 64 QT queries); the kernels are
-// compiled for a number of waves per SIMD (the names' w*).
-template <class Pol, bool CAUSAL, int QT>
+// compiled for a number of waves per SIMD (the names' w*). PAGED: K/V rows
+// through Params::block_table (the kernels named *_pg).
+template <class Pol, bool CAUSAL, int QT, bool PAGED = false>
 __device__ __forceinline__ void fwd_entry(const Params &p) {
     using T = typename Pol::T;
     using Frag = typename Pol::Frag;
@@ -339,7 +340,19 @@ __device__ __forceinline__ void fwd_entry(const Params &p) {
     wg_info(2, qb, nsteps);
 
     const RowPlan<Pol> plan(tid);
-    stage_kv<Pol>(sK[0], sV[0], K, V, 0, Nk, plan, wave, p.kv_rs);
+    // PAGED: the table entries of stage 0 now, then each stage fetches those
+    // of the stage after the one it stages
+    PagedRows<Pol> paged;
+    auto stage_next = [&](T *sk, T *sv, int k0) __attribute__((always_inline)) {
+        if constexpr (PAGED) {
+            paged.stage(sk, sv, K, V, k0, Nk, p.bs_shift, plan, wave, p.kv_rs);
+            if (k0 + BK < Nk) paged.fetch(p.block_table, p.bs_shift, k0 + BK, Nk, plan);
+        } else {
+            stage_kv<Pol>(sk, sv, K, V, k0, Nk, plan, wave, p.kv_rs);
+        }
+    };
+    if constexpr (PAGED) paged.fetch(p.block_table, p.bs_shift, 0, Nk, plan);
+    stage_next(sK[0], sV[0], 0);
     wait_stage();
     __syncthreads();
     wg_time(1);
@@ -352,7 +365,7 @@ __device__ __forceinline__ void fwd_entry(const Params &p) {
     // starts at -inf); later ones the lazy-rescaling body.
     auto main_stage = [&](auto buf, auto first, int st) __attribute__((always_inline)) {
         constexpr int B = decltype(buf)::value;
-        if (st + 1 < nsteps) stage_kv<Pol>(sK[B ^ 1], sV[B ^ 1], K, V, (st + 1) * BK, Nk, plan, wave, p.kv_rs);
+        if (st + 1 < nsteps) stage_next(sK[B ^ 1], sV[B ^ 1], (st + 1) * BK);
         if constexpr (decltype(first)::value) {
             fwd_stage<Pol, QT, CAUSAL, false, kPrio>(acc, m, lsum, qf, sK[B], sV[B], st * BK, qpos0, Nk, g, l16,
                                                      p.scale_log2);
@@ -377,7 +390,7 @@ __device__ __forceinline__ void fwd_entry(const Params &p) {
     // one masked body each for the first stage and the later ones
     for (; st < nsteps; ++st) {
         const int cur = st & 1;
-        if (st + 1 < nsteps) stage_kv<Pol>(sK[cur ^ 1], sV[cur ^ 1], K, V, (st + 1) * BK, Nk, plan, wave, p.kv_rs);
+        if (st + 1 < nsteps) stage_next(sK[cur ^ 1], sV[cur ^ 1], (st + 1) * BK);
         const int k0 = st * BK;
         // a wave whose queries all precede the stage's keys has nothing to do
         if (!CAUSAL || k0 <= qpos0 + 16 * QT - 1) {
@@ -420,6 +433,8 @@ __device__ __forceinline__ void fwd_entry(const Params &p) {
 #if defined(__HIP_DEVICE_COMPILE__)
 #define MXFA_FWD(NAME, POL, CAUSAL, WPS, QT)                                                            \
     extern "C" __global__ __launch_bounds__(256, WPS) void NAME(Params p) { fwd_entry<POL, CAUSAL, QT>(p); }
+#define MXFA_FWD_PG(NAME, POL, WPS, QT)                                                                 \
+    extern "C" __global__ __launch_bounds__(256, WPS) void NAME(Params p) { fwd_entry<POL, true, QT, true>(p); }
 MXFA_FWD(mxfa_fwd_b64_c_w3_q2, PolBF16<64>, true, 3, 2)
 MXFA_FWD(mxfa_fwd_b64_c_w2_q2, PolBF16<64>, true, 2, 2)
 MXFA_FWD(mxfa_fwd_b64_c_w3_q1, PolBF16<64>, true, 3, 1)
@@ -430,20 +445,33 @@ MXFA_FWD(mxfa_fwd_b128_c_w2_q1, PolBF16<128>, true, 2, 1)
 MXFA_FWD(mxfa_fwd_b128_n_w2_q2, PolBF16<128>, false, 2, 2)
 MXFA_FWD(mxfa_fwd_f64_c_w1_q2, PolF32<64>, true, 1, 2)
 MXFA_FWD(mxfa_fwd_f64_n_w1_q2, PolF32<64>, false, 1, 2)
+// the prefill over a paged cache (causal, as the prefill always is)
+// (the table entries take registers: the three-wave 128-query d = 64 and the
+// 128-query d = 128 forms would spill in their loops, so paged launches use
+// two waves at d = 64 and 64-query work-groups at d = 128)
+MXFA_FWD_PG(mxfa_fwd_b64_c_w2_q2_pg, PolBF16<64>, 2, 2)
+MXFA_FWD_PG(mxfa_fwd_b64_c_w3_q1_pg, PolBF16<64>, 3, 1)
+MXFA_FWD_PG(mxfa_fwd_b128_c_w2_q1_pg, PolBF16<128>, 2, 1)
+MXFA_FWD_PG(mxfa_fwd_f64_c_w1_q2_pg, PolF32<64>, 1, 2)
 #undef MXFA_FWD
+#undef MXFA_FWD_PG
 #endif
 
 // The kernel of (policy, causal) compiled for `wps` waves per SIMD with `qt`
-// query tiles per wave (one of the list above).
+// query tiles per wave (one of the list above); paged: its *_pg form (causal
+// kernels only).
 template <class Pol, bool CAUSAL>
-static KernelId fwd_kernel_id(int wps, int qt) {
+static KernelId fwd_kernel_id(int wps, int qt, bool paged) {
     if constexpr (Pol::kExactScale && Pol::D == 64) {
+        if (CAUSAL && paged) return qt == 1 ? k_mxfa_fwd_b64_c_w3_q1_pg : k_mxfa_fwd_b64_c_w2_q2_pg;
         if (CAUSAL) return qt == 1 ? k_mxfa_fwd_b64_c_w3_q1 : wps == 3 ? k_mxfa_fwd_b64_c_w3_q2 : k_mxfa_fwd_b64_c_w2_q2;
         return qt == 1 ? k_mxfa_fwd_b64_n_w3_q1 : k_mxfa_fwd_b64_n_w2_q2;
     } else if constexpr (Pol::kExactScale) {
+        if (CAUSAL && paged) return k_mxfa_fwd_b128_c_w2_q1_pg;
         if (CAUSAL) return qt == 1 ? k_mxfa_fwd_b128_c_w2_q1 : k_mxfa_fwd_b128_c_w2_q2;
         return k_mxfa_fwd_b128_n_w2_q2;
     } else {
+        if (CAUSAL && paged) return k_mxfa_fwd_f64_c_w1_q2_pg;
         return CAUSAL ? k_mxfa_fwd_f64_c_w1_q2 : k_mxfa_fwd_f64_n_w1_q2;
     }
 }
@@ -454,11 +482,12 @@ static hipError_t launch_fwd_qt(Params p, hipStream_t stream) {
     constexpr int kHi = Pol::kWavesFwdCausal;
     int wps = QT == 1 ? kHi : Pol::kWaves;
     if constexpr (CAUSAL && kHi > Pol::kWaves && QT > 1) {
-        // enough causal work-groups to fill kHi per CU (256 CUs)
-        if ((long long)grid.x * grid.y >= 256LL * kHi) wps = kHi;
+        // enough causal work-groups to fill kHi per CU (256 CUs); not paged
+        if ((long long)grid.x * grid.y >= 256LL * kHi && p.block_table == nullptr) wps = kHi;
     }
     void *args[] = {&p};
-    return launch_kernel(fwd_kernel_id<Pol, CAUSAL>(wps, QT), grid, dim3(256), args, stream);
+    return launch_kernel(fwd_kernel_id<Pol, CAUSAL>(wps, QT, p.block_table != nullptr), grid, dim3(256), args,
+                         stream);
 }
 
 // bf16 launches whose 128-query work-groups would not fill every resident
@@ -475,12 +504,14 @@ template <class Pol, bool CAUSAL>
 static hipError_t launch_fwd_t(const Params &p, hipStream_t stream) {
     if constexpr (Pol::kExactScale && (CAUSAL || Pol::D == 64)) {
         const long long wg = (long long)p.B * p.Hq * ((p.N + 127) / 128);
-        if (wg < kFwdSmallGrid) return launch_fwd_qt<Pol, CAUSAL, 1>(p, stream);
+        if (wg < kFwdSmallGrid || (Pol::D == 128 && p.block_table != nullptr))
+            return launch_fwd_qt<Pol, CAUSAL, 1>(p, stream);
     }
     return launch_fwd_qt<Pol, CAUSAL, 2>(p, stream);
 }
 
 hipError_t launch_fwd(const Params &p, int dtype_bf16, int d, int causal, hipStream_t stream) {
+    if (p.block_table != nullptr && !causal) return hipErrorInvalidValue;  // paged kernels are causal
 #define MXFA_FWD(POL, DD)                                                            \
     if (d == DD) return causal ? launch_fwd_t<POL<DD>, true>(p, stream)            \
                                : launch_fwd_t<POL<DD>, false>(p, stream);

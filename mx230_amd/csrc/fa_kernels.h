@@ -6,7 +6,8 @@
 // hipModuleGetFunction when it loads the code object; a name missing from
 // the code object fails that load. Naming: pass, dtype and head dim (b64 =
 // bf16 d = 64, b128, f64 = fp32 d = 64), c / n = causal / not, then the
-// variant (waves per SIMD w*, query tiles per wave q*, d = computes Delta).
+// variant (waves per SIMD w*, query tiles per wave q*, d = computes Delta,
+// pg = K/V through a block table).
 #pragma once
 
 #define MXFA_KERNEL_LIST(X)                                                                   \
@@ -15,6 +16,8 @@
     X(mxfa_fwd_b64_n_w2_q2) X(mxfa_fwd_b64_n_w3_q1)                                           \
     X(mxfa_fwd_b128_c_w2_q2) X(mxfa_fwd_b128_c_w2_q1) X(mxfa_fwd_b128_n_w2_q2)                \
     X(mxfa_fwd_f64_c_w1_q2) X(mxfa_fwd_f64_n_w1_q2)                                           \
+    X(mxfa_fwd_b64_c_w2_q2_pg) X(mxfa_fwd_b64_c_w3_q1_pg) X(mxfa_fwd_b128_c_w2_q1_pg)          \
+    X(mxfa_fwd_f64_c_w1_q2_pg)                                                                \
     /* backward (fa_bwd.hip) */                                                               \
     X(mxfa_preprocess_b64) X(mxfa_preprocess_b128) X(mxfa_preprocess_f64)                     \
     X(mxfa_dq_b64_c) X(mxfa_dq_b64_c_d) X(mxfa_dq_b64_n) X(mxfa_dq_b64_n_d)                   \

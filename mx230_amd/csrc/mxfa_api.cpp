@@ -57,6 +57,8 @@ Params make_params(const mxfa_shape *s) {
     p.kv_bs = nd * s->Hkv;
     p.Nk = s->N;
     p.pos0 = 0;
+    p.block_table = nullptr;  // contiguous K/V
+    p.bs_shift = 0;
     p.dkv_ws = nullptr;
     p.dkv_split = p.dkv_min_shares = 1;
     p.dkv_share_stages = 1 << 30;
@@ -399,12 +401,10 @@ int mxfa_check_prefill(const mxfa_prefill_shape *s) {
     return MXFA_OK;
 }
 
-int mxfa_run_prefill(const mxfa_prefill_shape *s, const void *q, const void *kcache, const void *vcache, void *out,
-                     void *stream) {
-    int rc = mxfa_check_prefill(s);
-    if (rc != MXFA_OK) return rc;
-    rc = check_ptrs({q, kcache, vcache, out});
-    if (rc != MXFA_OK) return rc;
+namespace {
+// The forward's parameters for a prefill shape (checked by the caller).
+Params prefill_params(const mxfa_prefill_shape *s, const void *q, const void *kcache, const void *vcache,
+                      void *out) {
     mxfa_shape sh{1, s->n_head, s->n_kv_head, s->n_tok, s->head_dim, 1, s->dtype, s->scale};
     Params p = make_params(&sh);
     p.q = q;
@@ -420,6 +420,33 @@ int mxfa_run_prefill(const mxfa_prefill_shape *s, const void *q, const void *kca
     p.q_bs = p.o_bs = p.kv_bs = 0;
     p.Nk = s->pos0 + s->n_tok;
     p.pos0 = s->pos0;
+    return p;
+}
+}  // namespace
+
+int mxfa_run_prefill(const mxfa_prefill_shape *s, const void *q, const void *kcache, const void *vcache, void *out,
+                     void *stream) {
+    int rc = mxfa_check_prefill(s);
+    if (rc != MXFA_OK) return rc;
+    rc = check_ptrs({q, kcache, vcache, out});
+    if (rc != MXFA_OK) return rc;
+    const Params p = prefill_params(s, q, kcache, vcache, out);
+    return from_hip(mxfa::launch_fwd(p, s->dtype == MXFA_BF16, s->head_dim, 1, static_cast<hipStream_t>(stream)));
+}
+
+int mxfa_run_prefill_paged(const mxfa_prefill_shape *s, const void *q, const void *kcache, const void *vcache,
+                           void *out, const int *block_table, int block_size, void *stream) {
+    int rc = mxfa_check_prefill(s);
+    if (rc != MXFA_OK) return rc;
+    rc = check_ptrs({q, kcache, vcache, out});
+    if (rc != MXFA_OK) return rc;
+    if (block_table == nullptr) return MXFA_ERR_NULL;
+    if (reinterpret_cast<uintptr_t>(block_table) % alignof(int) != 0) return MXFA_ERR_ALIGN;
+    // block sizes are powers of two (the reference engine's is 16)
+    if (block_size < 1 || block_size > (1 << 24) || (block_size & (block_size - 1)) != 0) return MXFA_ERR_UNSUPPORTED;
+    Params p = prefill_params(s, q, kcache, vcache, out);
+    p.block_table = block_table;
+    while ((1 << p.bs_shift) < block_size) ++p.bs_shift;
     return from_hip(mxfa::launch_fwd(p, s->dtype == MXFA_BF16, s->head_dim, 1, static_cast<hipStream_t>(stream)));
 }
 

@@ -220,6 +220,22 @@ def test_prefill_null_and_alignment(lib):
     assert lib.mxfa_run_prefill(ctypes.byref(sh), ok, ok, bad, ok, None) == -5
 
 
+@pytest.mark.parametrize("block_size,code", [(0, -4), (-16, -4), (24, -4), (1 << 25, -4)])
+def test_prefill_paged_block_sizes(lib, block_size, code):
+    """Block sizes are powers of two up to 2^24; others are refused before any launch."""
+    ok = ctypes.c_void_p(4096)
+    assert lib.mxfa_run_prefill_paged(ctypes.byref(_prefill()), ok, ok, ok, ok, ok, block_size, None) == code
+
+
+def test_prefill_paged_null_and_alignment(lib):
+    sh = _prefill()
+    ok, bad = ctypes.c_void_p(4096), ctypes.c_void_p(4096 + 4)
+    assert lib.mxfa_run_prefill_paged(ctypes.byref(sh), ok, ok, ok, ok, None, 16, None) == -1
+    assert lib.mxfa_run_prefill_paged(ctypes.byref(sh), ok, ok, ok, ok, ctypes.c_void_p(4096 + 2), 16, None) == -5
+    assert lib.mxfa_run_prefill_paged(ctypes.byref(sh), ok, ok, bad, ok, ok, 16, None) == -5
+    assert lib.mxfa_run_prefill_paged(ctypes.byref(_prefill(head_dim=96)), ok, ok, ok, ok, ok, 16, None) == -4
+
+
 def test_probe_argument_checks(lib):
     """The probes validate before launching (no device needed for these)."""
     import ctypes
