@@ -77,6 +77,9 @@ def parse():
                          "of the code object, mxfa_gfx950_timeline.hsaco)")
     ap.add_argument("--config-table", action="store_true",
                     help="forward and backward timings at every BASELINE config (one JSON line)")
+    ap.add_argument("--prefill-table", action="store_true",
+                    help="the prefill (mxfa_run_prefill) and the paged prefill (mxfa_run_prefill_paged, "
+                         "16-row blocks) at engine shapes (one JSON line)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run a plain device-to-device copy of MIB "
                          "MiB three times (calibrates the FETCH_SIZE / WRITE_SIZE counters)")
@@ -174,6 +177,54 @@ CONFIGS = [
     ("cfg5 TinyLlama GQA 8:1", 1, 32, 4, 2048, 128, True, "bf16", 0.5),
     ("north star", 4, 12, 12, 4096, 64, True, "bf16", 1.0),
 ]
+
+
+def prefill_table():
+    """The inference-side forward at the reference engine's shapes (Qwen2.5-0.5B:
+    14 query heads over 2 KV heads; TinyLlama-1.1B: 32 over 4; head_dim 64): a
+    first chunk and a chunk after history, over a contiguous cache
+    (mxfa_run_prefill) and a paged one (mxfa_run_prefill_paged, 16-row blocks
+    in shuffled order, the engine's KV_BLOCK), fp32 (the engine's cache) and
+    bf16. Token-major rows, a fused QKV buffer as the engine has; median of
+    per-call event pairs after warm-up (mx.time_median_ms), which for the
+    short launches holds the host's time to issue the call (the kernels'
+    own durations: rocprofv3 --kernel-trace of this mode). TFLOP/s: the
+    causal work 4 d sum_i (pos0 + i + 1) per query head, over the call time."""
+    import torch
+    import mx230_amd as mx
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    mx.init(0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1234)
+    rows = []
+    for model, nh, nkv in (("Qwen2.5-0.5B", 14, 2), ("TinyLlama-1.1B", 32, 4)):
+        for n_tok, pos0 in ((512, 0), (512, 3584), (4096, 0)):
+            for dt in (torch.float32, torch.bfloat16):
+                hd, bs = 64, 16
+                nk = pos0 + n_tok
+                nblk = -(-nk // bs)
+                qkv = torch.randn((n_tok, (nh + 2 * nkv) * hd), generator=gen, device=dev).to(dt)
+                kc = torch.randn((nblk * bs, nkv * hd), generator=gen, device=dev).to(dt)
+                vc = torch.randn_like(kc)
+                perm = torch.randperm(nblk, device=dev, generator=gen).to(torch.int32)
+                kp, vp = torch.empty_like(kc), torch.empty_like(vc)
+                kp.view(nblk, bs, -1)[perm.long()] = kc.view(nblk, bs, -1)
+                vp.view(nblk, bs, -1)[perm.long()] = vc.view(nblk, bs, -1)
+                out = torch.empty((n_tok, nh * hd), device=dev, dtype=dt)
+                q = qkv[:, :nh * hd]
+                flops = 4.0 * hd * nh * (n_tok * (pos0 + 1) + n_tok * (n_tok - 1) / 2)
+                contig = mx.time_median_ms(lambda: mx.run_prefill(q, kc, vc, out, pos0, nh, nkv, hd),
+                                           warmup=20, iters=21)
+                paged = mx.time_median_ms(lambda: mx.run_prefill_paged(q, kp, vp, out, perm, bs, pos0, nh, nkv, hd),
+                                          warmup=20, iters=21)
+                rows.append({"model": model, "n_head": nh, "n_kv_head": nkv, "head_dim": hd, "n_tok": n_tok,
+                             "pos0": pos0, "dtype": "bf16" if dt == torch.bfloat16 else "f32",
+                             "contiguous_call_us": round(contig * 1e3, 1), "paged_call_us": round(paged * 1e3, 1),
+                             "contiguous_tflops": round(flops / (contig * 1e-3) / 1e12, 1),
+                             "paged_tflops": round(flops / (paged * 1e-3) / 1e12, 1)})
+                print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+    print(json.dumps({"prefill_table": rows, "block_size": 16}), flush=True)
 
 
 def config_table():
@@ -529,6 +580,9 @@ def main():
         return
     if a.config_table:
         config_table()
+        return
+    if a.prefill_table:
+        prefill_table()
         return
     if a.atomic_probe:
         atomic_probe(a)
