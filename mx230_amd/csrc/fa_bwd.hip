@@ -839,11 +839,11 @@ __device__ __forceinline__ void dkv_reduce_body(const Params &p, unsigned n4, in
 // ------------------------------------------------------------------ kernels
 
 // The tiles of each dtype / head dim.
-using DqB64 = DqTile16<PolBF16<64>, 2>;
+using DqB64 = DqTile16<PolBF16<64>, PolBF16<64>::kDqTiles>;
 using DkvB64 = DkvTile16<PolBF16<64>, 2>;
-using DqF32 = DqTile16<PolF32<64>, 2>;
+using DqF32 = DqTile16<PolF32<64>, PolF32<64>::kDqTiles>;
 using DkvF32 = DkvTile16<PolF32<64>, 2>;
-using DqB128 = DqTile16<PolBF16<128>, 2>;
+using DqB128 = DqTile16<PolBF16<128>, PolBF16<128>::kDqTiles>;
 using DkvB128 = DkvTile16<PolBF16<128>, 1>;
 
 // The code object's kernels (names: fa_kernels.h), one per instantiation.

@@ -337,10 +337,15 @@ struct PolF32 {
     static constexpr int ROWS = 64;
     // fp32 operands: the scale folds into the operand with a 2^-24 rounding
     static constexpr bool kExactScale = false;
-    static constexpr int kWaves = 1;
-    static constexpr int kWavesFwdCausal = 1;
-    static constexpr int kWavesDq = 1;
-    static constexpr int kDqTiles = 2;
+    // the forward runs 64-query work-groups at two waves per SIMD (fa_fwd.hip)
+    static constexpr int kWaves = 2;
+    static constexpr int kWavesFwdCausal = 2;
+    // dQ pass: one 16-query tile per wave at two waves per SIMD (202 VGPRs);
+    // two tiles at one wave ran slower (B1 H1 N256 backward 70.8 -> 57.5 us,
+    // B4 H12 N1024 causal 244 -> 235, B1 H12 N4096 non-causal 1812 -> 1604).
+    // dK/dV keeps 32 keys per wave at one wave: 16 keys spill at two
+    static constexpr int kWavesDq = 2;
+    static constexpr int kDqTiles = 1;
     static constexpr int kDqWavesPerGroup = 4;
     static constexpr int kWavesDkv = 1;
     static constexpr int kDkvBuffers = 2;

@@ -443,8 +443,14 @@ MXFA_FWD(mxfa_fwd_b64_n_w3_q1, PolBF16<64>, false, 3, 1)
 MXFA_FWD(mxfa_fwd_b128_c_w2_q2, PolBF16<128>, true, 2, 2)
 MXFA_FWD(mxfa_fwd_b128_c_w2_q1, PolBF16<128>, true, 2, 1)
 MXFA_FWD(mxfa_fwd_b128_n_w2_q2, PolBF16<128>, false, 2, 2)
-MXFA_FWD(mxfa_fwd_f64_c_w1_q2, PolF32<64>, true, 1, 2)
-MXFA_FWD(mxfa_fwd_f64_n_w1_q2, PolF32<64>, false, 1, 2)
+// fp32: 64-query work-groups at two waves per SIMD (218 VGPRs). The 128-query
+// form ran at one wave (331 registers) and was slower at every shape measured
+// (causal B4 H12 N1024 75.6 -> 69.6 us, B1 H12 N4096 275 -> 232, B4 H12 N4096
+// 886 -> 803; non-causal B1 H1 N256 22.5 -> 13.9, B4 H12 N1024 145 -> 108,
+// B1 H12 N32768 25.5 -> 23.9 ms; the prefill of 512 tokens after 3584 at 14
+// query heads 274 -> 151 us)
+MXFA_FWD(mxfa_fwd_f64_c_w2_q1, PolF32<64>, true, 2, 1)
+MXFA_FWD(mxfa_fwd_f64_n_w2_q1, PolF32<64>, false, 2, 1)
 // the prefill over a paged cache (causal, as the prefill always is)
 // (the table entries take registers: the three-wave 128-query d = 64 and the
 // 128-query d = 128 forms would spill in their loops, so paged launches use
@@ -452,7 +458,7 @@ MXFA_FWD(mxfa_fwd_f64_n_w1_q2, PolF32<64>, false, 1, 2)
 MXFA_FWD_PG(mxfa_fwd_b64_c_w2_q2_pg, PolBF16<64>, 2, 2)
 MXFA_FWD_PG(mxfa_fwd_b64_c_w3_q1_pg, PolBF16<64>, 3, 1)
 MXFA_FWD_PG(mxfa_fwd_b128_c_w2_q1_pg, PolBF16<128>, 2, 1)
-MXFA_FWD_PG(mxfa_fwd_f64_c_w1_q2_pg, PolF32<64>, 1, 2)
+MXFA_FWD_PG(mxfa_fwd_f64_c_w2_q1_pg, PolF32<64>, 2, 1)
 #undef MXFA_FWD
 #undef MXFA_FWD_PG
 #endif
@@ -471,8 +477,8 @@ static KernelId fwd_kernel_id(int wps, int qt, bool paged) {
         if (CAUSAL) return qt == 1 ? k_mxfa_fwd_b128_c_w2_q1 : k_mxfa_fwd_b128_c_w2_q2;
         return k_mxfa_fwd_b128_n_w2_q2;
     } else {
-        if (CAUSAL && paged) return k_mxfa_fwd_f64_c_w1_q2_pg;
-        return CAUSAL ? k_mxfa_fwd_f64_c_w1_q2 : k_mxfa_fwd_f64_n_w1_q2;
+        if (CAUSAL && paged) return k_mxfa_fwd_f64_c_w2_q1_pg;
+        return CAUSAL ? k_mxfa_fwd_f64_c_w2_q1 : k_mxfa_fwd_f64_n_w2_q1;
     }
 }
 
@@ -507,6 +513,7 @@ static hipError_t launch_fwd_t(const Params &p, hipStream_t stream) {
         if (wg < kFwdSmallGrid || (Pol::D == 128 && p.block_table != nullptr))
             return launch_fwd_qt<Pol, CAUSAL, 1>(p, stream);
     }
+    if constexpr (!Pol::kExactScale) return launch_fwd_qt<Pol, CAUSAL, 1>(p, stream);  // fp32: see the kernels
     return launch_fwd_qt<Pol, CAUSAL, 2>(p, stream);
 }
 

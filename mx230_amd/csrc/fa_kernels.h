@@ -15,9 +15,9 @@
     X(mxfa_fwd_b64_c_w3_q2) X(mxfa_fwd_b64_c_w2_q2) X(mxfa_fwd_b64_c_w3_q1)                   \
     X(mxfa_fwd_b64_n_w2_q2) X(mxfa_fwd_b64_n_w3_q1)                                           \
     X(mxfa_fwd_b128_c_w2_q2) X(mxfa_fwd_b128_c_w2_q1) X(mxfa_fwd_b128_n_w2_q2)                \
-    X(mxfa_fwd_f64_c_w1_q2) X(mxfa_fwd_f64_n_w1_q2)                                           \
+    X(mxfa_fwd_f64_c_w2_q1) X(mxfa_fwd_f64_n_w2_q1)                                           \
     X(mxfa_fwd_b64_c_w2_q2_pg) X(mxfa_fwd_b64_c_w3_q1_pg) X(mxfa_fwd_b128_c_w2_q1_pg)          \
-    X(mxfa_fwd_f64_c_w1_q2_pg)                                                                \
+    X(mxfa_fwd_f64_c_w2_q1_pg)                                                                \
     /* backward (fa_bwd.hip) */                                                               \
     X(mxfa_preprocess_b64) X(mxfa_preprocess_b128) X(mxfa_preprocess_f64)                     \
     X(mxfa_dq_b64_c) X(mxfa_dq_b64_c_d) X(mxfa_dq_b64_n) X(mxfa_dq_b64_n_d)                   \
