@@ -182,10 +182,11 @@ CONFIGS = [
 def prefill_table():
     """The inference-side forward at the reference engine's shapes (Qwen2.5-0.5B:
     14 query heads over 2 KV heads; TinyLlama-1.1B: 32 over 4; head_dim 64): a
-    first chunk and a chunk after history, over a contiguous cache
-    (mxfa_run_prefill) and a paged one (mxfa_run_prefill_paged, 16-row blocks
-    in shuffled order, the engine's KV_BLOCK), fp32 (the engine's cache) and
-    bf16. Token-major rows, a fused QKV buffer as the engine has; median of
+    first chunk, a chunk after history and a single row after history, over a
+    contiguous cache (mxfa_run_prefill; mxfa_run_prefill_ws, its keys split
+    over work-groups where the query blocks alone would not fill the GPU) and
+    a paged one (mxfa_run_prefill_paged, 16-row blocks in shuffled order, the
+    engine's KV_BLOCK), fp32 (the engine's cache) and bf16. Token-major rows, a fused QKV buffer as the engine has; median of
     per-call event pairs after warm-up (mx.time_median_ms), which for the
     short launches holds the host's time to issue the call (the kernels'
     own durations: rocprofv3 --kernel-trace of this mode). TFLOP/s: the
@@ -199,7 +200,7 @@ def prefill_table():
     gen.manual_seed(1234)
     rows = []
     for model, nh, nkv in (("Qwen2.5-0.5B", 14, 2), ("TinyLlama-1.1B", 32, 4)):
-        for n_tok, pos0 in ((512, 0), (512, 3584), (4096, 0)):
+        for n_tok, pos0 in ((512, 0), (512, 3584), (4096, 0), (1, 4095)):
             for dt in (torch.float32, torch.bfloat16):
                 hd, bs = 64, 16
                 nk = pos0 + n_tok
@@ -218,11 +219,18 @@ def prefill_table():
                                            warmup=20, iters=21)
                 paged = mx.time_median_ms(lambda: mx.run_prefill_paged(q, kp, vp, out, perm, bs, pos0, nh, nkv, hd),
                                           warmup=20, iters=21)
+                ws = mx.run_prefill_split(q, kc, vc, out, pos0, nh, nkv, hd)
+                split = mx.time_median_ms(lambda: mx.run_prefill_split(q, kc, vc, out, pos0, nh, nkv, hd,
+                                                                       workspace=ws), warmup=20, iters=21)
+                nsplit = mx.prefill_workspace_bytes(n_tok, pos0, nh, nkv, hd, dt == torch.bfloat16) // \
+                    (nh * n_tok * (hd + 2) * 4)
                 rows.append({"model": model, "n_head": nh, "n_kv_head": nkv, "head_dim": hd, "n_tok": n_tok,
                              "pos0": pos0, "dtype": "bf16" if dt == torch.bfloat16 else "f32",
                              "contiguous_call_us": round(contig * 1e3, 1), "paged_call_us": round(paged * 1e3, 1),
+                             "key_splits": max(nsplit, 1), "split_call_us": round(split * 1e3, 1),
                              "contiguous_tflops": round(flops / (contig * 1e-3) / 1e12, 1),
-                             "paged_tflops": round(flops / (paged * 1e-3) / 1e12, 1)})
+                             "paged_tflops": round(flops / (paged * 1e-3) / 1e12, 1),
+                             "split_tflops": round(flops / (split * 1e-3) / 1e12, 1)})
                 print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
     print(json.dumps({"prefill_table": rows, "block_size": 16}), flush=True)
 

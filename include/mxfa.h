@@ -52,7 +52,7 @@ typedef enum {
     MXFA_ERR_ALIGN = -5,       /* a device pointer is not 16-byte aligned */
     MXFA_ERR_LAUNCH = -6,      /* the HIP runtime rejected a launch */
     MXFA_ERR_DEVICE = -7,      /* no usable gfx950 device */
-    MXFA_ERR_WORKSPACE = -8,   /* a workspace smaller than mxfa_bwd_workspace_bytes(shape) */
+    MXFA_ERR_WORKSPACE = -8,   /* a workspace smaller than mxfa_{bwd,prefill}_workspace_bytes(shape) */
     MXFA_ERR_CODE_OBJECT = -9, /* the gfx950 code object is missing, malformed, for another
                                   processor, or lacks a kernel */
     MXFA_ERR_SCRATCH = -10     /* mxfa_run_bwd_noalloc: the shape needs more than
@@ -324,6 +324,24 @@ int mxfa_run_prefill(const mxfa_prefill_shape *shape, const void *q, const void 
  * gathered, contiguous cache. */
 int mxfa_run_prefill_paged(const mxfa_prefill_shape *shape, const void *q, const void *kcache, const void *vcache,
                            void *out, const int *block_table, int block_size, void *stream);
+
+/* The prefill with its keys split over work-groups, for chunks whose query
+ * blocks alone would leave most of the GPU idle (a few hundred tokens after a
+ * long history, or a single decode-like row). Replaces the same
+ * `attn_prefill` launch as mxfa_run_prefill (llm.cu:3806-3815, gpu.rs:3235-3289),
+ * which has no counterpart of the split: each work-group takes a range of the
+ * cache's 64-key stages of one 64-query block and writes its unnormalised
+ * output and its rows' running max and sum to `workspace` (fp32); a second
+ * launch adds the ranges (out = sum_s w_s O_s / sum_s w_s l_s with
+ * w_s = 2^(m_s - max m)). Same arguments as mxfa_run_prefill, plus the
+ * workspace: mxfa_prefill_workspace_bytes(shape) bytes, 16-byte aligned,
+ * device memory (no contents needed; calls that share one race). When that
+ * size is 0 the shape needs no split and this is mxfa_run_prefill (workspace
+ * may be NULL). A smaller workspace gives MXFA_ERR_WORKSPACE. Results equal
+ * mxfa_run_prefill's to fp32 rounding of the merge, not bitwise. */
+size_t mxfa_prefill_workspace_bytes(const mxfa_prefill_shape *shape);
+int mxfa_run_prefill_ws(const mxfa_prefill_shape *shape, const void *q, const void *kcache, const void *vcache,
+                        void *out, void *workspace, size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

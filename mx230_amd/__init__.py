@@ -55,7 +55,7 @@ EXPORTS = (
     "mxfa_run_bwd_dkv", "mxfa_run_bwd_flash", "mxfa_run_bwd_dq_delta", "mxfa_run_bwd", "mxfa_bwd_one_launch", "mxfa_bwd_workspace_bytes",
     "mxfa_run_bwd_dkv_ws", "mxfa_run_bwd_ws", "mxfa_run_bwd_naive",
     "mxfa_naive_scratch_bytes", "mxfa_run_naive_fwd", "mxfa_check_prefill", "mxfa_run_prefill",
-    "mxfa_run_prefill_paged",
+    "mxfa_run_prefill_paged", "mxfa_prefill_workspace_bytes", "mxfa_run_prefill_ws",
     "mxfa_set_bwd_options", "mxfa_get_bwd_options", "mxfa_bwd_delta_fallbacks",
     "mxfa_run_bwd_noalloc", "mxfa_bwd_noalloc_scratch_bytes",
 )
@@ -146,6 +146,9 @@ def load_library(path: str | None = None):
     lib.mxfa_check_prefill.argtypes = [pp]
     lib.mxfa_run_prefill.argtypes = [pp, vp, vp, vp, vp, vp]
     lib.mxfa_run_prefill_paged.argtypes = [pp, vp, vp, vp, vp, vp, ctypes.c_int, vp]
+    lib.mxfa_prefill_workspace_bytes.argtypes = [pp]
+    lib.mxfa_prefill_workspace_bytes.restype = ctypes.c_size_t
+    lib.mxfa_run_prefill_ws.argtypes = [pp, vp, vp, vp, vp, vp, ctypes.c_size_t, vp]
     lib.mxfa_probe_sink_len.argtypes = []
     lib.mxfa_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_int, fp, ctypes.POINTER(ctypes.c_double), vp]
     lib.mxfa_probe_mfma32.argtypes = [ctypes.c_int, fp, ctypes.POINTER(ctypes.c_double), vp]
@@ -161,7 +164,8 @@ def load_library(path: str | None = None):
     lib.mxfa_bwd_delta_fallbacks.argtypes = [ctypes.POINTER(ctypes.c_ulonglong)]
     for name in EXPORTS + PROBE_EXPORTS:
         if name not in ("mxfa_version", "mxfa_strerror", "mxfa_bwd_workspace_bytes",
-                        "mxfa_naive_scratch_bytes", "mxfa_bwd_noalloc_scratch_bytes"):
+                        "mxfa_naive_scratch_bytes", "mxfa_bwd_noalloc_scratch_bytes",
+                        "mxfa_prefill_workspace_bytes"):
             getattr(lib, name).restype = ctypes.c_int
     if path is None:
         _lib = lib
@@ -540,6 +544,49 @@ def run_prefill_paged(q, kcache, vcache, out, block_table, block_size: int, pos0
            load_library().mxfa_run_prefill_paged(ctypes.byref(sh), qp, kp, vp, op,
                                                  ctypes.c_void_p(block_table.data_ptr()), int(block_size),
                                                  _stream(stream)))
+
+
+def prefill_workspace_bytes(n_tok: int, pos0: int, n_head: int, n_kv_head: int, head_dim: int = 64,
+                            bf16: bool = True) -> int:
+    """mxfa_prefill_workspace_bytes for contiguous rows: the fp32 partials
+    run_prefill_split needs (0: the shape runs unsplit)."""
+    w = n_head * head_dim
+    sh = MxfaPrefillShape(n_tok, n_head, n_kv_head, head_dim, pos0, w, n_kv_head * head_dim, w,
+                          MXFA_BF16 if bf16 else MXFA_F32, 0.0)
+    return int(load_library().mxfa_prefill_workspace_bytes(ctypes.byref(sh)))
+
+
+def run_prefill_split(q, kcache, vcache, out, pos0: int, n_head: int, n_kv_head: int, head_dim: int = 64,
+                      scale: float = 0.0, workspace=None, stream=None):
+    """mxfa_run_prefill_ws: run_prefill with the cache's keys split over
+    work-groups when the chunk's query blocks would not fill the GPU (the same
+    attn_prefill launch, 03-llm-engine/kernels/llm.cu:3806-3815). Arguments as
+    run_prefill; workspace: a device tensor of at least the size
+    mxfa_prefill_workspace_bytes reports (allocated here when None). Results
+    equal run_prefill's to fp32 rounding, not bitwise."""
+    torch = _torch()
+    if q.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"q: dtype {q.dtype}; bf16 or float32 expected")
+    n_tok = q.shape[0] if q.dim() == 2 else -1
+    qp, qs = _rows(q, "q", q.dtype, 1, n_head * head_dim)
+    kp, ks = _rows(kcache, "kcache", q.dtype, pos0 + n_tok, n_kv_head * head_dim)
+    vp, vs = _rows(vcache, "vcache", q.dtype, pos0 + n_tok, n_kv_head * head_dim)
+    if ks != vs:
+        raise ValueError(f"kcache and vcache must share a row stride ({ks} != {vs})")
+    op, os_ = _rows(out, "out", q.dtype, n_tok, n_head * head_dim)
+    sh = MxfaPrefillShape(n_tok, n_head, n_kv_head, head_dim, pos0, qs, ks, os_,
+                          MXFA_BF16 if q.dtype == torch.bfloat16 else MXFA_F32, scale)
+    lib = load_library()
+    need = int(lib.mxfa_prefill_workspace_bytes(ctypes.byref(sh)))
+    if workspace is None:
+        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=q.device)
+    if not isinstance(workspace, torch.Tensor) or workspace.device.type != "cuda" or not workspace.is_contiguous():
+        raise ValueError("workspace: expected a contiguous device tensor")
+    have = workspace.numel() * workspace.element_size()
+    _check("mxfa_run_prefill_ws",
+           lib.mxfa_run_prefill_ws(ctypes.byref(sh), qp, kp, vp, op, ctypes.c_void_p(workspace.data_ptr()),
+                                   have, _stream(stream)))
+    return workspace
 
 
 # ------------------------------------------------------------ conveniences --

@@ -51,6 +51,11 @@ struct Params {
     // from the K/V base of the head; null: cache row t.
     const int *block_table;
     int bs_shift;
+    // Split forward (fwd_entry<..., SPLIT>, the prefill with a workspace):
+    // per split s and row r of the B*Hq*N query rows, the unnormalised O at
+    // fwd_part[(s rows + r) D], then (running max in log2 units, sum) at
+    // fwd_part[S rows D + 2 (s rows + r)].
+    float *fwd_part;
     // dK/dV pass with dkv_split > 1: the group's query heads' stages of a
     // key block (group x its stages per head, in head order) are split into
     // dkv_block_shares(...) contiguous runs, one work-group each; share s

@@ -44,8 +44,9 @@ __device__ __forceinline__ constexpr int fwd_mask_offset(int blk, int t, int g, 
 // One 64-key stage for one wave: scores in log2 units (x xmul when Q is kept
 // exact, else qf holds Q scale log2(e)), online-softmax update,
 // O^T += V^T P^T. PRIO: the matrix products run at raised wave priority.
-// qpos0: position of the wave's first query row; Nk: key rows.
-template <class Pol, int QT, bool CAUSAL, bool MASK, bool PRIO = false>
+// qpos0: position of the wave's first query row; Nk: key rows. EMPTY_ROWS:
+// rows may have every key of the stage masked (a key split's first stage).
+template <class Pol, int QT, bool CAUSAL, bool MASK, bool PRIO = false, bool EMPTY_ROWS = false>
 __device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][QT], float (&m)[QT], float (&lsum)[QT],
                                           const typename Pol::Frag (&qf)[QT][Pol::NC],
                                           const typename Pol::T *sk, const typename Pol::T *sv, int k0, int qpos0,
@@ -89,7 +90,10 @@ __device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][QT], float (
         }
         mx = xg_max(mx);
         const float mnew = fmaxf(m[qt], mx);
-        const float corr = fast_exp2(m[qt] - mnew);
+        // a row with every key of the stage masked keeps m = -inf and gets
+        // p = 0 (2^(-inf - 0)), not 2^(-inf - -inf) = NaN
+        const float mref = EMPTY_ROWS && mnew == -INFINITY ? 0.f : mnew;
+        const float corr = fast_exp2(m[qt] - mref);
         m[qt] = mnew;
         float ls = lsum[qt] * corr;
 #pragma unroll
@@ -100,7 +104,7 @@ __device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][QT], float (
             for (int t = 0; t < 2; ++t) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const float pv = fast_exp2(s[blk][t][qt][r] - mnew);
+                    const float pv = fast_exp2(s[blk][t][qt][r] - mref);
                     s[blk][t][qt][r] = pv;
                     ls += pv;
                 }
@@ -127,7 +131,9 @@ __device__ __forceinline__ void fwd_stage(f32x4 (&acc)[Pol::D / 16][QT], float (
 
 // fwd_stage for every stage after the first, with lazy rescaling. Key 0 is
 // visible to every query (pos0 >= 0), so after the first stage m is finite for
-// every row. The scores come out of the MFMAs relative to the running max m
+// every row; a key split's work-group may leave a row at m = -inf after its
+// first stage only when the row precedes every key of the split (causal), so
+// every later stage masks the whole row (p = 0, nothing to rescale). The scores come out of the MFMAs relative to the running max m
 // (the accumulators start at -m), and p = 2^(s - m) is taken optimistically
 // with the old m. A lane's per-row sum of its p over the stage (16 keys)
 // bounds each of them, so when no such sum exceeds kLazySum no p does either:
@@ -281,8 +287,12 @@ __device__ __forceinline__ void fwd_stage_lazy(f32x4 (&acc)[Pol::D / 16][QT], fl
 // One work-group of the forward, grid (B Hq, query blocks). QT: 16-query
 // tiles per wave (the work-group takes 64 QT queries); the kernels are
 // compiled for a number of waves per SIMD (the names' w*). PAGED: K/V rows
-// through Params::block_table (the kernels named *_pg).
-template <class Pol, bool CAUSAL, int QT, bool PAGED = false>
+// through Params::block_table (the kernels named *_pg). SPLIT (kernels *_sp,
+// grid.z = the splits): work-group z takes stages [z nsteps / S, (z + 1)
+// nsteps / S) of its query block's keys and writes its unnormalised O and
+// its rows' running max and sum to Params::fwd_part; fwd_merge adds the
+// splits.
+template <class Pol, bool CAUSAL, int QT, bool PAGED = false, bool SPLIT = false>
 __device__ __forceinline__ void fwd_entry(const Params &p) {
     using T = typename Pol::T;
     using Frag = typename Pol::Frag;
@@ -337,7 +347,11 @@ __device__ __forceinline__ void fwd_entry(const Params &p) {
 
     const int kend = CAUSAL ? min(Nk, pos0 + qb * BQ + BQ) : Nk;
     const int nsteps = (kend + BK - 1) / BK;
-    wg_info(2, qb, nsteps);
+    // this work-group's stages [s_lo, s_hi) (SPLIT: its share; the first one
+    // it runs takes the plain softmax body, the running max starting at -inf)
+    const int s_lo = SPLIT ? (int)((long long)blockIdx.z * nsteps / gridDim.z) : 0;
+    const int s_hi = SPLIT ? (int)((long long)(blockIdx.z + 1) * nsteps / gridDim.z) : nsteps;
+    wg_info(2, qb, s_hi - s_lo);
 
     const RowPlan<Pol> plan(tid);
     // PAGED: the table entries of stage 0 now, then each stage fetches those
@@ -351,8 +365,10 @@ __device__ __forceinline__ void fwd_entry(const Params &p) {
             stage_kv<Pol>(sk, sv, K, V, k0, Nk, plan, wave, p.kv_rs);
         }
     };
-    if constexpr (PAGED) paged.fetch(p.block_table, p.bs_shift, 0, Nk, plan);
-    stage_next(sK[0], sV[0], 0);
+    if (!SPLIT || s_lo < s_hi) {
+        if constexpr (PAGED) paged.fetch(p.block_table, p.bs_shift, s_lo * BK, Nk, plan);
+        stage_next(sK[0], sV[0], s_lo * BK);
+    }
     wait_stage();
     __syncthreads();
     wg_time(1);
@@ -365,7 +381,7 @@ __device__ __forceinline__ void fwd_entry(const Params &p) {
     // starts at -inf); later ones the lazy-rescaling body.
     auto main_stage = [&](auto buf, auto first, int st) __attribute__((always_inline)) {
         constexpr int B = decltype(buf)::value;
-        if (st + 1 < nsteps) stage_next(sK[B ^ 1], sV[B ^ 1], (st + 1) * BK);
+        if (st + 1 < s_hi) stage_next(sK[B ^ 1], sV[B ^ 1], (st + 1) * BK);
         if constexpr (decltype(first)::value) {
             fwd_stage<Pol, QT, CAUSAL, false, kPrio>(acc, m, lsum, qf, sK[B], sV[B], st * BK, qpos0, Nk, g, l16,
                                                      p.scale_log2);
@@ -378,25 +394,27 @@ __device__ __forceinline__ void fwd_entry(const Params &p) {
     };
     using B0 = std::integral_constant<int, 0>;
     using B1 = std::integral_constant<int, 1>;
-    const int nmain = min(min(nsteps, Nk / BK), CAUSAL ? (pos0 + qb * BQ + 1) / BK : nsteps);
-    int st = 0;
-    if (nmain > 0) main_stage(B0{}, std::true_type{}, st++);
+    const int nmain = min(min(s_hi, Nk / BK), CAUSAL ? (pos0 + qb * BQ + 1) / BK : s_hi);
+    int st = s_lo;
+    if (nmain > st) main_stage(B0{}, std::true_type{}, st++);
     for (; st + 1 < nmain; st += 2) {
         main_stage(B1{}, std::false_type{}, st);
         main_stage(B0{}, std::false_type{}, st + 1);
     }
     if (st < nmain) main_stage(B1{}, std::false_type{}, st++);
     // the remaining stages may straddle the diagonal or the end of the keys:
-    // one masked body each for the first stage and the later ones
-    for (; st < nsteps; ++st) {
-        const int cur = st & 1;
-        if (st + 1 < nsteps) stage_next(sK[cur ^ 1], sV[cur ^ 1], (st + 1) * BK);
+    // one masked body each for the first stage and the later ones (a wave
+    // that skips a stage skips every later one, so its first run stage is
+    // the work-group's first)
+    for (; st < s_hi; ++st) {
+        const int cur = (st - s_lo) & 1;
+        if (st + 1 < s_hi) stage_next(sK[cur ^ 1], sV[cur ^ 1], (st + 1) * BK);
         const int k0 = st * BK;
         // a wave whose queries all precede the stage's keys has nothing to do
         if (!CAUSAL || k0 <= qpos0 + 16 * QT - 1) {
-            if (st == 0) {
-                fwd_stage<Pol, QT, CAUSAL, true, kPrio>(acc, m, lsum, qf, sK[cur], sV[cur], k0, qpos0, Nk, g, l16,
-                                                        p.scale_log2);
+            if (st == s_lo) {
+                fwd_stage<Pol, QT, CAUSAL, true, kPrio, SPLIT>(acc, m, lsum, qf, sK[cur], sV[cur], k0, qpos0, Nk, g,
+                                                               l16, p.scale_log2);
             } else {
                 fwd_stage_lazy<Pol, QT, CAUSAL, true, kPrio>(acc, m, lsum, qf, sK[cur], sV[cur], k0, qpos0, Nk, g, l16,
                                                              p.scale_log2);
@@ -407,6 +425,27 @@ __device__ __forceinline__ void fwd_entry(const Params &p) {
     }
 
     wg_time(2);
+    if constexpr (SPLIT) {
+        // the split's partial: O unnormalised, then (running max, sum) per row
+        const size_t rows = (size_t)gridDim.z * p.B * p.Hq * N;
+        const size_t r0 = ((size_t)blockIdx.z * p.B * p.Hq + bh) * N;
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+            const int qi = q0 + 16 * qt + l16;
+            const float ltot = xg_sum(lsum[qt]);
+            if (qi < N) {
+                float *po = p.fwd_part + (r0 + qi) * D;
+#pragma unroll
+                for (int xt = 0; xt < XT; ++xt) store4<float>(po + 16 * xt + 4 * g, acc[xt][qt], 1.0f);
+                if (g == 0) {
+                    float *pml = p.fwd_part + rows * D + 2 * (r0 + qi);
+                    *reinterpret_cast<float2 *>(pml) = make_float2(m[qt], ltot);
+                }
+            }
+        }
+        wg_time_after_stores();
+        return;
+    }
     T *O = static_cast<T *>(p.o) + b * p.o_bs + h * p.o_hs;
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
@@ -426,6 +465,57 @@ __device__ __forceinline__ void fwd_entry(const Params &p) {
         if (qi < N && p.lse != nullptr && g == 0) p.lse[(size_t)bh * N + qi] = (m[qt] + fast_log2(ltot)) * kLn2;
     }
     wg_time_after_stores();
+}
+
+// Adds the S key splits of a split forward (fwd_entry<..., SPLIT>), one
+// thread per four elements of a query row: with M the largest of the splits'
+// running maxima (log2 units), O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M)
+// l_s, in split order, written as the forward writes O. A split that holds
+// no key of the row has m = -inf and weight 0. Every load is issued before
+// the first is used (the loops unrolled to kFwdMaxSplits), so a call costs
+// one memory latency rather than one per split.
+constexpr int kFwdMaxSplits = 16;
+
+template <class T, int D>
+__device__ __forceinline__ void fwd_merge_body(const Params &p, int S) {
+    constexpr int C = D / 4;
+    const size_t rows = (size_t)p.B * p.Hq * p.N;
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= rows * C) return;
+    const size_t r = t / C;
+    const int c = (int)(t % C);
+    const float2 *ml = reinterpret_cast<const float2 *>(p.fwd_part + (size_t)S * rows * D);
+    float2 v[kFwdMaxSplits];
+    float4 a[kFwdMaxSplits];
+#pragma unroll
+    for (int sp = 0; sp < kFwdMaxSplits; ++sp) {
+        if (sp < S) {
+            v[sp] = ml[sp * rows + r];
+            a[sp] = *reinterpret_cast<const float4 *>(p.fwd_part + (sp * rows + r) * D + 4 * c);
+        }
+    }
+    // the split holding key 0 (visible to every row) makes M finite
+    float M = -INFINITY;
+#pragma unroll
+    for (int sp = 0; sp < kFwdMaxSplits; ++sp) M = sp < S ? fmaxf(M, v[sp].x) : M;
+    float L = 0.f;
+    f32x4 o = zero4();
+#pragma unroll
+    for (int sp = 0; sp < kFwdMaxSplits; ++sp) {
+        if (sp < S) {
+            const float w = fast_exp2(v[sp].x - M);
+            L += w * v[sp].y;
+            o[0] += w * a[sp].x;
+            o[1] += w * a[sp].y;
+            o[2] += w * a[sp].z;
+            o[3] += w * a[sp].w;
+        }
+    }
+    const int bh = (int)(r / p.N), qi = (int)(r % p.N);
+    const int b = bh / p.Hq, h = bh % p.Hq;
+    T *O = static_cast<T *>(p.o) + b * p.o_bs + h * p.o_hs + (size_t)qi * p.o_rs + 4 * c;
+    store4<T>(O, o, 1.0f / L);
+    if (p.lse != nullptr && c == 0) p.lse[r] = (M + fast_log2(L)) * kLn2;
 }
 
 // The code object's forward kernels (fa_kernels.h): policy, causal, waves
@@ -459,8 +549,22 @@ MXFA_FWD_PG(mxfa_fwd_b64_c_w2_q2_pg, PolBF16<64>, 2, 2)
 MXFA_FWD_PG(mxfa_fwd_b64_c_w3_q1_pg, PolBF16<64>, 3, 1)
 MXFA_FWD_PG(mxfa_fwd_b128_c_w2_q1_pg, PolBF16<128>, 2, 1)
 MXFA_FWD_PG(mxfa_fwd_f64_c_w2_q1_pg, PolF32<64>, 2, 1)
+// the prefill split over its keys (causal, 64-query work-groups) and the
+// merge of the splits
+#define MXFA_FWD_SP(NAME, POL, WPS)                                                                    \
+    extern "C" __global__ __launch_bounds__(256, WPS) void NAME(Params p) { fwd_entry<POL, true, 1, false, true>(p); }
+MXFA_FWD_SP(mxfa_fwd_b64_c_w3_q1_sp, PolBF16<64>, 3)
+MXFA_FWD_SP(mxfa_fwd_b128_c_w2_q1_sp, PolBF16<128>, 2)
+MXFA_FWD_SP(mxfa_fwd_f64_c_w2_q1_sp, PolF32<64>, 2)
+#define MXFA_FWD_MERGE(NAME, T, D)                                                                     \
+    extern "C" __global__ __launch_bounds__(256) void NAME(Params p, int splits) { fwd_merge_body<T, D>(p, splits); }
+MXFA_FWD_MERGE(mxfa_fwd_merge_b64, u16, 64)
+MXFA_FWD_MERGE(mxfa_fwd_merge_b128, u16, 128)
+MXFA_FWD_MERGE(mxfa_fwd_merge_f64, float, 64)
 #undef MXFA_FWD
 #undef MXFA_FWD_PG
+#undef MXFA_FWD_SP
+#undef MXFA_FWD_MERGE
 #endif
 
 // The kernel of (policy, causal) compiled for `wps` waves per SIMD with `qt`
@@ -515,6 +619,45 @@ static hipError_t launch_fwd_t(const Params &p, hipStream_t stream) {
     }
     if constexpr (!Pol::kExactScale) return launch_fwd_qt<Pol, CAUSAL, 1>(p, stream);  // fp32: see the kernels
     return launch_fwd_qt<Pol, CAUSAL, 2>(p, stream);
+}
+
+// Splits of the prefill's keys: none (1) when the 64-query work-groups
+// already fill the resident slots (256 CUs x waves per SIMD) halfway, or when
+// the heaviest query block has under 16 key stages (bf16; 8 for fp32), where
+// the merging launch costs more than the split saves (measured on the MI355X,
+// Qwen2.5 heads, 512 tokens at position 0, 8 stages: bf16 19.7 -> 24.6 us
+// with 2 splits, fp32 36.5 -> 32.6 us); else enough to fill them, with at
+// least 4 key stages per split and at most 16 splits.
+int fwd_splits(const Params &p, int dtype_bf16, int d) {
+    const long long wgs = (long long)p.B * p.Hq * ((p.N + 63) / 64);
+    const long long slots = 256LL * (dtype_bf16 && d == 64 ? 3 : 2);
+    if (2 * wgs >= slots) return 1;
+    const long long stages = (std::min(p.Nk, p.pos0 + p.N) + 63) / 64;  // the heaviest block's
+    if (stages < (dtype_bf16 ? 16 : 8)) return 1;
+    long long s = (slots + wgs - 1) / wgs;
+    s = std::min(s, std::max(1LL, stages / 4));
+    return (int)std::min(s, (long long)kFwdMaxSplits);
+}
+
+size_t fwd_split_workspace_bytes(const Params &p, int d, int splits) {
+    if (splits <= 1) return 0;
+    return (size_t)splits * p.B * p.Hq * p.N * (size_t)(d + 2) * sizeof(float);
+}
+
+hipError_t launch_fwd_split(const Params &p, int dtype_bf16, int d, int splits, hipStream_t stream) {
+    if (p.fwd_part == nullptr || splits < 2 || splits > kFwdMaxSplits || p.block_table != nullptr)
+        return hipErrorInvalidValue;
+    const KernelId kf = dtype_bf16 ? (d == 64 ? k_mxfa_fwd_b64_c_w3_q1_sp : k_mxfa_fwd_b128_c_w2_q1_sp)
+                                   : k_mxfa_fwd_f64_c_w2_q1_sp;
+    const KernelId km = dtype_bf16 ? (d == 64 ? k_mxfa_fwd_merge_b64 : k_mxfa_fwd_merge_b128) : k_mxfa_fwd_merge_f64;
+    Params q = p;
+    void *args[] = {&q};
+    hipError_t e = launch_kernel(kf, dim3(p.B * p.Hq, (p.N + 63) / 64, splits), dim3(256), args, stream);
+    if (e != hipSuccess) return e;
+    const size_t n = (size_t)p.B * p.Hq * p.N * (d / 4);
+    int s = splits;
+    void *margs[] = {&q, &s};
+    return launch_kernel(km, dim3((unsigned)((n + 255) / 256)), dim3(256), margs, stream);
 }
 
 hipError_t launch_fwd(const Params &p, int dtype_bf16, int d, int causal, hipStream_t stream) {

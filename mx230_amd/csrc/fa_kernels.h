@@ -7,7 +7,7 @@
 // the code object fails that load. Naming: pass, dtype and head dim (b64 =
 // bf16 d = 64, b128, f64 = fp32 d = 64), c / n = causal / not, then the
 // variant (waves per SIMD w*, query tiles per wave q*, d = computes Delta,
-// pg = K/V through a block table).
+// pg = K/V through a block table, sp = one split of the keys).
 #pragma once
 
 #define MXFA_KERNEL_LIST(X)                                                                   \
@@ -18,6 +18,8 @@
     X(mxfa_fwd_f64_c_w2_q1) X(mxfa_fwd_f64_n_w2_q1)                                           \
     X(mxfa_fwd_b64_c_w2_q2_pg) X(mxfa_fwd_b64_c_w3_q1_pg) X(mxfa_fwd_b128_c_w2_q1_pg)          \
     X(mxfa_fwd_f64_c_w2_q1_pg)                                                                \
+    X(mxfa_fwd_b64_c_w3_q1_sp) X(mxfa_fwd_b128_c_w2_q1_sp) X(mxfa_fwd_f64_c_w2_q1_sp)          \
+    X(mxfa_fwd_merge_b64) X(mxfa_fwd_merge_b128) X(mxfa_fwd_merge_f64)                        \
     /* backward (fa_bwd.hip) */                                                               \
     X(mxfa_preprocess_b64) X(mxfa_preprocess_b128) X(mxfa_preprocess_f64)                     \
     X(mxfa_dq_b64_c) X(mxfa_dq_b64_c_d) X(mxfa_dq_b64_n) X(mxfa_dq_b64_n_d)                   \

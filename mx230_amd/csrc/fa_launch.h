@@ -33,6 +33,13 @@ void unload_code_objects();
 hipError_t launch_kernel(KernelId id, dim3 grid, dim3 block, void **args, hipStream_t stream);
 
 hipError_t launch_fwd(const Params &p, int dtype_bf16, int d, int causal, hipStream_t stream);
+// The causal forward with its keys split over work-groups (grid.z) and a
+// merging launch: the split count for a shape (1: no split pays), the fp32
+// partials it needs in p.fwd_part, and the two launches (splits >= 2,
+// contiguous K/V).
+int fwd_splits(const Params &p, int dtype_bf16, int d);
+size_t fwd_split_workspace_bytes(const Params &p, int d, int splits);
+hipError_t launch_fwd_split(const Params &p, int dtype_bf16, int d, int splits, hipStream_t stream);
 hipError_t launch_preprocess(const Params &p, int dtype_bf16, int d, hipStream_t stream);
 // delta != 0: the dQ pass computes Delta from p.o_in and writes it to p.delta
 hipError_t launch_bwd_dq(const Params &p, int dtype_bf16, int d, int causal, int delta, hipStream_t stream);

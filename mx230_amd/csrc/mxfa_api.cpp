@@ -58,6 +58,7 @@ Params make_params(const mxfa_shape *s) {
     p.Nk = s->N;
     p.pos0 = 0;
     p.block_table = nullptr;  // contiguous K/V
+    p.fwd_part = nullptr;     // the unsplit forward
     p.bs_shift = 0;
     p.dkv_ws = nullptr;
     p.dkv_split = p.dkv_min_shares = 1;
@@ -134,7 +135,7 @@ const char *mxfa_strerror(int status) {
         case MXFA_ERR_ALIGN: return "a device pointer is not 16-byte aligned";
         case MXFA_ERR_LAUNCH: return "the HIP runtime rejected a kernel launch";
         case MXFA_ERR_DEVICE: return "no usable gfx950 device";
-        case MXFA_ERR_WORKSPACE: return "the workspace is smaller than mxfa_bwd_workspace_bytes(shape)";
+        case MXFA_ERR_WORKSPACE: return "the workspace is smaller than the *_workspace_bytes(shape) of the call";
         case MXFA_ERR_SCRATCH:
             return "the shape needs more scratch than mxfa_bwd_noalloc_scratch_bytes() (use mxfa_run_bwd_ws)";
         case MXFA_ERR_CODE_OBJECT:
@@ -432,6 +433,32 @@ int mxfa_run_prefill(const mxfa_prefill_shape *s, const void *q, const void *kca
     if (rc != MXFA_OK) return rc;
     const Params p = prefill_params(s, q, kcache, vcache, out);
     return from_hip(mxfa::launch_fwd(p, s->dtype == MXFA_BF16, s->head_dim, 1, static_cast<hipStream_t>(stream)));
+}
+
+size_t mxfa_prefill_workspace_bytes(const mxfa_prefill_shape *s) {
+    if (mxfa_check_prefill(s) != MXFA_OK) return 0;
+    const Params p = prefill_params(s, nullptr, nullptr, nullptr, nullptr);
+    const int dtype_bf16 = s->dtype == MXFA_BF16;
+    return mxfa::fwd_split_workspace_bytes(p, s->head_dim, mxfa::fwd_splits(p, dtype_bf16, s->head_dim));
+}
+
+int mxfa_run_prefill_ws(const mxfa_prefill_shape *s, const void *q, const void *kcache, const void *vcache, void *out,
+                        void *workspace, size_t workspace_bytes, void *stream) {
+    int rc = mxfa_check_prefill(s);
+    if (rc != MXFA_OK) return rc;
+    rc = check_ptrs({q, kcache, vcache, out});
+    if (rc != MXFA_OK) return rc;
+    Params p = prefill_params(s, q, kcache, vcache, out);
+    const int dtype_bf16 = s->dtype == MXFA_BF16;
+    const int splits = mxfa::fwd_splits(p, dtype_bf16, s->head_dim);
+    const size_t need = mxfa::fwd_split_workspace_bytes(p, s->head_dim, splits);
+    if (splits <= 1)  // the unsplit launch: no workspace needed or read
+        return from_hip(mxfa::launch_fwd(p, dtype_bf16, s->head_dim, 1, static_cast<hipStream_t>(stream)));
+    if (workspace == nullptr) return MXFA_ERR_NULL;
+    if (!aligned16(workspace)) return MXFA_ERR_ALIGN;
+    if (workspace_bytes < need) return MXFA_ERR_WORKSPACE;
+    p.fwd_part = static_cast<float *>(workspace);
+    return from_hip(mxfa::launch_fwd_split(p, dtype_bf16, s->head_dim, splits, static_cast<hipStream_t>(stream)));
 }
 
 int mxfa_run_prefill_paged(const mxfa_prefill_shape *s, const void *q, const void *kcache, const void *vcache,

@@ -236,6 +236,36 @@ def test_prefill_paged_null_and_alignment(lib):
     assert lib.mxfa_run_prefill_paged(ctypes.byref(_prefill(head_dim=96)), ok, ok, ok, ok, ok, 16, None) == -4
 
 
+@pytest.mark.parametrize("kw,splits", [
+    (dict(n_tok=512, pos0=3584), 7),               # Qwen2.5 chunk after history: 112 work-groups, 64 stages
+    (dict(n_tok=1, pos0=1777), 7),                 # one row: 28 stages, at least 4 a split
+    (dict(n_tok=1, pos0=777), 1),                  # 13 stages: too few for bf16 ...
+    (dict(n_tok=1, pos0=777, dtype=mx.MXFA_F32), 3),  # ... not for fp32
+    (dict(n_tok=512, pos0=0), 1),                  # 8 stages
+    (dict(n_tok=1, pos0=0), 1),                    # one stage: no split
+    (dict(n_tok=4096, pos0=0), 1),                 # 896 work-groups fill the GPU
+    (dict(n_tok=960, pos0=100, n_head=1, n_kv_head=1, q_stride=3 * 64, kv_stride=64, out_stride=64), 4),
+    (dict(n_tok=100, pos0=100000, n_head=1, n_kv_head=1, q_stride=3 * 64, kv_stride=64, out_stride=64), 16),
+])
+def test_prefill_split_workspace(lib, kw, splits):
+    """The split prefill's workspace: splits x rows x (head_dim + 2) fp32, 0 when no split pays."""
+    sh = _prefill(**kw)
+    want = 0 if splits == 1 else splits * sh.n_head * sh.n_tok * (sh.head_dim + 2) * 4
+    assert lib.mxfa_prefill_workspace_bytes(ctypes.byref(sh)) == want
+    assert lib.mxfa_prefill_workspace_bytes(ctypes.byref(_prefill(n_tok=0))) == 0
+
+
+def test_prefill_split_argument_checks(lib):
+    """A split shape needs an aligned workspace of the reported size; checked before any launch."""
+    sh = _prefill(n_tok=512, pos0=3584)
+    need = lib.mxfa_prefill_workspace_bytes(ctypes.byref(sh))
+    ok = ctypes.c_void_p(4096)
+    assert lib.mxfa_run_prefill_ws(ctypes.byref(sh), ok, ok, ok, ok, None, need, None) == -1
+    assert lib.mxfa_run_prefill_ws(ctypes.byref(sh), ok, ok, ok, ok, ctypes.c_void_p(4104), need, None) == -5
+    assert lib.mxfa_run_prefill_ws(ctypes.byref(sh), ok, ok, ok, ok, ok, need - 4, None) == -8
+    assert lib.mxfa_run_prefill_ws(ctypes.byref(_prefill(head_dim=96)), ok, ok, ok, ok, ok, need, None) == -4
+
+
 def test_probe_argument_checks(lib):
     """The probes validate before launching (no device needed for these)."""
     import ctypes
