@@ -186,7 +186,8 @@ def prefill_table():
     contiguous cache (mxfa_run_prefill; mxfa_run_prefill_ws, its keys split
     over work-groups where the query blocks alone would not fill the GPU) and
     a paged one (mxfa_run_prefill_paged, 16-row blocks in shuffled order, the
-    engine's KV_BLOCK), fp32 (the engine's cache) and bf16. Token-major rows, a fused QKV buffer as the engine has; median of
+    engine's KV_BLOCK; mxfa_run_prefill_paged_ws split), fp32 (the engine's
+    cache) and bf16. Token-major rows, a fused QKV buffer as the engine has; median of
     per-call event pairs after warm-up (mx.time_median_ms), which for the
     short launches holds the host's time to issue the call (the kernels'
     own durations: rocprofv3 --kernel-trace of this mode). TFLOP/s: the
@@ -222,15 +223,21 @@ def prefill_table():
                 ws = mx.run_prefill_split(q, kc, vc, out, pos0, nh, nkv, hd)
                 split = mx.time_median_ms(lambda: mx.run_prefill_split(q, kc, vc, out, pos0, nh, nkv, hd,
                                                                        workspace=ws), warmup=20, iters=21)
+                mx.run_prefill_paged(q, kp, vp, out, perm, bs, pos0, nh, nkv, hd, split=True, workspace=ws)
+                psplit = mx.time_median_ms(lambda: mx.run_prefill_paged(q, kp, vp, out, perm, bs, pos0, nh, nkv, hd,
+                                                                        split=True, workspace=ws),
+                                           warmup=20, iters=21)
                 nsplit = mx.prefill_workspace_bytes(n_tok, pos0, nh, nkv, hd, dt == torch.bfloat16) // \
                     (nh * n_tok * (hd + 2) * 4)
                 rows.append({"model": model, "n_head": nh, "n_kv_head": nkv, "head_dim": hd, "n_tok": n_tok,
                              "pos0": pos0, "dtype": "bf16" if dt == torch.bfloat16 else "f32",
                              "contiguous_call_us": round(contig * 1e3, 1), "paged_call_us": round(paged * 1e3, 1),
                              "key_splits": max(nsplit, 1), "split_call_us": round(split * 1e3, 1),
+                             "paged_split_call_us": round(psplit * 1e3, 1),
                              "contiguous_tflops": round(flops / (contig * 1e-3) / 1e12, 1),
                              "paged_tflops": round(flops / (paged * 1e-3) / 1e12, 1),
-                             "split_tflops": round(flops / (split * 1e-3) / 1e12, 1)})
+                             "split_tflops": round(flops / (split * 1e-3) / 1e12, 1),
+                             "paged_split_tflops": round(flops / (psplit * 1e-3) / 1e12, 1)})
                 print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
     print(json.dumps({"prefill_table": rows, "block_size": 16}), flush=True)
 

@@ -342,6 +342,15 @@ int mxfa_run_prefill_paged(const mxfa_prefill_shape *shape, const void *q, const
 size_t mxfa_prefill_workspace_bytes(const mxfa_prefill_shape *shape);
 int mxfa_run_prefill_ws(const mxfa_prefill_shape *shape, const void *q, const void *kcache, const void *vcache,
                         void *out, void *workspace, size_t workspace_bytes, void *stream);
+/* mxfa_run_prefill_paged with the same key split (replaces the
+ * `attn_prefill_paged` launch, llm.cu:3827-3836, gpu.rs:3270-3289): the
+ * paged cache arguments of mxfa_run_prefill_paged and the workspace of
+ * mxfa_run_prefill_ws, sized by mxfa_prefill_workspace_bytes(shape) (the
+ * same for both caches). Outputs are bitwise those of mxfa_run_prefill_ws over
+ * the gathered, contiguous cache. */
+int mxfa_run_prefill_paged_ws(const mxfa_prefill_shape *shape, const void *q, const void *kcache,
+                              const void *vcache, void *out, const int *block_table, int block_size,
+                              void *workspace, size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -55,7 +55,7 @@ EXPORTS = (
     "mxfa_run_bwd_dkv", "mxfa_run_bwd_flash", "mxfa_run_bwd_dq_delta", "mxfa_run_bwd", "mxfa_bwd_one_launch", "mxfa_bwd_workspace_bytes",
     "mxfa_run_bwd_dkv_ws", "mxfa_run_bwd_ws", "mxfa_run_bwd_naive",
     "mxfa_naive_scratch_bytes", "mxfa_run_naive_fwd", "mxfa_check_prefill", "mxfa_run_prefill",
-    "mxfa_run_prefill_paged", "mxfa_prefill_workspace_bytes", "mxfa_run_prefill_ws",
+    "mxfa_run_prefill_paged", "mxfa_prefill_workspace_bytes", "mxfa_run_prefill_ws", "mxfa_run_prefill_paged_ws",
     "mxfa_set_bwd_options", "mxfa_get_bwd_options", "mxfa_bwd_delta_fallbacks",
     "mxfa_run_bwd_noalloc", "mxfa_bwd_noalloc_scratch_bytes",
 )
@@ -149,6 +149,7 @@ def load_library(path: str | None = None):
     lib.mxfa_prefill_workspace_bytes.argtypes = [pp]
     lib.mxfa_prefill_workspace_bytes.restype = ctypes.c_size_t
     lib.mxfa_run_prefill_ws.argtypes = [pp, vp, vp, vp, vp, vp, ctypes.c_size_t, vp]
+    lib.mxfa_run_prefill_paged_ws.argtypes = [pp, vp, vp, vp, vp, vp, ctypes.c_int, vp, ctypes.c_size_t, vp]
     lib.mxfa_probe_sink_len.argtypes = []
     lib.mxfa_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_int, fp, ctypes.POINTER(ctypes.c_double), vp]
     lib.mxfa_probe_mfma32.argtypes = [ctypes.c_int, fp, ctypes.POINTER(ctypes.c_double), vp]
@@ -509,7 +510,8 @@ def run_prefill(q, kcache, vcache, out, pos0: int, n_head: int, n_kv_head: int, 
 
 
 def run_prefill_paged(q, kcache, vcache, out, block_table, block_size: int, pos0: int, n_head: int,
-                      n_kv_head: int, head_dim: int = 64, scale: float = 0.0, stream=None):
+                      n_kv_head: int, head_dim: int = 64, scale: float = 0.0, stream=None, split: bool = False,
+                      workspace=None):
     """mxfa_run_prefill_paged, run_prefill over a paged KV cache
     (attn_prefill_paged, 03-llm-engine/kernels/llm.cu:3827-3836): logical
     position t sits in cache row block_table[t // block_size] * block_size +
@@ -519,7 +521,11 @@ def run_prefill_paged(q, kcache, vcache, out, block_table, block_size: int, pos0
     pool holding every block the table names; block_table: int32 device tensor
     with at least ceil((pos0 + n_tok) / block_size) entries; block_size: a power
     of two. The rest as run_prefill; the outputs equal run_prefill's over the
-    gathered cache bit for bit."""
+    gathered cache bit for bit.
+
+    split=True: mxfa_run_prefill_paged_ws, the keys split as run_prefill_split
+    does (workspace as there, allocated here when None and returned); its
+    outputs equal run_prefill_split's over the gathered cache bit for bit."""
     torch = _torch()
     if q.dtype not in (torch.bfloat16, torch.float32):
         raise ValueError(f"q: dtype {q.dtype}; bf16 or float32 expected")
@@ -540,10 +546,29 @@ def run_prefill_paged(q, kcache, vcache, out, block_table, block_size: int, pos0
         raise ValueError(f"block_table: {block_table.numel()} entries, positions 0..{pos0 + n_tok - 1} need {need}")
     sh = MxfaPrefillShape(n_tok, n_head, n_kv_head, head_dim, pos0, qs, ks, os_,
                           MXFA_BF16 if q.dtype == torch.bfloat16 else MXFA_F32, scale)
-    _check("mxfa_run_prefill_paged",
-           load_library().mxfa_run_prefill_paged(ctypes.byref(sh), qp, kp, vp, op,
-                                                 ctypes.c_void_p(block_table.data_ptr()), int(block_size),
-                                                 _stream(stream)))
+    lib = load_library()
+    if not split:
+        _check("mxfa_run_prefill_paged",
+               lib.mxfa_run_prefill_paged(ctypes.byref(sh), qp, kp, vp, op, ctypes.c_void_p(block_table.data_ptr()),
+                                          int(block_size), _stream(stream)))
+        return None
+    workspace = _split_workspace(lib, sh, workspace, q.device)
+    _check("mxfa_run_prefill_paged_ws",
+           lib.mxfa_run_prefill_paged_ws(ctypes.byref(sh), qp, kp, vp, op, ctypes.c_void_p(block_table.data_ptr()),
+                                         int(block_size), ctypes.c_void_p(workspace.data_ptr()),
+                                         workspace.numel() * workspace.element_size(), _stream(stream)))
+    return workspace
+
+
+def _split_workspace(lib, sh, workspace, device):
+    """The split prefill's workspace: `workspace` checked, or a new one of the size the shape needs."""
+    torch = _torch()
+    if workspace is None:
+        need = int(lib.mxfa_prefill_workspace_bytes(ctypes.byref(sh)))
+        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=device)
+    if not isinstance(workspace, torch.Tensor) or workspace.device.type != "cuda" or not workspace.is_contiguous():
+        raise ValueError("workspace: expected a contiguous device tensor")
+    return workspace
 
 
 def prefill_workspace_bytes(n_tok: int, pos0: int, n_head: int, n_kv_head: int, head_dim: int = 64,
@@ -577,11 +602,7 @@ def run_prefill_split(q, kcache, vcache, out, pos0: int, n_head: int, n_kv_head:
     sh = MxfaPrefillShape(n_tok, n_head, n_kv_head, head_dim, pos0, qs, ks, os_,
                           MXFA_BF16 if q.dtype == torch.bfloat16 else MXFA_F32, scale)
     lib = load_library()
-    need = int(lib.mxfa_prefill_workspace_bytes(ctypes.byref(sh)))
-    if workspace is None:
-        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=q.device)
-    if not isinstance(workspace, torch.Tensor) or workspace.device.type != "cuda" or not workspace.is_contiguous():
-        raise ValueError("workspace: expected a contiguous device tensor")
+    workspace = _split_workspace(lib, sh, workspace, q.device)
     have = workspace.numel() * workspace.element_size()
     _check("mxfa_run_prefill_ws",
            lib.mxfa_run_prefill_ws(ctypes.byref(sh), qp, kp, vp, op, ctypes.c_void_p(workspace.data_ptr()),

@@ -551,11 +551,14 @@ MXFA_FWD_PG(mxfa_fwd_b128_c_w2_q1_pg, PolBF16<128>, 2, 1)
 MXFA_FWD_PG(mxfa_fwd_f64_c_w2_q1_pg, PolF32<64>, 2, 1)
 // the prefill split over its keys (causal, 64-query work-groups) and the
 // merge of the splits
-#define MXFA_FWD_SP(NAME, POL, WPS)                                                                    \
-    extern "C" __global__ __launch_bounds__(256, WPS) void NAME(Params p) { fwd_entry<POL, true, 1, false, true>(p); }
-MXFA_FWD_SP(mxfa_fwd_b64_c_w3_q1_sp, PolBF16<64>, 3)
-MXFA_FWD_SP(mxfa_fwd_b128_c_w2_q1_sp, PolBF16<128>, 2)
-MXFA_FWD_SP(mxfa_fwd_f64_c_w2_q1_sp, PolF32<64>, 2)
+#define MXFA_FWD_SP(NAME, POL, WPS, PG)                                                                \
+    extern "C" __global__ __launch_bounds__(256, WPS) void NAME(Params p) { fwd_entry<POL, true, 1, PG, true>(p); }
+MXFA_FWD_SP(mxfa_fwd_b64_c_w3_q1_sp, PolBF16<64>, 3, false)
+MXFA_FWD_SP(mxfa_fwd_b128_c_w2_q1_sp, PolBF16<128>, 2, false)
+MXFA_FWD_SP(mxfa_fwd_f64_c_w2_q1_sp, PolF32<64>, 2, false)
+MXFA_FWD_SP(mxfa_fwd_b64_c_w3_q1_pg_sp, PolBF16<64>, 3, true)
+MXFA_FWD_SP(mxfa_fwd_b128_c_w2_q1_pg_sp, PolBF16<128>, 2, true)
+MXFA_FWD_SP(mxfa_fwd_f64_c_w2_q1_pg_sp, PolF32<64>, 2, true)
 #define MXFA_FWD_MERGE(NAME, T, D)                                                                     \
     extern "C" __global__ __launch_bounds__(256) void NAME(Params p, int splits) { fwd_merge_body<T, D>(p, splits); }
 MXFA_FWD_MERGE(mxfa_fwd_merge_b64, u16, 64)
@@ -645,10 +648,12 @@ size_t fwd_split_workspace_bytes(const Params &p, int d, int splits) {
 }
 
 hipError_t launch_fwd_split(const Params &p, int dtype_bf16, int d, int splits, hipStream_t stream) {
-    if (p.fwd_part == nullptr || splits < 2 || splits > kFwdMaxSplits || p.block_table != nullptr)
-        return hipErrorInvalidValue;
-    const KernelId kf = dtype_bf16 ? (d == 64 ? k_mxfa_fwd_b64_c_w3_q1_sp : k_mxfa_fwd_b128_c_w2_q1_sp)
-                                   : k_mxfa_fwd_f64_c_w2_q1_sp;
+    if (p.fwd_part == nullptr || splits < 2 || splits > kFwdMaxSplits) return hipErrorInvalidValue;
+    const bool pg = p.block_table != nullptr;
+    const KernelId kf =
+        dtype_bf16 ? (d == 64 ? (pg ? k_mxfa_fwd_b64_c_w3_q1_pg_sp : k_mxfa_fwd_b64_c_w3_q1_sp)
+                              : (pg ? k_mxfa_fwd_b128_c_w2_q1_pg_sp : k_mxfa_fwd_b128_c_w2_q1_sp))
+                   : (pg ? k_mxfa_fwd_f64_c_w2_q1_pg_sp : k_mxfa_fwd_f64_c_w2_q1_sp);
     const KernelId km = dtype_bf16 ? (d == 64 ? k_mxfa_fwd_merge_b64 : k_mxfa_fwd_merge_b128) : k_mxfa_fwd_merge_f64;
     Params q = p;
     void *args[] = {&q};

@@ -19,6 +19,7 @@
     X(mxfa_fwd_b64_c_w2_q2_pg) X(mxfa_fwd_b64_c_w3_q1_pg) X(mxfa_fwd_b128_c_w2_q1_pg)          \
     X(mxfa_fwd_f64_c_w2_q1_pg)                                                                \
     X(mxfa_fwd_b64_c_w3_q1_sp) X(mxfa_fwd_b128_c_w2_q1_sp) X(mxfa_fwd_f64_c_w2_q1_sp)          \
+    X(mxfa_fwd_b64_c_w3_q1_pg_sp) X(mxfa_fwd_b128_c_w2_q1_pg_sp) X(mxfa_fwd_f64_c_w2_q1_pg_sp) \
     X(mxfa_fwd_merge_b64) X(mxfa_fwd_merge_b128) X(mxfa_fwd_merge_f64)                        \
     /* backward (fa_bwd.hip) */                                                               \
     X(mxfa_preprocess_b64) X(mxfa_preprocess_b128) X(mxfa_preprocess_f64)                     \

@@ -435,6 +435,40 @@ int mxfa_run_prefill(const mxfa_prefill_shape *s, const void *q, const void *kca
     return from_hip(mxfa::launch_fwd(p, s->dtype == MXFA_BF16, s->head_dim, 1, static_cast<hipStream_t>(stream)));
 }
 
+namespace {
+// The checks and parameters of a paged prefill (MXFA_OK and *p set, or the status).
+int paged_params(const mxfa_prefill_shape *s, const void *q, const void *kcache, const void *vcache, void *out,
+                 const int *block_table, int block_size, Params *p) {
+    int rc = mxfa_check_prefill(s);
+    if (rc != MXFA_OK) return rc;
+    rc = check_ptrs({q, kcache, vcache, out});
+    if (rc != MXFA_OK) return rc;
+    if (block_table == nullptr) return MXFA_ERR_NULL;
+    if (reinterpret_cast<uintptr_t>(block_table) % alignof(int) != 0) return MXFA_ERR_ALIGN;
+    // block sizes are powers of two (the reference engine's is 16)
+    if (block_size < 1 || block_size > (1 << 24) || (block_size & (block_size - 1)) != 0) return MXFA_ERR_UNSUPPORTED;
+    *p = prefill_params(s, q, kcache, vcache, out);
+    p->block_table = block_table;
+    while ((1 << p->bs_shift) < block_size) ++p->bs_shift;
+    return MXFA_OK;
+}
+
+// The split launch when the shape gains from one, else the unsplit one
+// (p.block_table, if set, selects the paged kernels).
+int run_prefill_maybe_split(const mxfa_prefill_shape *s, Params p, void *workspace, size_t workspace_bytes,
+                            void *stream) {
+    const int dtype_bf16 = s->dtype == MXFA_BF16;
+    const int splits = mxfa::fwd_splits(p, dtype_bf16, s->head_dim);
+    if (splits <= 1)  // the unsplit launch: no workspace needed or read
+        return from_hip(mxfa::launch_fwd(p, dtype_bf16, s->head_dim, 1, static_cast<hipStream_t>(stream)));
+    if (workspace == nullptr) return MXFA_ERR_NULL;
+    if (!aligned16(workspace)) return MXFA_ERR_ALIGN;
+    if (workspace_bytes < mxfa::fwd_split_workspace_bytes(p, s->head_dim, splits)) return MXFA_ERR_WORKSPACE;
+    p.fwd_part = static_cast<float *>(workspace);
+    return from_hip(mxfa::launch_fwd_split(p, dtype_bf16, s->head_dim, splits, static_cast<hipStream_t>(stream)));
+}
+}  // namespace
+
 size_t mxfa_prefill_workspace_bytes(const mxfa_prefill_shape *s) {
     if (mxfa_check_prefill(s) != MXFA_OK) return 0;
     const Params p = prefill_params(s, nullptr, nullptr, nullptr, nullptr);
@@ -448,33 +482,24 @@ int mxfa_run_prefill_ws(const mxfa_prefill_shape *s, const void *q, const void *
     if (rc != MXFA_OK) return rc;
     rc = check_ptrs({q, kcache, vcache, out});
     if (rc != MXFA_OK) return rc;
-    Params p = prefill_params(s, q, kcache, vcache, out);
-    const int dtype_bf16 = s->dtype == MXFA_BF16;
-    const int splits = mxfa::fwd_splits(p, dtype_bf16, s->head_dim);
-    const size_t need = mxfa::fwd_split_workspace_bytes(p, s->head_dim, splits);
-    if (splits <= 1)  // the unsplit launch: no workspace needed or read
-        return from_hip(mxfa::launch_fwd(p, dtype_bf16, s->head_dim, 1, static_cast<hipStream_t>(stream)));
-    if (workspace == nullptr) return MXFA_ERR_NULL;
-    if (!aligned16(workspace)) return MXFA_ERR_ALIGN;
-    if (workspace_bytes < need) return MXFA_ERR_WORKSPACE;
-    p.fwd_part = static_cast<float *>(workspace);
-    return from_hip(mxfa::launch_fwd_split(p, dtype_bf16, s->head_dim, splits, static_cast<hipStream_t>(stream)));
+    return run_prefill_maybe_split(s, prefill_params(s, q, kcache, vcache, out), workspace, workspace_bytes, stream);
 }
 
 int mxfa_run_prefill_paged(const mxfa_prefill_shape *s, const void *q, const void *kcache, const void *vcache,
                            void *out, const int *block_table, int block_size, void *stream) {
-    int rc = mxfa_check_prefill(s);
+    Params p;
+    const int rc = paged_params(s, q, kcache, vcache, out, block_table, block_size, &p);
     if (rc != MXFA_OK) return rc;
-    rc = check_ptrs({q, kcache, vcache, out});
-    if (rc != MXFA_OK) return rc;
-    if (block_table == nullptr) return MXFA_ERR_NULL;
-    if (reinterpret_cast<uintptr_t>(block_table) % alignof(int) != 0) return MXFA_ERR_ALIGN;
-    // block sizes are powers of two (the reference engine's is 16)
-    if (block_size < 1 || block_size > (1 << 24) || (block_size & (block_size - 1)) != 0) return MXFA_ERR_UNSUPPORTED;
-    Params p = prefill_params(s, q, kcache, vcache, out);
-    p.block_table = block_table;
-    while ((1 << p.bs_shift) < block_size) ++p.bs_shift;
     return from_hip(mxfa::launch_fwd(p, s->dtype == MXFA_BF16, s->head_dim, 1, static_cast<hipStream_t>(stream)));
+}
+
+int mxfa_run_prefill_paged_ws(const mxfa_prefill_shape *s, const void *q, const void *kcache, const void *vcache,
+                              void *out, const int *block_table, int block_size, void *workspace,
+                              size_t workspace_bytes, void *stream) {
+    Params p;
+    const int rc = paged_params(s, q, kcache, vcache, out, block_table, block_size, &p);
+    if (rc != MXFA_OK) return rc;
+    return run_prefill_maybe_split(s, p, workspace, workspace_bytes, stream);
 }
 
 int mxfa_probe_sink_len(void) { return mxfa::probe_sink_len(); }

@@ -264,6 +264,11 @@ def test_prefill_split_argument_checks(lib):
     assert lib.mxfa_run_prefill_ws(ctypes.byref(sh), ok, ok, ok, ok, ctypes.c_void_p(4104), need, None) == -5
     assert lib.mxfa_run_prefill_ws(ctypes.byref(sh), ok, ok, ok, ok, ok, need - 4, None) == -8
     assert lib.mxfa_run_prefill_ws(ctypes.byref(_prefill(head_dim=96)), ok, ok, ok, ok, ok, need, None) == -4
+    # paged: the paged checks first, then the workspace's
+    assert lib.mxfa_run_prefill_paged_ws(ctypes.byref(sh), ok, ok, ok, ok, None, 16, ok, need, None) == -1
+    assert lib.mxfa_run_prefill_paged_ws(ctypes.byref(sh), ok, ok, ok, ok, ok, 24, ok, need, None) == -4
+    assert lib.mxfa_run_prefill_paged_ws(ctypes.byref(sh), ok, ok, ok, ok, ok, 16, None, need, None) == -1
+    assert lib.mxfa_run_prefill_paged_ws(ctypes.byref(sh), ok, ok, ok, ok, ok, 16, ok, need - 4, None) == -8
 
 
 def test_probe_argument_checks(lib):

@@ -1,7 +1,8 @@
 """GPU parity of the prefill over a paged KV cache (mxfa_run_prefill_paged, the
 MI355X counterpart of attn_prefill_paged, 03-llm-engine/kernels/llm.cu:3827-3836).
 
-The cache's blocks sit in a pool in shuffled order, among unused blocks filled
+The same for the key split (mxfa_run_prefill_paged_ws against
+mxfa_run_prefill_ws). The cache's blocks sit in a pool in shuffled order, among unused blocks filled
 with NaN (a read through a wrong entry would show); the block table maps each
 logical block to its physical one, as the engine's does (kv_row<true>,
 llm.cu:959-963). Two checks:
@@ -24,7 +25,7 @@ from gpu_helpers import ORACLE_THREADS, TOL_BF16, TOL_F32, rel_err
 pytestmark = pytest.mark.gpu
 
 
-def _paged_case(n_tok, pos0, nh, nkv, hd, bs, bf16, seed=0, check_oracle=False, spare_blocks=7):
+def _paged_case(n_tok, pos0, nh, nkv, hd, bs, bf16, seed=0, check_oracle=False, spare_blocks=7, split=False):
     import torch
     import mx230_amd as mx
     rng = np.random.default_rng(seed)
@@ -56,9 +57,15 @@ def _paged_case(n_tok, pos0, nh, nkv, hd, bs, bf16, seed=0, check_oracle=False, 
     table = torch.from_numpy(perm).to("cuda")
     out_c = torch.full((n_tok, nh * hd), 7.0, device="cuda", dtype=dt)
     out_p = torch.full((n_tok, nh * hd), 7.0, device="cuda", dtype=dt)
-    print(f"\n[prefill paged] n_tok={n_tok} pos0={pos0} Hq={nh} Hkv={nkv} d={hd} bs={bs} bf16={bf16}", flush=True)
-    mx.run_prefill(tqkv[:, :nh * hd], tk, tv, out_c, pos0, nh, nkv, hd)
-    mx.run_prefill_paged(tqkv[:, :nh * hd], tkp, tvp, out_p, table, bs, pos0, nh, nkv, hd)
+    print(f"\n[prefill paged] n_tok={n_tok} pos0={pos0} Hq={nh} Hkv={nkv} d={hd} bs={bs} bf16={bf16} "
+          f"split={split}", flush=True)
+    if split:
+        assert mx.prefill_workspace_bytes(n_tok, pos0, nh, nkv, hd, bf16) > 0
+        mx.run_prefill_split(tqkv[:, :nh * hd], tk, tv, out_c, pos0, nh, nkv, hd)
+        mx.run_prefill_paged(tqkv[:, :nh * hd], tkp, tvp, out_p, table, bs, pos0, nh, nkv, hd, split=True)
+    else:
+        mx.run_prefill(tqkv[:, :nh * hd], tk, tv, out_c, pos0, nh, nkv, hd)
+        mx.run_prefill_paged(tqkv[:, :nh * hd], tkp, tvp, out_p, table, bs, pos0, nh, nkv, hd)
     torch.cuda.synchronize()
     assert torch.equal(out_p, out_c), "paged prefill differs from the contiguous one"
     got = out_p.float().cpu().numpy()
@@ -95,6 +102,20 @@ def test_paged_d128_bf16():
 def test_paged_large_grid_bf16():
     """768 work-groups of 128 queries: the two-wave 128-query kernel."""
     _paged_case(n_tok=3072, pos0=512, nh=32, nkv=4, hd=64, bs=16, bf16=True, seed=9)
+
+
+@pytest.mark.parametrize("bs", [1, 16, 256])
+@pytest.mark.parametrize("n_tok,pos0", [(512, 3584), (1, 4095), (960, 100)])
+def test_paged_split_equals_contiguous_split_bf16(bs, n_tok, pos0):
+    """The key split over a paged cache: bitwise the split over the gathered one."""
+    nh, nkv = (1, 1) if pos0 == 100 else (14, 2)
+    _paged_case(n_tok=n_tok, pos0=pos0, nh=nh, nkv=nkv, hd=64, bs=bs, bf16=True, seed=bs + n_tok, split=True)
+
+
+def test_paged_split_oracle():
+    """fp32 and d = 128 bf16 splits over a paged cache against the oracle."""
+    _paged_case(n_tok=100, pos0=2000, nh=4, nkv=2, hd=64, bs=16, bf16=False, seed=11, check_oracle=True, split=True)
+    _paged_case(n_tok=96, pos0=1000, nh=8, nkv=1, hd=128, bs=16, bf16=True, seed=12, check_oracle=True, split=True)
 
 
 def test_paged_block_size_refused():
