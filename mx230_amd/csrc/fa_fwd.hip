@@ -472,11 +472,12 @@ __device__ __forceinline__ void fwd_entry(const Params &p) {
 // running maxima (log2 units), O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M)
 // l_s, in split order, written as the forward writes O. A split that holds
 // no key of the row has m = -inf and weight 0. Every load is issued before
-// the first is used (the loops unrolled to kFwdMaxSplits), so a call costs
-// one memory latency rather than one per split.
-constexpr int kFwdMaxSplits = 16;
+// the first is used (the loops unrolled to MAXS >= S), so a call costs one
+// memory latency rather than one per split; MAXS = 8 keeps the registers of
+// the common case low (the 32-split form takes 205 VGPRs).
+constexpr int kFwdMaxSplits = 32;
 
-template <class T, int D>
+template <class T, int D, int MAXS>
 __device__ __forceinline__ void fwd_merge_body(const Params &p, int S) {
     constexpr int C = D / 4;
     const size_t rows = (size_t)p.B * p.Hq * p.N;
@@ -485,10 +486,10 @@ __device__ __forceinline__ void fwd_merge_body(const Params &p, int S) {
     const size_t r = t / C;
     const int c = (int)(t % C);
     const float2 *ml = reinterpret_cast<const float2 *>(p.fwd_part + (size_t)S * rows * D);
-    float2 v[kFwdMaxSplits];
-    float4 a[kFwdMaxSplits];
+    float2 v[MAXS];
+    float4 a[MAXS];
 #pragma unroll
-    for (int sp = 0; sp < kFwdMaxSplits; ++sp) {
+    for (int sp = 0; sp < MAXS; ++sp) {
         if (sp < S) {
             v[sp] = ml[sp * rows + r];
             a[sp] = *reinterpret_cast<const float4 *>(p.fwd_part + (sp * rows + r) * D + 4 * c);
@@ -497,11 +498,11 @@ __device__ __forceinline__ void fwd_merge_body(const Params &p, int S) {
     // the split holding key 0 (visible to every row) makes M finite
     float M = -INFINITY;
 #pragma unroll
-    for (int sp = 0; sp < kFwdMaxSplits; ++sp) M = sp < S ? fmaxf(M, v[sp].x) : M;
+    for (int sp = 0; sp < MAXS; ++sp) M = sp < S ? fmaxf(M, v[sp].x) : M;
     float L = 0.f;
     f32x4 o = zero4();
 #pragma unroll
-    for (int sp = 0; sp < kFwdMaxSplits; ++sp) {
+    for (int sp = 0; sp < MAXS; ++sp) {
         if (sp < S) {
             const float w = fast_exp2(v[sp].x - M);
             L += w * v[sp].y;
@@ -559,11 +560,16 @@ MXFA_FWD_SP(mxfa_fwd_f64_c_w2_q1_sp, PolF32<64>, 2, false)
 MXFA_FWD_SP(mxfa_fwd_b64_c_w3_q1_pg_sp, PolBF16<64>, 3, true)
 MXFA_FWD_SP(mxfa_fwd_b128_c_w2_q1_pg_sp, PolBF16<128>, 2, true)
 MXFA_FWD_SP(mxfa_fwd_f64_c_w2_q1_pg_sp, PolF32<64>, 2, true)
-#define MXFA_FWD_MERGE(NAME, T, D)                                                                     \
-    extern "C" __global__ __launch_bounds__(256) void NAME(Params p, int splits) { fwd_merge_body<T, D>(p, splits); }
-MXFA_FWD_MERGE(mxfa_fwd_merge_b64, u16, 64)
-MXFA_FWD_MERGE(mxfa_fwd_merge_b128, u16, 128)
-MXFA_FWD_MERGE(mxfa_fwd_merge_f64, float, 64)
+#define MXFA_FWD_MERGE(NAME, T, D, MAXS)                                                               \
+    extern "C" __global__ __launch_bounds__(256) void NAME(Params p, int splits) {                     \
+        fwd_merge_body<T, D, MAXS>(p, splits);                                                         \
+    }
+MXFA_FWD_MERGE(mxfa_fwd_merge8_b64, u16, 64, 8)
+MXFA_FWD_MERGE(mxfa_fwd_merge8_b128, u16, 128, 8)
+MXFA_FWD_MERGE(mxfa_fwd_merge8_f64, float, 64, 8)
+MXFA_FWD_MERGE(mxfa_fwd_merge32_b64, u16, 64, kFwdMaxSplits)
+MXFA_FWD_MERGE(mxfa_fwd_merge32_b128, u16, 128, kFwdMaxSplits)
+MXFA_FWD_MERGE(mxfa_fwd_merge32_f64, float, 64, kFwdMaxSplits)
 #undef MXFA_FWD
 #undef MXFA_FWD_PG
 #undef MXFA_FWD_SP
@@ -630,7 +636,7 @@ static hipError_t launch_fwd_t(const Params &p, hipStream_t stream) {
 // the merging launch costs more than the split saves (measured on the MI355X,
 // Qwen2.5 heads, 512 tokens at position 0, 8 stages: bf16 19.7 -> 24.6 us
 // with 2 splits, fp32 36.5 -> 32.6 us); else enough to fill them, with at
-// least 4 key stages per split and at most 16 splits.
+// least 2 key stages per split and at most kFwdMaxSplits splits.
 int fwd_splits(const Params &p, int dtype_bf16, int d) {
     const long long wgs = (long long)p.B * p.Hq * ((p.N + 63) / 64);
     const long long slots = 256LL * (dtype_bf16 && d == 64 ? 3 : 2);
@@ -638,7 +644,7 @@ int fwd_splits(const Params &p, int dtype_bf16, int d) {
     const long long stages = (std::min(p.Nk, p.pos0 + p.N) + 63) / 64;  // the heaviest block's
     if (stages < (dtype_bf16 ? 16 : 8)) return 1;
     long long s = (slots + wgs - 1) / wgs;
-    s = std::min(s, std::max(1LL, stages / 4));
+    s = std::min(s, std::max(1LL, stages / 2));
     return (int)std::min(s, (long long)kFwdMaxSplits);
 }
 
@@ -654,7 +660,10 @@ hipError_t launch_fwd_split(const Params &p, int dtype_bf16, int d, int splits, 
         dtype_bf16 ? (d == 64 ? (pg ? k_mxfa_fwd_b64_c_w3_q1_pg_sp : k_mxfa_fwd_b64_c_w3_q1_sp)
                               : (pg ? k_mxfa_fwd_b128_c_w2_q1_pg_sp : k_mxfa_fwd_b128_c_w2_q1_sp))
                    : (pg ? k_mxfa_fwd_f64_c_w2_q1_pg_sp : k_mxfa_fwd_f64_c_w2_q1_sp);
-    const KernelId km = dtype_bf16 ? (d == 64 ? k_mxfa_fwd_merge_b64 : k_mxfa_fwd_merge_b128) : k_mxfa_fwd_merge_f64;
+    const bool m8 = splits <= 8;
+    const KernelId km = dtype_bf16 ? (d == 64 ? (m8 ? k_mxfa_fwd_merge8_b64 : k_mxfa_fwd_merge32_b64)
+                                              : (m8 ? k_mxfa_fwd_merge8_b128 : k_mxfa_fwd_merge32_b128))
+                                   : (m8 ? k_mxfa_fwd_merge8_f64 : k_mxfa_fwd_merge32_f64);
     Params q = p;
     void *args[] = {&q};
     hipError_t e = launch_kernel(kf, dim3(p.B * p.Hq, (p.N + 63) / 64, splits), dim3(256), args, stream);

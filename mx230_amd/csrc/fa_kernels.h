@@ -20,7 +20,8 @@
     X(mxfa_fwd_f64_c_w2_q1_pg)                                                                \
     X(mxfa_fwd_b64_c_w3_q1_sp) X(mxfa_fwd_b128_c_w2_q1_sp) X(mxfa_fwd_f64_c_w2_q1_sp)          \
     X(mxfa_fwd_b64_c_w3_q1_pg_sp) X(mxfa_fwd_b128_c_w2_q1_pg_sp) X(mxfa_fwd_f64_c_w2_q1_pg_sp) \
-    X(mxfa_fwd_merge_b64) X(mxfa_fwd_merge_b128) X(mxfa_fwd_merge_f64)                        \
+    X(mxfa_fwd_merge8_b64) X(mxfa_fwd_merge8_b128) X(mxfa_fwd_merge8_f64)                     \
+    X(mxfa_fwd_merge32_b64) X(mxfa_fwd_merge32_b128) X(mxfa_fwd_merge32_f64)                  \
     /* backward (fa_bwd.hip) */                                                               \
     X(mxfa_preprocess_b64) X(mxfa_preprocess_b128) X(mxfa_preprocess_f64)                     \
     X(mxfa_dq_b64_c) X(mxfa_dq_b64_c_d) X(mxfa_dq_b64_n) X(mxfa_dq_b64_n_d)                   \

@@ -421,6 +421,19 @@ Params prefill_params(const mxfa_prefill_shape *s, const void *q, const void *kc
     p.q_bs = p.o_bs = p.kv_bs = 0;
     p.Nk = s->pos0 + s->n_tok;
     p.pos0 = s->pos0;
+    if (s->n_tok == 1 && s->n_head > s->n_kv_head) {
+        // A single row (decode-like): the query heads of a GQA group become the
+        // rows of one block per KV head, so each K/V stage staged serves the
+        // whole group instead of one head. Row i sits at column (kvh group + i)
+        // head_dim of the one Q / O row. With Nk = pos0 + 1 every row's causal
+        // limit min(pos0 + i, Nk - 1) is pos0, as the row's own.
+        const int group = s->n_head / s->n_kv_head;
+        p.Hq = s->n_kv_head;
+        p.group = 1;
+        p.N = group;
+        p.q_rs = p.o_rs = s->head_dim;
+        p.q_hs = p.o_hs = (long long)group * s->head_dim;
+    }
     return p;
 }
 }  // namespace

@@ -238,14 +238,14 @@ def test_prefill_paged_null_and_alignment(lib):
 
 @pytest.mark.parametrize("kw,splits", [
     (dict(n_tok=512, pos0=3584), 7),               # Qwen2.5 chunk after history: 112 work-groups, 64 stages
-    (dict(n_tok=1, pos0=1777), 7),                 # one row: 28 stages, at least 4 a split
+    (dict(n_tok=1, pos0=1777), 14),                # one row: 28 stages, at least 2 a split
     (dict(n_tok=1, pos0=777), 1),                  # 13 stages: too few for bf16 ...
-    (dict(n_tok=1, pos0=777, dtype=mx.MXFA_F32), 3),  # ... not for fp32
+    (dict(n_tok=1, pos0=777, dtype=mx.MXFA_F32), 6),  # ... not for fp32
     (dict(n_tok=512, pos0=0), 1),                  # 8 stages
     (dict(n_tok=1, pos0=0), 1),                    # one stage: no split
     (dict(n_tok=4096, pos0=0), 1),                 # 896 work-groups fill the GPU
-    (dict(n_tok=960, pos0=100, n_head=1, n_kv_head=1, q_stride=3 * 64, kv_stride=64, out_stride=64), 4),
-    (dict(n_tok=100, pos0=100000, n_head=1, n_kv_head=1, q_stride=3 * 64, kv_stride=64, out_stride=64), 16),
+    (dict(n_tok=960, pos0=100, n_head=1, n_kv_head=1, q_stride=3 * 64, kv_stride=64, out_stride=64), 8),
+    (dict(n_tok=100, pos0=100000, n_head=1, n_kv_head=1, q_stride=3 * 64, kv_stride=64, out_stride=64), 32),
 ])
 def test_prefill_split_workspace(lib, kw, splits):
     """The split prefill's workspace: splits x rows x (head_dim + 2) fp32, 0 when no split pays."""

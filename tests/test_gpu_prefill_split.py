@@ -74,12 +74,12 @@ def _run(n_tok, pos0, nh, nkv, hd, bf16, seed=0, check_oracle=False, expect_spli
 
 
 def test_split_reference_configuration():
-    """fp32, head_dim 64, GQA (the reference's own types): 8 splits of 33 stages."""
+    """fp32, head_dim 64, GQA (the reference's own types): 16 splits of 33 stages."""
     _run(n_tok=100, pos0=2000, nh=4, nkv=2, hd=64, bf16=False, check_oracle=True)
 
 
 def test_split_rows_before_a_split():
-    """64-query blocks straddling stage boundaries (pos0 = 100), 4 splits: the
+    """64-query blocks straddling stage boundaries (pos0 = 100), 8 splits: the
     light blocks' last splits start at their diagonal stage, which some of their
     rows precede entirely."""
     _run(n_tok=960, pos0=100, nh=1, nkv=1, hd=64, bf16=True, seed=1, check_oracle=True)
@@ -91,7 +91,8 @@ def test_split_d128_bf16():
 
 
 def test_split_single_row():
-    """A decode-like call: one query row after 1777 positions (7 splits)."""
+    """A decode-like call: one query row after 1777 positions (14 splits), the
+    GQA group's heads as the rows of one block."""
     _run(n_tok=1, pos0=1777, nh=14, nkv=2, hd=64, bf16=True, seed=4, check_oracle=True)
     _run(n_tok=1, pos0=5000, nh=4, nkv=2, hd=64, bf16=False, seed=5, check_oracle=True)
 
