@@ -6,6 +6,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -387,7 +388,9 @@ int mxfa_check_prefill(const mxfa_prefill_shape *s) {
     if (s->n_tok < 1 || s->n_head < 1 || s->n_kv_head < 1 || s->head_dim < 1 || s->pos0 < 0) return MXFA_ERR_SHAPE;
     if (s->n_head % s->n_kv_head != 0) return MXFA_ERR_SHAPE;
     if (!(s->scale >= 0.0f) || std::isinf(s->scale)) return MXFA_ERR_SHAPE;
-    if ((long long)s->pos0 + s->n_tok > 0x7fffffffLL - 128) return MXFA_ERR_SHAPE;
+    // query positions (pos0 + row, the rows of a single-row call being its
+    // GQA group's heads) stay inside int with a block to spare
+    if ((long long)s->pos0 + std::max(s->n_tok, s->n_head) > 0x7fffffffLL - 128) return MXFA_ERR_SHAPE;
     if (((long long)s->n_tok + 127) / 128 > kMaxGridY) return MXFA_ERR_SHAPE;
     if (s->head_dim != 64 && s->head_dim != 128) return MXFA_ERR_UNSUPPORTED;
     if (s->dtype == MXFA_F32 && s->head_dim != 64) return MXFA_ERR_UNSUPPORTED;

@@ -255,6 +255,15 @@ def test_prefill_split_workspace(lib, kw, splits):
     assert lib.mxfa_prefill_workspace_bytes(ctypes.byref(_prefill(n_tok=0))) == 0
 
 
+def test_prefill_position_limit(lib):
+    """Query positions stay inside int: pos0 plus the rows (a single row's GQA heads included)."""
+    top = 2 ** 31 - 1 - 128
+    assert lib.mxfa_check_prefill(ctypes.byref(_prefill(n_tok=1, pos0=top - 14))) == 0
+    assert lib.mxfa_check_prefill(ctypes.byref(_prefill(n_tok=1, pos0=top - 13))) == -2
+    assert lib.mxfa_check_prefill(ctypes.byref(_prefill(n_tok=100, pos0=top - 100))) == 0
+    assert lib.mxfa_check_prefill(ctypes.byref(_prefill(n_tok=100, pos0=top - 99))) == -2
+
+
 def test_prefill_split_argument_checks(lib):
     """A split shape needs an aligned workspace of the reported size; checked before any launch."""
     sh = _prefill(n_tok=512, pos0=3584)
