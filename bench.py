@@ -78,8 +78,9 @@ def parse():
     ap.add_argument("--config-table", action="store_true",
                     help="forward and backward timings at every BASELINE config (one JSON line)")
     ap.add_argument("--prefill-table", action="store_true",
-                    help="the prefill (mxfa_run_prefill) and the paged prefill (mxfa_run_prefill_paged, "
-                         "16-row blocks) at engine shapes (one JSON line)")
+                    help="the prefill (mxfa_run_prefill), the paged prefill (mxfa_run_prefill_paged, "
+                         "16-row blocks) and both with their keys split (mxfa_run_prefill_ws, "
+                         "mxfa_run_prefill_paged_ws) at engine shapes (one JSON line)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run a plain device-to-device copy of MIB "
                          "MiB three times (calibrates the FETCH_SIZE / WRITE_SIZE counters)")
