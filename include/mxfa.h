@@ -305,7 +305,9 @@ typedef struct {
 } mxfa_prefill_shape;
 
 /* MXFA_OK if the prefill shape is supported; strides whose rows would not start
- * on 16-byte boundaries give MXFA_ERR_ALIGN. */
+ * on 16-byte boundaries give MXFA_ERR_ALIGN, and pos0 + max(n_tok, n_head)
+ * above 2^31 - 129 gives MXFA_ERR_SHAPE (a single row runs its GQA group's
+ * heads as rows at positions pos0, pos0 + 1, ...). */
 int mxfa_check_prefill(const mxfa_prefill_shape *shape);
 int mxfa_run_prefill(const mxfa_prefill_shape *shape, const void *q, const void *kcache, const void *vcache,
                      void *out, void *stream);
