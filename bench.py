@@ -76,7 +76,8 @@ def parse():
                     help="per-work-group timeline of one one-launch backward at the bench shape (timeline build "
                          "of the code object, mxfa_gfx950_timeline.hsaco)")
     ap.add_argument("--config-table", action="store_true",
-                    help="forward and backward timings at every BASELINE config (one JSON line)")
+                    help="forward and backward timings at every BASELINE config (one JSON line); with the CPU path "
+                         "timed per config unless --no-cpu")
     ap.add_argument("--prefill-table", action="store_true",
                     help="the prefill (mxfa_run_prefill), the paged prefill (mxfa_run_prefill_paged, "
                          "16-row blocks) and both with their keys split (mxfa_run_prefill_ws, "
@@ -243,19 +244,69 @@ def prefill_table():
     print(json.dumps({"prefill_table": rows, "block_size": 16}), flush=True)
 
 
-def config_table():
+def cpu_config(B, H, Hkv, N, d, causal, dtype, sc, threads):
+    """The reference's CPU path (cpu_attention, then cpu_attention_bwd,
+    02-flash-attention/src/main.rs:213-300) for one config, timed on the oracle:
+    one (batch, head) slice on one thread, as the reference runs it, scaled to
+    the config's B*H slices; and min(B*H, threads) slices on that many threads
+    (the oracle's multi-head forward and backward), scaled the same way. Inputs
+    seeded N(0,1) (x sc for Q/K/V), rounded to bf16 for a bf16 config; fp32
+    math either way. Above N = 8192 (cfg3: one slice would take minutes) the
+    slices are timed at N = 4096 and scaled by (N / 4096)^2 as well: the
+    path's work per slice is N^2 d. Returns the figures and what was sampled."""
+    import numpy as np
+    import mx230_amd as mx
+    import oracle  # the checker; used here only as the timed CPU baseline
+    lib = oracle.load()
+    nsl = min(B * H, threads)
+    n_full = N
+    if N > 8192:
+        N = 4096
+    nscale = (n_full / N) ** 2
+    q = oracle.normal(nsl * N * d, 11, sc).reshape(1, nsl, N, d)
+    k = oracle.normal(nsl * N * d, 12, sc).reshape(1, nsl, N, d)
+    v = oracle.normal(nsl * N * d, 13, sc).reshape(1, nsl, N, d)
+    do = oracle.normal(nsl * N * d, 14, 1.0).reshape(1, nsl, N, d)
+    if dtype == "bf16":
+        q, k, v, do = (oracle.bf16_round(x) for x in (q, k, v, do))
+    t0 = time.perf_counter()
+    oracle.cpu_attention(q[0, 0], k[0, 0], v[0, 0], N, d, causal, lib=lib)
+    oracle.cpu_attention_bwd(q[0, 0], k[0, 0], v[0, 0], do[0, 0], N, d, causal, lib=lib)
+    t1 = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    oracle.mha_fwd(q, k, v, 1, nsl, nsl, N, d, causal, nthreads=nsl, lib=lib)
+    oracle.mha_bwd(q, k, v, do, 1, nsl, nsl, N, d, causal, nthreads=nsl, lib=lib)
+    tp = time.perf_counter() - t0
+    del np
+    flops = mx.fwd_flops(B, H, n_full, d, causal) + mx.bwd_flops(B, H, n_full, d, causal)
+    whole1 = t1 * B * H * nscale
+    wholep = tp * B * H / nsl * nscale
+    at = f" at N={N}, scaled x{nscale:g} for N={n_full}," if nscale != 1 else ""
+    return {"cpu_1t_s": round(whole1, 2), "cpu_1t_tflops": flops / whole1 / 1e12,
+            "cpu_par_s": round(wholep, 2), "cpu_par_tflops": flops / wholep / 1e12, "cpu_threads": nsl,
+            "cpu_sample": f"fwd+bwd of 1 slice on 1 thread ({t1:.2f} s) and of {nsl} slices on {nsl} threads "
+                          f"({tp:.2f} s){at} each scaled x{B * H}/(slices) to the config's {B * H} slices"}
+
+
+def config_table(cpu=False):
     """Forward (mxfa_run_flash_lse) and backward from O (mxfa_run_bwd_ws: the
     dQ pass with Delta, then dK/dV, split over the query heads of a GQA group
     through its workspace where that applies) at every BASELINE config, each the median of
     20 event-timed runs after 3 warm-ups, inputs resident. TFLOP/s are the
     algorithmic 4 N^2 d (forward) and 10 N^2 d (backward) per (batch, query
-    head), halved when causal; % peak against the dense MFMA peak of the dtype."""
+    head), halved when causal; % peak against the dense MFMA peak of the dtype,
+    and frac_of_measured against the MFMA probe's rate on this box. cpu: each
+    row also carries the reference's CPU path timed on this host (cpu_config:
+    one thread, and one thread per slice over up to 16 slices)."""
     import torch
     import mx230_amd as mx
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     mx.init(0)
     stream = torch.cuda.current_stream()
+    measured = {"bf16": mx.probe_mfma_tflops(True), "f32": mx.probe_mfma_tflops(False)}
+    host = cpu_host()
+    threads = max(1, min(16, os.cpu_count() or 1))
 
     def median_ms(fn, reps=20):
         # warm-up: at least 50 ms of back-to-back calls (the clocks ramp up
@@ -294,13 +345,22 @@ def config_table():
         peak = PEAK_TFLOPS[dtype]
         ftf = mx.fwd_flops(B, H, N, d, causal) / (fwd * 1e-3) / 1e12
         btf = mx.bwd_flops(B, H, N, d, causal) / (bwd * 1e-3) / 1e12
+        meas = measured[dtype]
         rows.append({"config": name, "B": B, "Hq": H, "Hkv": Hkv, "N": N, "d": d, "causal": causal,
                      "dtype": dtype, "workspace_mb": round(nws / 1e6, 1), "fwd_ms": round(fwd, 4), "fwd_tflops": round(ftf, 2),
-                     "fwd_pct_peak": round(100 * ftf / peak, 1), "bwd_ms": round(bwd, 4),
-                     "bwd_tflops": round(btf, 2), "bwd_pct_peak": round(100 * btf / peak, 1)})
-        print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+                     "fwd_pct_peak": round(100 * ftf / peak, 1), "fwd_frac_of_measured": round(ftf / meas, 3),
+                     "bwd_ms": round(bwd, 4), "bwd_tflops": round(btf, 2), "bwd_pct_peak": round(100 * btf / peak, 1),
+                     "bwd_frac_of_measured": round(btf / meas, 3)})
         del q, k, v, do, o, lse, delta, dq, dk, dv, ws
+        if cpu:
+            c = cpu_config(B, H, Hkv, N, d, causal, dtype, sc, threads)
+            c["gpu_vs_cpu_1t"] = round(c["cpu_1t_s"] / ((fwd + bwd) * 1e-3), 1)
+            c["cpu_1t_tflops"] = float(f"{c['cpu_1t_tflops']:.3g}")
+            c["cpu_par_tflops"] = float(f"{c['cpu_par_tflops']:.3g}")
+            rows[-1].update(c)
+        print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
     print(json.dumps({"config_table": rows, "peak_tflops": PEAK_TFLOPS,
+                      "measured_mfma_tflops": {k: round(x, 1) for k, x in measured.items()}, "host": host,
                       "data": "synthetic (seeded N(0,1) on the GPU; Q/K/V x0.5 where BASELINE says so)",
                       "timing": "median of 20 after >= 50 ms of warm-up calls, HIP events on the launch stream"}), flush=True)
 
@@ -595,7 +655,7 @@ def main():
         naive_table()
         return
     if a.config_table:
-        config_table()
+        config_table(cpu=not a.no_cpu)
         return
     if a.prefill_table:
         prefill_table()

@@ -348,6 +348,14 @@ struct DkvTile16 {
     // form issues the loads together, but measured no faster here (they
     // overlap the first stage's loads either way) and made the register
     // allocator spill inside the two-launch dK/dV kernel's stage loops
+    // The score accumulators' start for 4 query rows from their staged LSE.
+    __device__ __forceinline__ f32x4 nl_of(const float *l) const {
+#if MXFA_X_NEGK
+        if (Pol::kExactScale) return *reinterpret_cast<const f32x4 *>(l);
+#endif
+        return *reinterpret_cast<const f32x4 *>(l) * lmul;
+    }
+
     __device__ __forceinline__ void load(const Params &p, const T *K, const T *V, int kw0, int lane) {
         const int g = lane >> 4, l16 = lane & 15;
         const int N = p.N;
@@ -358,17 +366,129 @@ struct DkvTile16 {
             Pol::gmem_row_frags_if(vf[kt], V + (size_t)key * D, g, key < N);
 #pragma unroll
             for (int kc = 0; kc < NC; ++kc) {
+#if MXFA_X_NEGK
+                if (Pol::kExactScale) kf[kt][kc] = Pol::scaled(kf[kt][kc], -p.scale);
+#endif
                 if (!Pol::kExactScale) kf[kt][kc] = Pol::scaled(kf[kt][kc], p.scale_log2);
                 vf[kt][kc] = Pol::neg(vf[kt][kc]);
             }
         }
         lmul = Pol::kExactScale ? -1.0f / p.scale : -kLog2e;
         xmul = p.scale_log2;
+#if MXFA_X_NEGK
+        if (Pol::kExactScale) xmul = -kLog2e;
+#endif
 #pragma unroll
         for (int xt = 0; xt < XT; ++xt) {
 #pragma unroll
             for (int kt = 0; kt < KT; ++kt) accK[xt][kt] = accV[xt][kt] = zero4();
         }
+    }
+
+    // The three parts of one 32-query block, for the pipelined stage: the
+    // scores and dP (first GEMMs, operands from LDS rows), the softmax
+    // recompute and dS (VALU), and the chained dV / dK updates.
+    using ChainB = typename Pol::ChainB;
+    __device__ __forceinline__ void blk_sd(f32x4 (&s)[2][KT], f32x4 (&dp)[2][KT], const T *sq, const T *sdo,
+                                           const float *sl, const float *sd, int blk, int g, int l16) const {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int q4 = 32 * blk + Pol::bidx(t, g, 0);
+            const f32x4 nl = nl_of(sl + q4);
+            const f32x4 dl = *reinterpret_cast<const f32x4 *>(sd + q4);
+            Frag a[NC], b[NC];
+            const int n = 32 * blk + Pol::arow(t, l16);
+            Pol::lds_row_frags(a, sq, n, g);
+            Pol::lds_row_frags(b, sdo, n, g);
+#pragma unroll
+            for (int kt = 0; kt < KT; ++kt) {
+                f32x4 c = nl;
+#pragma unroll
+                for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], kf[kt][kc], c);
+                s[t][kt] = c;
+            }
+#pragma unroll
+            for (int kt = 0; kt < KT; ++kt) {
+                f32x4 c = dl;
+#pragma unroll
+                for (int kc = 0; kc < NC; ++kc) c = Pol::mma(b[kc], vf[kt][kc], c);
+                dp[t][kt] = c;
+            }
+        }
+    }
+    template <bool CAUSAL, bool MASK>
+    __device__ __forceinline__ void blk_sm(f32x4 (&s)[2][KT], f32x4 (&dp)[2][KT], ChainB (&cp)[KT], ChainB (&cds)[KT],
+                                           int qs, int kw0, int blk, int g, int l16) const {
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float x = Pol::kExactScale ? s[t][kt][r] * xmul : s[t][kt][r];
+                    if constexpr (MASK) {
+                        const bool before = Pol::bidx(t, g, r) - l16 < kw0 - qs + 16 * kt - 32 * blk;
+                        x = before ? -INFINITY : x;
+                    }
+                    const float pv = fast_exp2(x);
+                    s[t][kt][r] = pv;
+                    dp[t][kt][r] = pv * dp[t][kt][r];  // -dS / scale
+                }
+            }
+            cp[kt] = Pol::pack(s[0][kt], s[1][kt]);
+            cds[kt] = Pol::pack(dp[0][kt], dp[1][kt]);
+        }
+    }
+    __device__ __forceinline__ void blk_ch(const ChainB (&cp)[KT], const ChainB (&cds)[KT], const T *sq, const T *sdo,
+                                           int blk, int g, int l16) {
+#pragma unroll
+        for (int xt = 0; xt < XT; ++xt) {
+#pragma unroll
+            for (int kt = 0; kt < KT; ++kt) {
+                accV[xt][kt] = Pol::chain(accV[xt][kt], cp[kt], sdo, 16 * xt, 32 * blk, g, l16);
+                accK[xt][kt] = Pol::chain(accK[xt][kt], cds[kt], sq, 16 * xt, 32 * blk, g, l16);
+            }
+        }
+    }
+
+    // The stage's two blocks as a pipeline inside the wave, so the matrix
+    // products of one block issue between the softmax instructions of the
+    // other: scores/dP of block 0; softmax of block 0 with scores/dP of block
+    // 1; chained updates of block 0 with softmax of block 1; chained updates
+    // of block 1. The interleave of each overlapped part is fixed with
+    // scheduling-group barriers (one MFMA, then VALU instructions).
+    template <bool CAUSAL, bool MASK>
+    __device__ __forceinline__ void stage_pipe(const T *sq, const T *sdo, const float *sl, const float *sd, int qs,
+                                               int kw0, int lane) {
+        const int g = lane >> 4, l16 = lane & 15;
+        f32x4 s0[2][KT], dp0[2][KT], s1[2][KT], dp1[2][KT];
+        ChainB cp0[KT], cds0[KT], cp1[KT], cds1[KT];
+        blk_sd(s0, dp0, sq, sdo, sl, sd, 0, g, l16);
+        __builtin_amdgcn_sched_barrier(0);
+        blk_sd(s1, dp1, sq, sdo, sl, sd, 1, g, l16);
+        blk_sm<CAUSAL, MASK>(s0, dp0, cp0, cds0, qs, kw0, 0, g, l16);
+#if MXFA_X_SGB
+        __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);  // block 1's LDS rows, LSE, Delta
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, MXFA_X_SGB, 0);
+        }
+#endif
+        __builtin_amdgcn_sched_barrier(0);
+        blk_ch(cp0, cds0, sq, sdo, 0, g, l16);
+        blk_sm<CAUSAL, MASK>(s1, dp1, cp1, cds1, qs, kw0, 1, g, l16);
+#if MXFA_X_SGB
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+#endif
+        __builtin_amdgcn_sched_barrier(0);
+        blk_ch(cp1, cds1, sq, sdo, 1, g, l16);
     }
 
     // The score accumulators start at L lmul, so they come out as the
@@ -378,6 +498,12 @@ struct DkvTile16 {
     template <bool CAUSAL, bool MASK, bool PRIO>
     __device__ __forceinline__ void stage(const T *sq, const T *sdo, const float *sl, const float *sd, int qs, int kw0,
                                           int lane) {
+#if MXFA_X_DKVPIPE
+        if constexpr (Pol::D == 64 && sizeof(T) == 2) {
+            stage_pipe<CAUSAL, MASK>(sq, sdo, sl, sd, qs, kw0, lane);
+            return;
+        }
+#endif
         const int g = lane >> 4, l16 = lane & 15;
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
@@ -387,7 +513,7 @@ struct DkvTile16 {
             for (int t = 0; t < 2; ++t) {
                 // block rows bidx(t, g, 0..3) are consecutive: one 16-byte LDS read
                 const int q4 = 32 * blk + Pol::bidx(t, g, 0);
-                const f32x4 nl = *reinterpret_cast<const f32x4 *>(sl + q4) * lmul;
+                const f32x4 nl = nl_of(sl + q4);
                 const f32x4 dl = *reinterpret_cast<const f32x4 *>(sd + q4);
                 Frag a[NC];
                 const int n = 32 * blk + Pol::arow(t, l16);

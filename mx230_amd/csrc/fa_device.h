@@ -206,14 +206,22 @@ struct PolBF16 {
     static constexpr bool kExactScale = true;
     static constexpr int kWaves = 2;
     static constexpr int kWavesFwdCausal = D == 64 ? 3 : 2;
+#ifdef MXFA_X_DQ_WAVES
+    static constexpr int kWavesDq = D == 64 ? MXFA_X_DQ_WAVES : 2;
+#else
     static constexpr int kWavesDq = D == 64 ? 3 : 2;
+#endif
     // dQ pass: 16-query tiles per wave and waves per work-group. 64 queries
     // per wave halve the LDS reads per MFMA but need two waves per SIMD, and
     // ran 9-10% slower (48 queries: 8%); 16 queries at five waves per SIMD
     // double them and ran 13% slower
     static constexpr int kDqTiles = 2;
     static constexpr int kDqWavesPerGroup = 4;
+#ifdef MXFA_X_DKV_WAVES
+    static constexpr int kWavesDkv = D == 64 ? MXFA_X_DKV_WAVES : 2;
+#else
     static constexpr int kWavesDkv = D == 64 ? 3 : 2;
+#endif
     // dK/dV stage ring depth (loads issued kDkvBuffers - 1 stages ahead); a
     // third buffer measured no faster at d = 64
     static constexpr int kDkvBuffers = 2;
@@ -511,7 +519,8 @@ __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)
 // stamps the 100 MHz real-time counter at its start (0), once its first stage
 // is staged (1), at the end of its loop (2) and once its stores are
 // acknowledged (3), into mxfa_wg_times[8 g + i] for its linear work-group
-// index g, and records what it ran: (kind << 32) | block at 8 g + 4 (kind 0 =
+// index g ((z Y + y) X + x over the grid, so each split of a split forward
+// has its own slot), and records what it ran: (kind << 32) | block at 8 g + 4 (kind 0 =
 // dQ, block = query block; 1 = dK/dV, block = key block; 2 = forward, block =
 // query block), its stages at 8 g + 5 and where it ran at 8 g + 6 ((XCC_ID
 // << 32) | HW_ID; read by mxfa_probe_wg_times). In every other build these
@@ -521,7 +530,7 @@ constexpr unsigned kTimelineGroups = 1u << 16;
 extern "C" __device__ unsigned long long mxfa_wg_times[kTimelineGroups * 8];
 __device__ unsigned long long mxfa_wg_times[kTimelineGroups * 8];
 __device__ __forceinline__ void wg_put(int i, unsigned long long v) {
-    const unsigned g = blockIdx.y * gridDim.x + blockIdx.x;
+    const unsigned g = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
     if (threadIdx.x == 0 && g < kTimelineGroups) {
         *reinterpret_cast<volatile unsigned long long *>(mxfa_wg_times + 8 * (size_t)g + i) = v;
     }

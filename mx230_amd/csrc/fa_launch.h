@@ -35,8 +35,8 @@ hipError_t launch_kernel(KernelId id, dim3 grid, dim3 block, void **args, hipStr
 hipError_t launch_fwd(const Params &p, int dtype_bf16, int d, int causal, hipStream_t stream);
 // The causal forward with its keys split over work-groups (grid.z) and a
 // merging launch: the split count for a shape (1: no split pays), the fp32
-// partials it needs in p.fwd_part, and the two launches (2 <= splits <= 16;
-// K/V contiguous, or through p.block_table).
+// partials it needs in p.fwd_part, and the two launches (2 <= splits <=
+// kFwdMaxSplits = 32; K/V contiguous, or through p.block_table).
 int fwd_splits(const Params &p, int dtype_bf16, int d);
 size_t fwd_split_workspace_bytes(const Params &p, int d, int splits);
 hipError_t launch_fwd_split(const Params &p, int dtype_bf16, int d, int splits, hipStream_t stream);

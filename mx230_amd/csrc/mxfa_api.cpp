@@ -391,7 +391,11 @@ int mxfa_check_prefill(const mxfa_prefill_shape *s) {
     // query positions (pos0 + row, the rows of a single-row call being its
     // GQA group's heads) stay inside int with a block to spare
     if ((long long)s->pos0 + std::max(s->n_tok, s->n_head) > 0x7fffffffLL - 128) return MXFA_ERR_SHAPE;
-    if (((long long)s->n_tok + 127) / 128 > kMaxGridY) return MXFA_ERR_SHAPE;
+    // grid.y is the query blocks, 64 rows each in the smallest form a prefill
+    // launches (fp32, paged d = 128, the split kernels); a single row's
+    // blocks hold its GQA group's heads
+    const long long rows = s->n_tok == 1 ? std::max(1, s->n_head / s->n_kv_head) : s->n_tok;
+    if ((rows + 63) / 64 > kMaxGridY) return MXFA_ERR_SHAPE;
     if (s->head_dim != 64 && s->head_dim != 128) return MXFA_ERR_UNSUPPORTED;
     if (s->dtype == MXFA_F32 && s->head_dim != 64) return MXFA_ERR_UNSUPPORTED;
     // every head of a row must fit inside the row

@@ -207,6 +207,12 @@ def _prefill(**kw):
     (dict(head_dim=128, dtype=mx.MXFA_F32, q_stride=18 * 128, kv_stride=256, out_stride=14 * 128), -4),
     (dict(head_dim=128, q_stride=18 * 128, kv_stride=256, out_stride=14 * 128), 0),
     (dict(scale=float("nan")), -2),
+    # the query blocks of the smallest prefill work-group (64 rows: fp32,
+    # paged d = 128, the split kernels) must fit grid.y (65535)
+    (dict(n_tok=64 * 65535, dtype=mx.MXFA_F32), 0),
+    (dict(n_tok=64 * 65535 + 1, dtype=mx.MXFA_F32), -2),
+    (dict(n_tok=64 * 65535 + 1, head_dim=128, q_stride=18 * 128, kv_stride=256, out_stride=14 * 128), -2),
+    (dict(n_tok=128 * 65535), -2),
 ])
 def test_check_prefill(lib, kw, code):
     assert lib.mxfa_check_prefill(ctypes.byref(_prefill(**kw))) == code
@@ -408,3 +414,20 @@ def test_time_median_ms_needs_an_iteration():
     """mx.time_median_ms rejects iters < 1 before touching a device."""
     with pytest.raises(ValueError):
         mx.time_median_ms(lambda: None, warmup=0, iters=0)
+
+
+def test_integration_rust_block_binds_every_entry_point():
+    """INTEGRATION.md's Rust extern block declares every function of
+    include/mxfa.h (a maintainer copying it gets the whole binding)."""
+    import re
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    with open(os.path.join(root, "include", "mxfa.h")) as f:
+        header = re.sub(r"/\*.*?\*/", "", f.read(), flags=re.S)
+    names = set(re.findall(r"\b(mxfa_\w+)\s*\(", header))
+    with open(os.path.join(root, "INTEGRATION.md")) as f:
+        doc = f.read()
+    block = doc[doc.index("// 02-flash-attention/src/mxfa.rs"):]
+    block = block[:block.index("```")]
+    bound = set(re.findall(r"pub fn (mxfa_\w+)\(", block))
+    assert names, "no declarations parsed"
+    assert names == bound, (sorted(names - bound), sorted(bound - names))

@@ -112,6 +112,13 @@ def test_paged_split_equals_contiguous_split_bf16(bs, n_tok, pos0):
     _paged_case(n_tok=n_tok, pos0=pos0, nh=nh, nkv=nkv, hd=64, bs=bs, bf16=True, seed=bs + n_tok, split=True)
 
 
+def test_paged_single_row_mqa_oracle():
+    """A single row of 128 query heads over one KV head (its group spans two
+    64-query blocks) over a paged cache, unsplit and split, against the oracle."""
+    _paged_case(n_tok=1, pos0=1300, nh=128, nkv=1, hd=64, bs=16, bf16=True, seed=13, check_oracle=True)
+    _paged_case(n_tok=1, pos0=1300, nh=128, nkv=1, hd=64, bs=16, bf16=False, seed=14, check_oracle=True, split=True)
+
+
 def test_paged_split_oracle():
     """fp32 and d = 128 bf16 splits over a paged cache against the oracle."""
     _paged_case(n_tok=100, pos0=2000, nh=4, nkv=2, hd=64, bs=16, bf16=False, seed=11, check_oracle=True, split=True)

@@ -97,6 +97,19 @@ def test_split_single_row():
     _run(n_tok=1, pos0=5000, nh=4, nkv=2, hd=64, bf16=False, seed=5, check_oracle=True)
 
 
+def test_single_row_group_over_two_blocks_and_mha():
+    """A single row whose GQA group fills two 64-query blocks (128 query heads
+    over one KV head, MQA-like: the second block's rows are heads 64-127, all at
+    the row's position), bf16 and fp32, split and unsplit; and a single MHA row
+    (no packing: one row per head), unsplit in bf16 and split in fp32. Each
+    against the oracle (the unsplit result through its agreement with the
+    split one, or directly)."""
+    _run(n_tok=1, pos0=1500, nh=128, nkv=1, hd=64, bf16=True, seed=11, check_oracle=True)
+    _run(n_tok=1, pos0=1500, nh=128, nkv=1, hd=64, bf16=False, seed=12, check_oracle=True)
+    _run(n_tok=1, pos0=900, nh=12, nkv=12, hd=64, bf16=True, seed=13, check_oracle=True, expect_split=False)
+    _run(n_tok=1, pos0=900, nh=12, nkv=12, hd=64, bf16=False, seed=14, check_oracle=True)
+
+
 def test_split_engine_chunk_bf16():
     """Qwen2.5's head layout, a 512-token chunk after 3584 positions (7 splits)."""
     _run(n_tok=512, pos0=3584, nh=14, nkv=2, hd=64, bf16=True, seed=6)

@@ -3,7 +3,8 @@ through the C ABI it gives exactly what mxfa_run_bwd_ws gives with a
 caller-owned workspace (the same kernels, split and summation order, so the
 outputs are bitwise equal), on consecutive calls whose second is smaller (the
 static scratch keeps the first call's partial sums, which the second must not
-read), for GQA shapes that split their dK/dV pass and for one that does not."""
+read), for GQA shapes that split their dK/dV pass and for one that does not;
+and the device's free memory does not change across a call."""
 from __future__ import annotations
 
 import ctypes
@@ -61,10 +62,17 @@ def test_noalloc_equals_workspace_path(calls):
         assert rc == 0, rc
         got = _outs(q, k)
         stream = torch.cuda.current_stream()
+        # the entry point's defining property: the device's free memory is the
+        # same before and after it (no allocation by the library or a
+        # runtime it calls; every buffer above was allocated before this)
+        torch.cuda.synchronize()
+        free0 = torch.cuda.mem_get_info()[0]
         rc = lib.mxfa_run_bwd_noalloc(ctypes.byref(sh), P(q), P(k), P(v), P(o), P(do), P(lse), P(got[0]),
                                       P(got[1]), P(got[2]), P(got[3]), ctypes.c_void_p(stream.cuda_stream))
         assert rc == 0, rc
         torch.cuda.synchronize()
+        free1 = torch.cuda.mem_get_info()[0]
+        assert free1 == free0, f"call {i}: device free memory changed by {free0 - free1} bytes"
         for name, a, b in zip(("Delta", "dQ", "dK", "dV"), got, ref):
             assert torch.equal(a, b), f"call {i}: {name} of mxfa_run_bwd_noalloc differs from mxfa_run_bwd_ws"
         print(f"[noalloc] call {i}: workspace {nws} bytes, outputs bitwise equal", flush=True)
