@@ -46,6 +46,10 @@ int mxfa_probe_mfma32(int iters, float *sink, double *flops, void *stream);
  *   MXFA_PROBE_MIX_DKV_LDS   its LDS part alone
  *   MXFA_PROBE_MIX_DQ        dQ pass: 21 exp, 60 mul, 11 cvt, 10 b128, 11 tr
  *   MXFA_PROBE_MIX_FWD       forward: 32 exp, 106 mul, 16 cvt, 8 b128, 16 tr
+ *   MXFA_PROBE_MIX32_*       the MFMA-only, dK/dV, dQ and forward mixes with
+ *                            the same work issued as 16 v_mfma_f32_32x32x16_bf16
+ *                            per round (4 independent accumulators), the other
+ *                            instructions unchanged
  * Writes the launch's MFMA flops to *flops. Not the reference's: its audit
  * (isa.cu:11-63) times one instruction kind at a time. */
 enum {
@@ -54,7 +58,11 @@ enum {
     MXFA_PROBE_MIX_DKV_VALU = 2,
     MXFA_PROBE_MIX_DKV_LDS = 3,
     MXFA_PROBE_MIX_DQ = 4,
-    MXFA_PROBE_MIX_FWD = 5
+    MXFA_PROBE_MIX_FWD = 5,
+    MXFA_PROBE_MIX32_MFMA = 6,
+    MXFA_PROBE_MIX32_DKV = 7,
+    MXFA_PROBE_MIX32_DQ = 8,
+    MXFA_PROBE_MIX32_FWD = 9
 };
 int mxfa_probe_mix(int mix, int waves_per_simd, int iters, float *sink, double *flops, void *stream);
 /* Work-group timeline of the forward and the backward. With the timeline
@@ -65,8 +73,8 @@ int mxfa_probe_mix(int mix, int waves_per_simd, int iters, float *sink, double *
  * of its loop and once its stores are acknowledged, and records its kind and
  * block ((kind << 32) | block; kind 0 = dQ, query block; 1 = dK/dV, key block;
  * 2 = forward, query block), its stages and where it ran ((XCC_ID << 32) |
- * HW_ID): eight uint64 per linear work-group index (blockIdx.y * gridDim.x +
- * blockIdx.x; the last one zero), for the first 65536 work-groups of each
+ * HW_ID): eight uint64 per linear work-group index ((blockIdx.z * gridDim.y +
+ * blockIdx.y) * gridDim.x + blockIdx.x; the last one zero), for the first 65536 work-groups of each
  * launch, each launch
  * overwriting the last one's. Copies up to `bytes` of them to host `dst` (a
  * synchronous device-to-host copy; dst may be NULL) and writes their size to

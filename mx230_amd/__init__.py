@@ -674,7 +674,8 @@ def probe_mfma_tflops(bf16: bool = True, iters: int = 256, reps: int = 5, big: b
 
 
 # The instruction mixes of mxfa_probe_mix (include/mxfa_probes.h, MXFA_PROBE_MIX_*).
-PROBE_MIXES = {"mfma": 0, "dkv": 1, "dkv_valu": 2, "dkv_lds": 3, "dq": 4, "fwd": 5}
+PROBE_MIXES = {"mfma": 0, "dkv": 1, "dkv_valu": 2, "dkv_lds": 3, "dq": 4, "fwd": 5,
+               "mfma32": 6, "dkv32": 7, "dq32": 8, "fwd32": 9}
 
 
 def probe_mix_tflops(mix: str, waves_per_simd: int = 3, iters: int = 64, reps: int = 5) -> float:

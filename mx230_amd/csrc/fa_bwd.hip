@@ -330,7 +330,12 @@ struct DqTile16 {
     }
 };
 
-template <class Pol_, int KT>
+// P2 (bf16, a softmax scale that is a power of two, as 1/sqrt(64) is): K is
+// held as -K scale, which is exact, so the score accumulators start at L
+// itself and come out as L - s scale; the exponent is that times -log2(e). This
+// saves the per-block multiply of the staged LSE rows (16 VALU per stage at
+// d = 64) and its wait before the first score MFMA.
+template <class Pol_, int KT, bool P2 = false>
 struct DkvTile16 {
     using Pol = Pol_;
     using T = typename Pol::T;
@@ -344,18 +349,16 @@ struct DkvTile16 {
     f32x4 accK[XT][KT], accV[XT][KT];
     float lmul, xmul;
 
+    // The score accumulators' start for 4 query rows from their staged LSE.
+    __device__ __forceinline__ f32x4 nl_of(const float *l) const {
+        if constexpr (P2) return *reinterpret_cast<const f32x4 *>(l);
+        return *reinterpret_cast<const f32x4 *>(l) * lmul;
+    }
+
     // K and V rows under a branch per row (gmem_row_frags_if): the branch-free
     // form issues the loads together, but measured no faster here (they
     // overlap the first stage's loads either way) and made the register
     // allocator spill inside the two-launch dK/dV kernel's stage loops
-    // The score accumulators' start for 4 query rows from their staged LSE.
-    __device__ __forceinline__ f32x4 nl_of(const float *l) const {
-#if MXFA_X_NEGK
-        if (Pol::kExactScale) return *reinterpret_cast<const f32x4 *>(l);
-#endif
-        return *reinterpret_cast<const f32x4 *>(l) * lmul;
-    }
-
     __device__ __forceinline__ void load(const Params &p, const T *K, const T *V, int kw0, int lane) {
         const int g = lane >> 4, l16 = lane & 15;
         const int N = p.N;
@@ -366,18 +369,16 @@ struct DkvTile16 {
             Pol::gmem_row_frags_if(vf[kt], V + (size_t)key * D, g, key < N);
 #pragma unroll
             for (int kc = 0; kc < NC; ++kc) {
-#if MXFA_X_NEGK
-                if (Pol::kExactScale) kf[kt][kc] = Pol::scaled(kf[kt][kc], -p.scale);
-#endif
-                if (!Pol::kExactScale) kf[kt][kc] = Pol::scaled(kf[kt][kc], p.scale_log2);
+                if constexpr (P2) {
+                    kf[kt][kc] = Pol::scaled(kf[kt][kc], -p.scale);
+                } else if constexpr (!Pol::kExactScale) {
+                    kf[kt][kc] = Pol::scaled(kf[kt][kc], p.scale_log2);
+                }
                 vf[kt][kc] = Pol::neg(vf[kt][kc]);
             }
         }
         lmul = Pol::kExactScale ? -1.0f / p.scale : -kLog2e;
-        xmul = p.scale_log2;
-#if MXFA_X_NEGK
-        if (Pol::kExactScale) xmul = -kLog2e;
-#endif
+        xmul = P2 ? -kLog2e : p.scale_log2;
 #pragma unroll
         for (int xt = 0; xt < XT; ++xt) {
 #pragma unroll
@@ -385,125 +386,14 @@ struct DkvTile16 {
         }
     }
 
-    // The three parts of one 32-query block, for the pipelined stage: the
-    // scores and dP (first GEMMs, operands from LDS rows), the softmax
-    // recompute and dS (VALU), and the chained dV / dK updates.
-    using ChainB = typename Pol::ChainB;
-    __device__ __forceinline__ void blk_sd(f32x4 (&s)[2][KT], f32x4 (&dp)[2][KT], const T *sq, const T *sdo,
-                                           const float *sl, const float *sd, int blk, int g, int l16) const {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int q4 = 32 * blk + Pol::bidx(t, g, 0);
-            const f32x4 nl = nl_of(sl + q4);
-            const f32x4 dl = *reinterpret_cast<const f32x4 *>(sd + q4);
-            Frag a[NC], b[NC];
-            const int n = 32 * blk + Pol::arow(t, l16);
-            Pol::lds_row_frags(a, sq, n, g);
-            Pol::lds_row_frags(b, sdo, n, g);
-#pragma unroll
-            for (int kt = 0; kt < KT; ++kt) {
-                f32x4 c = nl;
-#pragma unroll
-                for (int kc = 0; kc < NC; ++kc) c = Pol::mma(a[kc], kf[kt][kc], c);
-                s[t][kt] = c;
-            }
-#pragma unroll
-            for (int kt = 0; kt < KT; ++kt) {
-                f32x4 c = dl;
-#pragma unroll
-                for (int kc = 0; kc < NC; ++kc) c = Pol::mma(b[kc], vf[kt][kc], c);
-                dp[t][kt] = c;
-            }
-        }
-    }
-    template <bool CAUSAL, bool MASK>
-    __device__ __forceinline__ void blk_sm(f32x4 (&s)[2][KT], f32x4 (&dp)[2][KT], ChainB (&cp)[KT], ChainB (&cds)[KT],
-                                           int qs, int kw0, int blk, int g, int l16) const {
-#pragma unroll
-        for (int kt = 0; kt < KT; ++kt) {
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    float x = Pol::kExactScale ? s[t][kt][r] * xmul : s[t][kt][r];
-                    if constexpr (MASK) {
-                        const bool before = Pol::bidx(t, g, r) - l16 < kw0 - qs + 16 * kt - 32 * blk;
-                        x = before ? -INFINITY : x;
-                    }
-                    const float pv = fast_exp2(x);
-                    s[t][kt][r] = pv;
-                    dp[t][kt][r] = pv * dp[t][kt][r];  // -dS / scale
-                }
-            }
-            cp[kt] = Pol::pack(s[0][kt], s[1][kt]);
-            cds[kt] = Pol::pack(dp[0][kt], dp[1][kt]);
-        }
-    }
-    __device__ __forceinline__ void blk_ch(const ChainB (&cp)[KT], const ChainB (&cds)[KT], const T *sq, const T *sdo,
-                                           int blk, int g, int l16) {
-#pragma unroll
-        for (int xt = 0; xt < XT; ++xt) {
-#pragma unroll
-            for (int kt = 0; kt < KT; ++kt) {
-                accV[xt][kt] = Pol::chain(accV[xt][kt], cp[kt], sdo, 16 * xt, 32 * blk, g, l16);
-                accK[xt][kt] = Pol::chain(accK[xt][kt], cds[kt], sq, 16 * xt, 32 * blk, g, l16);
-            }
-        }
-    }
-
-    // The stage's two blocks as a pipeline inside the wave, so the matrix
-    // products of one block issue between the softmax instructions of the
-    // other: scores/dP of block 0; softmax of block 0 with scores/dP of block
-    // 1; chained updates of block 0 with softmax of block 1; chained updates
-    // of block 1. The interleave of each overlapped part is fixed with
-    // scheduling-group barriers (one MFMA, then VALU instructions).
-    template <bool CAUSAL, bool MASK>
-    __device__ __forceinline__ void stage_pipe(const T *sq, const T *sdo, const float *sl, const float *sd, int qs,
-                                               int kw0, int lane) {
-        const int g = lane >> 4, l16 = lane & 15;
-        f32x4 s0[2][KT], dp0[2][KT], s1[2][KT], dp1[2][KT];
-        ChainB cp0[KT], cds0[KT], cp1[KT], cds1[KT];
-        blk_sd(s0, dp0, sq, sdo, sl, sd, 0, g, l16);
-        __builtin_amdgcn_sched_barrier(0);
-        blk_sd(s1, dp1, sq, sdo, sl, sd, 1, g, l16);
-        blk_sm<CAUSAL, MASK>(s0, dp0, cp0, cds0, qs, kw0, 0, g, l16);
-#if MXFA_X_SGB
-        __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);  // block 1's LDS rows, LSE, Delta
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, MXFA_X_SGB, 0);
-        }
-#endif
-        __builtin_amdgcn_sched_barrier(0);
-        blk_ch(cp0, cds0, sq, sdo, 0, g, l16);
-        blk_sm<CAUSAL, MASK>(s1, dp1, cp1, cds1, qs, kw0, 1, g, l16);
-#if MXFA_X_SGB
-        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-#endif
-        __builtin_amdgcn_sched_barrier(0);
-        blk_ch(cp1, cds1, sq, sdo, 1, g, l16);
-    }
-
     // The score accumulators start at L lmul, so they come out as the
     // exponents of P, times xmul where the policy keeps K exact
     // (Pol::kExactScale: kf holds K, lmul = -1 / scale, xmul = scale
-    // log2(e)); otherwise kf holds K scale log2(e) and lmul = -log2(e).
+    // log2(e)); otherwise kf holds K scale log2(e) and lmul = -log2(e). With
+    // P2 they start at L and kf holds -K scale, xmul = -log2(e).
     template <bool CAUSAL, bool MASK, bool PRIO>
     __device__ __forceinline__ void stage(const T *sq, const T *sdo, const float *sl, const float *sd, int qs, int kw0,
                                           int lane) {
-#if MXFA_X_DKVPIPE
-        if constexpr (Pol::D == 64 && sizeof(T) == 2) {
-            stage_pipe<CAUSAL, MASK>(sq, sdo, sl, sd, qs, kw0, lane);
-            return;
-        }
-#endif
         const int g = lane >> 4, l16 = lane & 15;
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
@@ -541,7 +431,7 @@ struct DkvTile16 {
                 for (int r = 0; r < 4; ++r) {
 #pragma unroll
                     for (int kt = 0; kt < KT; ++kt) {
-                        float x = Pol::kExactScale ? s[t][kt][r] * xmul : s[t][kt][r];
+                        float x = Pol::kExactScale || P2 ? s[t][kt][r] * xmul : s[t][kt][r];
                         if constexpr (MASK) {
                             // causal: query qs + 32 blk + bidx(t, g, r) before key kw0 + 16 kt + l16
                             const bool before = Pol::bidx(t, g, r) - l16 < kw0 - qs + 16 * kt - 32 * blk;
@@ -967,6 +857,7 @@ __device__ __forceinline__ void dkv_reduce_body(const Params &p, unsigned n4, in
 // The tiles of each dtype / head dim.
 using DqB64 = DqTile16<PolBF16<64>, PolBF16<64>::kDqTiles>;
 using DkvB64 = DkvTile16<PolBF16<64>, 2>;
+using DkvB64P2 = DkvTile16<PolBF16<64>, 2, true>;
 using DqF32 = DqTile16<PolF32<64>, PolF32<64>::kDqTiles>;
 using DkvF32 = DkvTile16<PolF32<64>, 2>;
 using DqB128 = DqTile16<PolBF16<128>, PolBF16<128>::kDqTiles>;
@@ -1011,12 +902,16 @@ MXFA_DQ(mxfa_dq_f64_n, DqF32, false, false)
 MXFA_DQ(mxfa_dq_f64_n_d, DqF32, false, true)
 MXFA_DKV(mxfa_dkv_b64_c, DkvB64, true)
 MXFA_DKV(mxfa_dkv_b64_n, DkvB64, false)
+MXFA_DKV(mxfa_dkv_b64_c_p2, DkvB64P2, true)
+MXFA_DKV(mxfa_dkv_b64_n_p2, DkvB64P2, false)
 MXFA_DKV(mxfa_dkv_b128_c, DkvB128, true)
 MXFA_DKV(mxfa_dkv_b128_n, DkvB128, false)
 MXFA_DKV(mxfa_dkv_f64_c, DkvF32, true)
 MXFA_DKV(mxfa_dkv_f64_n, DkvF32, false)
 MXFA_FUSED(mxfa_bwd_b64_c, DqB64, DkvB64, true)
 MXFA_FUSED(mxfa_bwd_b64_n, DqB64, DkvB64, false)
+MXFA_FUSED(mxfa_bwd_b64_c_p2, DqB64, DkvB64P2, true)
+MXFA_FUSED(mxfa_bwd_b64_n_p2, DqB64, DkvB64P2, false)
 MXFA_FUSED(mxfa_bwd_b128_c, DqB128, DkvB128, true)
 MXFA_FUSED(mxfa_bwd_b128_n, DqB128, DkvB128, false)
 MXFA_REDUCE(mxfa_dkv_reduce_bf16, u16)
@@ -1038,6 +933,10 @@ struct KernelsB64 {
     static constexpr KernelId dq[2][2] = {{k_mxfa_dq_b64_n, k_mxfa_dq_b64_n_d}, {k_mxfa_dq_b64_c, k_mxfa_dq_b64_c_d}};
     static constexpr KernelId dkv[2] = {k_mxfa_dkv_b64_n, k_mxfa_dkv_b64_c};
     static constexpr KernelId fused[2] = {k_mxfa_bwd_b64_n, k_mxfa_bwd_b64_c};
+    // the same with DkvB64P2, for a softmax scale that is a power of two
+    static constexpr bool kHasP2 = true;
+    static constexpr KernelId dkv_p2[2] = {k_mxfa_dkv_b64_n_p2, k_mxfa_dkv_b64_c_p2};
+    static constexpr KernelId fused_p2[2] = {k_mxfa_bwd_b64_n_p2, k_mxfa_bwd_b64_c_p2};
     static constexpr KernelId reduce = k_mxfa_dkv_reduce_bf16;
 };
 struct KernelsB128 {
@@ -1047,6 +946,9 @@ struct KernelsB128 {
                                           {k_mxfa_dq_b128_c, k_mxfa_dq_b128_c_d}};
     static constexpr KernelId dkv[2] = {k_mxfa_dkv_b128_n, k_mxfa_dkv_b128_c};
     static constexpr KernelId fused[2] = {k_mxfa_bwd_b128_n, k_mxfa_bwd_b128_c};
+    static constexpr bool kHasP2 = false;
+    static constexpr KernelId dkv_p2[2] = {k_mxfa_dkv_b128_n, k_mxfa_dkv_b128_c};
+    static constexpr KernelId fused_p2[2] = {k_mxfa_bwd_b128_n, k_mxfa_bwd_b128_c};
     static constexpr KernelId reduce = k_mxfa_dkv_reduce_bf16;
 };
 struct KernelsF64 {
@@ -1054,8 +956,17 @@ struct KernelsF64 {
     using Dkv = DkvF32;
     static constexpr KernelId dq[2][2] = {{k_mxfa_dq_f64_n, k_mxfa_dq_f64_n_d}, {k_mxfa_dq_f64_c, k_mxfa_dq_f64_c_d}};
     static constexpr KernelId dkv[2] = {k_mxfa_dkv_f64_n, k_mxfa_dkv_f64_c};
+    static constexpr bool kHasP2 = false;
+    static constexpr KernelId dkv_p2[2] = {k_mxfa_dkv_f64_n, k_mxfa_dkv_f64_c};
     static constexpr KernelId reduce = k_mxfa_dkv_reduce_f32;
 };
+
+// A softmax scale that is a power of two (the default 1/sqrt(64) = 1/8 is):
+// the kernels with the P2 dK/dV tile hold K scale exactly in bf16.
+static bool scale_is_pow2(float scale) {
+    int e = 0;
+    return scale > 0.0f && std::frexp(scale, &e) == 0.5f;
+}
 
 hipError_t launch_preprocess(const Params &p, int dtype_bf16, int d, hipStream_t stream) {
     long rows = (long)p.B * p.Hq * p.N;
@@ -1228,8 +1139,8 @@ static hipError_t launch_fused_k(Params p, int causal, hipStream_t stream) {
     p.delta_wait = wait_us < 0 ? -1 : (int)std::min(100LL * wait_us, 0x7fffffffLL);
     p.fused_ndq = (int)ndq;
     void *args[] = {&p};
-    const hipError_t err = launch_kernel(K::fused[causal ? 1 : 0], dim3((unsigned)(ndq + ndkv)), dim3(256), args,
-                                         stream);
+    const KernelId id = K::kHasP2 && scale_is_pow2(p.scale) ? K::fused_p2[causal ? 1 : 0] : K::fused[causal ? 1 : 0];
+    const hipError_t err = launch_kernel(id, dim3((unsigned)(ndq + ndkv)), dim3(256), args, stream);
     if (err != hipSuccess || p.dkv_split == 1) return err;
     return launch_dkv_reduce<K>(p, causal, stream);
 }
@@ -1251,7 +1162,8 @@ static hipError_t launch_dkv_k(Params p, int causal, hipStream_t stream) {
     const long long n = dkv_work_groups<Tile>(p, causal != 0);
     if (n > 0x7fffffffLL) return hipErrorInvalidValue;
     void *args[] = {&p};
-    const hipError_t e = launch_kernel(K::dkv[causal ? 1 : 0], dim3((unsigned)n), dim3(256), args, stream);
+    const KernelId id = K::kHasP2 && scale_is_pow2(p.scale) ? K::dkv_p2[causal ? 1 : 0] : K::dkv[causal ? 1 : 0];
+    const hipError_t e = launch_kernel(id, dim3((unsigned)n), dim3(256), args, stream);
     if (e != hipSuccess || p.dkv_split == 1) return e;
     return launch_dkv_reduce<K>(p, causal, stream);
 }

@@ -206,22 +206,14 @@ struct PolBF16 {
     static constexpr bool kExactScale = true;
     static constexpr int kWaves = 2;
     static constexpr int kWavesFwdCausal = D == 64 ? 3 : 2;
-#ifdef MXFA_X_DQ_WAVES
-    static constexpr int kWavesDq = D == 64 ? MXFA_X_DQ_WAVES : 2;
-#else
     static constexpr int kWavesDq = D == 64 ? 3 : 2;
-#endif
     // dQ pass: 16-query tiles per wave and waves per work-group. 64 queries
     // per wave halve the LDS reads per MFMA but need two waves per SIMD, and
     // ran 9-10% slower (48 queries: 8%); 16 queries at five waves per SIMD
     // double them and ran 13% slower
     static constexpr int kDqTiles = 2;
     static constexpr int kDqWavesPerGroup = 4;
-#ifdef MXFA_X_DKV_WAVES
-    static constexpr int kWavesDkv = D == 64 ? MXFA_X_DKV_WAVES : 2;
-#else
     static constexpr int kWavesDkv = D == 64 ? 3 : 2;
-#endif
     // dK/dV stage ring depth (loads issued kDkvBuffers - 1 stages ahead); a
     // third buffer measured no faster at d = 64
     static constexpr int kDkvBuffers = 2;

@@ -7,7 +7,8 @@
 // the code object fails that load. Naming: pass, dtype and head dim (b64 =
 // bf16 d = 64, b128, f64 = fp32 d = 64), c / n = causal / not, then the
 // variant (waves per SIMD w*, query tiles per wave q*, d = computes Delta,
-// pg = K/V through a block table, sp = one split of the keys).
+// pg = K/V through a block table, sp = one split of the keys, p2 = a softmax
+// scale that is a power of two).
 #pragma once
 
 #define MXFA_KERNEL_LIST(X)                                                                   \
@@ -28,8 +29,9 @@
     X(mxfa_dq_b128_c) X(mxfa_dq_b128_c_d) X(mxfa_dq_b128_n) X(mxfa_dq_b128_n_d)               \
     X(mxfa_dq_f64_c) X(mxfa_dq_f64_c_d) X(mxfa_dq_f64_n) X(mxfa_dq_f64_n_d)                   \
     X(mxfa_dkv_b64_c) X(mxfa_dkv_b64_n) X(mxfa_dkv_b128_c) X(mxfa_dkv_b128_n)                 \
-    X(mxfa_dkv_f64_c) X(mxfa_dkv_f64_n)                                                       \
+    X(mxfa_dkv_f64_c) X(mxfa_dkv_f64_n) X(mxfa_dkv_b64_c_p2) X(mxfa_dkv_b64_n_p2)             \
     X(mxfa_bwd_b64_c) X(mxfa_bwd_b64_n) X(mxfa_bwd_b128_c) X(mxfa_bwd_b128_n)                 \
+    X(mxfa_bwd_b64_c_p2) X(mxfa_bwd_b64_n_p2)                                                 \
     X(mxfa_dkv_reduce_bf16) X(mxfa_dkv_reduce_f32)                                            \
     /* naive baselines (fa_naive.hip) */                                                      \
     X(mxfa_naive_scores) X(mxfa_naive_softmax) X(mxfa_naive_av) X(mxfa_naive_bwd)            \
@@ -37,7 +39,8 @@
     X(mxfa_probe_mfma_bf16) X(mxfa_probe_mfma_f32) X(mxfa_probe_mfma32_bf16)                  \
     X(mxfa_probe_read_f4) X(mxfa_probe_copy_f4) X(mxfa_probe_dq_atomic_add)                   \
     X(mxfa_probe_dq_atomic_store) X(mxfa_probe_mix_mfma) X(mxfa_probe_mix_dkv)                  \
-    X(mxfa_probe_mix_dkv_valu) X(mxfa_probe_mix_dkv_lds) X(mxfa_probe_mix_dq) X(mxfa_probe_mix_fwd)
+    X(mxfa_probe_mix_dkv_valu) X(mxfa_probe_mix_dkv_lds) X(mxfa_probe_mix_dq) X(mxfa_probe_mix_fwd)         \
+    X(mxfa_probe_mix32_mfma) X(mxfa_probe_mix32_dkv) X(mxfa_probe_mix32_dq) X(mxfa_probe_mix32_fwd)
 
 namespace mxfa {
 

@@ -161,13 +161,18 @@ __device__ __forceinline__ constexpr int mix_reads(int b, int r, int s0, int s1)
     return mix_first(b, s1) - mix_first(b, s0) + mix_first(r, s1) - mix_first(r, s0);
 }
 
-template <int E, int M, int C, int B, int R>
+// BIG: the same flops as 16 v_mfma_f32_32x32x16_bf16 per round (one on
+// every other slot, 4 independent accumulators), with the same other
+// instructions: whether the larger MFMA shape, which issues half as many MFMA
+// instructions for the work, raises a mix's ceiling.
+template <int E, int M, int C, int B, int R, bool BIG = false>
 __device__ __forceinline__ void probe_mix_body(float *sink, int iters) {
     __shared__ __attribute__((aligned(16))) float lds[4096];  // 16 KB
     const int tid = threadIdx.x, lane = tid & 63;
     for (int i = tid; i < 4096; i += kProbeThreads) lds[i] = 0.001f * (float)(i & 255);
     __syncthreads();
     f32x4 acc[8];
+    f32x16 acc32[4];
     float xe[8], xm[8];
     uint32_t u[4];
     f32x4 rb[4];
@@ -183,6 +188,8 @@ __device__ __forceinline__ void probe_mix_body(float *sink, int iters) {
         u[j] = 0;
         rb[j] = zero4();
         rt[j] = 0.0;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc32[j][e] = 0.f;
     }
     bf16x8 a, b;
 #pragma unroll
@@ -196,7 +203,12 @@ __device__ __forceinline__ void probe_mix_body(float *sink, int iters) {
     for (int i = 0; i < iters; ++i) {
 #pragma unroll
         for (int s = 0; s < kMixSlots; ++s) {
-            asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(acc[s & 7]) : "v"(a), "v"(b));
+            if constexpr (BIG) {
+                if (s % 2 == 0)
+                    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc32[(s / 2) & 3]) : "v"(a), "v"(b));
+            } else {
+                asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(acc[s & 7]) : "v"(a), "v"(b));
+            }
 #pragma unroll
             for (int j = mix_first(E, s); j < mix_first(E, s + 1); ++j) asm volatile("v_exp_f32 %0, %0" : "+v"(xe[j & 7]));
 #pragma unroll
@@ -223,7 +235,7 @@ __device__ __forceinline__ void probe_mix_body(float *sink, int iters) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) sum += acc[j][0] + xe[j] + xm[j];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) sum += (float)u[j] + rb[j][0] + (float)rt[j];
+    for (int j = 0; j < 4; ++j) sum += (float)u[j] + rb[j][0] + (float)rt[j] + acc32[j][0];
     sink[blockIdx.x * kProbeThreads + tid] = sum;
 }
 
@@ -248,16 +260,20 @@ extern "C" __global__ __launch_bounds__(256) void mxfa_probe_copy_f4(const float
 }
 // instruction mixes (counts per 32 MFMAs; the rows of MXFA_PROBE_MIX_* in
 // mxfa_probes.h)
-#define MXFA_MIX(NAME, E, M, C, B, R)                                                                       \
+#define MXFA_MIX(NAME, E, M, C, B, R, BIG)                                                                  \
     extern "C" __global__ __launch_bounds__(256) void NAME(float *sink, int iters) {                        \
-        probe_mix_body<E, M, C, B, R>(sink, iters);                                                         \
+        probe_mix_body<E, M, C, B, R, BIG>(sink, iters);                                                    \
     }
-MXFA_MIX(mxfa_probe_mix_mfma, 0, 0, 0, 0, 0)
-MXFA_MIX(mxfa_probe_mix_dkv, 16, 48, 16, 12, 16)
-MXFA_MIX(mxfa_probe_mix_dkv_valu, 16, 48, 16, 0, 0)
-MXFA_MIX(mxfa_probe_mix_dkv_lds, 0, 0, 0, 12, 16)
-MXFA_MIX(mxfa_probe_mix_dq, 21, 60, 11, 10, 11)
-MXFA_MIX(mxfa_probe_mix_fwd, 32, 106, 16, 8, 16)
+MXFA_MIX(mxfa_probe_mix_mfma, 0, 0, 0, 0, 0, false)
+MXFA_MIX(mxfa_probe_mix_dkv, 16, 48, 16, 12, 16, false)
+MXFA_MIX(mxfa_probe_mix_dkv_valu, 16, 48, 16, 0, 0, false)
+MXFA_MIX(mxfa_probe_mix_dkv_lds, 0, 0, 0, 12, 16, false)
+MXFA_MIX(mxfa_probe_mix_dq, 21, 60, 11, 10, 11, false)
+MXFA_MIX(mxfa_probe_mix_fwd, 32, 106, 16, 8, 16, false)
+MXFA_MIX(mxfa_probe_mix32_mfma, 0, 0, 0, 0, 0, true)
+MXFA_MIX(mxfa_probe_mix32_dkv, 16, 48, 16, 12, 16, true)
+MXFA_MIX(mxfa_probe_mix32_dq, 21, 60, 11, 10, 11, true)
+MXFA_MIX(mxfa_probe_mix32_fwd, 32, 106, 16, 8, 16, true)
 #undef MXFA_MIX
 extern "C" __global__ __launch_bounds__(256) void mxfa_probe_dq_atomic_add(float *acc, int n) {
     probe_dq_atomic_body<true>(acc, n);
@@ -307,8 +323,10 @@ hipError_t launch_probe_mfma32(int iters, float *sink, hipStream_t stream) {
     return launch_kernel(k_mxfa_probe_mfma32_bf16, dim3(kProbeBlocks), dim3(kProbeThreads), args, stream);
 }
 
-static const KernelId kMixKernels[] = {k_mxfa_probe_mix_mfma,     k_mxfa_probe_mix_dkv, k_mxfa_probe_mix_dkv_valu,
-                                       k_mxfa_probe_mix_dkv_lds, k_mxfa_probe_mix_dq,  k_mxfa_probe_mix_fwd};
+static const KernelId kMixKernels[] = {k_mxfa_probe_mix_mfma,    k_mxfa_probe_mix_dkv,     k_mxfa_probe_mix_dkv_valu,
+                                       k_mxfa_probe_mix_dkv_lds, k_mxfa_probe_mix_dq,      k_mxfa_probe_mix_fwd,
+                                       k_mxfa_probe_mix32_mfma,  k_mxfa_probe_mix32_dkv,   k_mxfa_probe_mix32_dq,
+                                       k_mxfa_probe_mix32_fwd};
 
 int probe_mix_count() { return (int)(sizeof(kMixKernels) / sizeof(kMixKernels[0])); }
 

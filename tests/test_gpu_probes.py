@@ -72,8 +72,11 @@ def test_probe_mix_ceilings_order():
     print("\n[probe] mix ceilings (3 waves/SIMD): " + " ".join(f"{m}={t:.0f}" for m, t in got.items())
           + f" (MFMA probe {mfma:.0f}) TFLOP/s", flush=True)
     assert 0.85 * mfma < got["mfma"] < 1.1 * mfma
+    assert 0.85 * mfma < got["mfma32"] < 1.1 * mfma
     for m in ("dkv", "dkv_valu", "dkv_lds", "dq", "fwd"):
         assert 0.2 * mfma < got[m] < 1.05 * got["mfma"], m
+        if m + "32" in got:
+            assert 0.2 * mfma < got[m + "32"] < 1.05 * got["mfma32"], m + "32"
     assert got["dkv"] < 1.05 * min(got["dkv_valu"], got["dkv_lds"])
 
 
