@@ -599,7 +599,7 @@ template <class Tile, bool CAUSAL, bool DELTA>
 __device__ __forceinline__ void dq_entry(const Params &p) {
     __shared__ DqSmem<typename Tile::Pol> sm;
     const int nqb = (p.N + 4 * Tile::ROWS - 1) / (4 * Tile::ROWS);
-    const int qb = CAUSAL ? (nqb - 1 - (int)blockIdx.y) : (int)blockIdx.y;
+    const int qb = CAUSAL ? (nqb - 1 - cu_order_block((int)blockIdx.y, p.qb_period)) : (int)blockIdx.y;
     dq_body<Tile, CAUSAL, DELTA>(p, blockIdx.x, qb, sm);
 }
 
@@ -991,8 +991,10 @@ template <class K>
 static hipError_t launch_dq_k(Params p, int causal, int delta, hipStream_t stream) {
     constexpr int BQ = 4 * K::Dq::ROWS;
     const dim3 grid(p.B * p.Hq, (p.N + BQ - 1) / BQ);
+    const KernelId id = K::dq[causal ? 1 : 0][delta ? 1 : 0];
+    p.qb_period = causal ? cu_balance_period(id, grid.x, grid.y) : 0;
     void *args[] = {&p};
-    return launch_kernel(K::dq[causal ? 1 : 0][delta ? 1 : 0], grid, dim3(256), args, stream);
+    return launch_kernel(id, grid, dim3(256), args, stream);
 }
 
 hipError_t launch_bwd_dq(const Params &p, int dtype_bf16, int d, int causal, int delta, hipStream_t stream) {
@@ -1138,8 +1140,8 @@ static hipError_t launch_fused_k(Params p, int causal, hipStream_t stream) {
     const int wait_us = g_delta_wait_us.load();
     p.delta_wait = wait_us < 0 ? -1 : (int)std::min(100LL * wait_us, 0x7fffffffLL);
     p.fused_ndq = (int)ndq;
-    void *args[] = {&p};
     const KernelId id = K::kHasP2 && scale_is_pow2(p.scale) ? K::fused_p2[causal ? 1 : 0] : K::fused[causal ? 1 : 0];
+    void *args[] = {&p};
     const hipError_t err = launch_kernel(id, dim3((unsigned)(ndq + ndkv)), dim3(256), args, stream);
     if (err != hipSuccess || p.dkv_split == 1) return err;
     return launch_dkv_reduce<K>(p, causal, stream);

@@ -72,7 +72,23 @@ struct Params {
     // (delta_wait < 0: always compute it).
     unsigned epoch;
     int flag_slot, delta_wait, fused_ndq;
+    // Causal block order (cu_order_block): 0 = the kernel's own order.
+    int qb_period;
 };
+
+// Where a grid is resident all at once, the dispatcher gives each XCD (work-
+// groups i mod 8) its work-groups in order and places them round robin on its
+// 32 CUs, so with bh = B Hq a multiple of 8 that divides 256 one CU holds one
+// head's blocks y, y + S, y + 2S, ... for S = 256 / bh (seen in the timeline
+// build: per-CU stage counts 52-80 against a mean of 66 for 1024 forward work-
+// groups of a causal B1 H32 N2048, and CU end times following them). Reversing
+// every other run of S block indices gives each CU blocks whose work (affine
+// in the index) sums to the same total. period <= 1: y itself.
+__host__ __device__ inline int cu_order_block(int y, int period) {
+    if (period <= 1) return y;
+    const int k = y / period, r = y - k * period;
+    return (k & 1) ? k * period + period - 1 - r : y;
+}
 
 // Delta flags of the one-launch backward: kFlagSlots slots (one per launch,
 // round robin, so launches in flight at once on one device do not share

@@ -313,7 +313,8 @@ __device__ __forceinline__ void fwd_entry(const Params &p) {
     const int N = p.N, Nk = p.Nk, pos0 = p.pos0;
     const int bh = blockIdx.x;
     const int nqb = (N + BQ - 1) / BQ;
-    const int qb = CAUSAL ? (nqb - 1 - (int)blockIdx.y) : (int)blockIdx.y;  // heaviest first
+    // heaviest first (the order balanced per CU where the grid is resident at once)
+    const int qb = CAUSAL ? (nqb - 1 - cu_order_block((int)blockIdx.y, p.qb_period)) : (int)blockIdx.y;
     const int b = bh / p.Hq, h = bh % p.Hq, kvh = h / p.group;
     const T *Q = static_cast<const T *>(p.q) + b * p.q_bs + h * p.q_hs;
     const size_t kvoff = b * p.kv_bs + kvh * p.kv_hs;
@@ -604,9 +605,10 @@ static hipError_t launch_fwd_qt(Params p, hipStream_t stream) {
         // enough causal work-groups to fill kHi per CU (256 CUs); not paged
         if ((long long)grid.x * grid.y >= 256LL * kHi && p.block_table == nullptr) wps = kHi;
     }
+    const KernelId id = fwd_kernel_id<Pol, CAUSAL>(wps, QT, p.block_table != nullptr);
+    p.qb_period = CAUSAL ? cu_balance_period(id, grid.x, grid.y) : 0;
     void *args[] = {&p};
-    return launch_kernel(fwd_kernel_id<Pol, CAUSAL>(wps, QT, p.block_table != nullptr), grid, dim3(256), args,
-                         stream);
+    return launch_kernel(id, grid, dim3(256), args, stream);
 }
 
 // bf16 launches whose 128-query work-groups would not fill every resident

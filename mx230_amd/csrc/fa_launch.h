@@ -31,6 +31,15 @@ void unload_code_objects();
 // Launches kernel `id` of the current device's code object (loading it on
 // first use). args: pointers to the kernel's arguments, in order.
 hipError_t launch_kernel(KernelId id, dim3 grid, dim3 block, void **args, hipStream_t stream);
+// The current device's CUs, and the 256-thread work-groups of kernel `id`
+// resident at once per CU (the runtime's occupancy); 0 when unknown.
+int device_cus();
+int kernel_occupancy(KernelId id);
+// The period of the block order (Params::qb_period) that gives every CU the
+// same work when all bh x nblocks work-groups of kernel `id` (bh fastest; a
+// block's work an affine function of its index) are resident at once; 0 when
+// that does not apply. See cu_order_block (fa_device.h).
+int cu_balance_period(KernelId id, long long bh, long long nblocks);
 
 hipError_t launch_fwd(const Params &p, int dtype_bf16, int d, int causal, hipStream_t stream);
 // The causal forward with its keys split over work-groups (grid.z) and a

@@ -40,6 +40,12 @@ struct DeviceModule {
     hipModule_t mod = nullptr;
     hipFunction_t fn[kNumKernels] = {};
     void *fallbacks = nullptr;  // the code object's Delta fallback counter
+    int cus = 0;                // the device's CUs
+    // work-groups of 256 threads of each kernel resident per CU (-1: not asked yet)
+    std::atomic<int> occupancy[kNumKernels];
+    DeviceModule() {
+        for (auto &o : occupancy) o.store(-1);
+    }
 };
 
 std::mutex g_mu;
@@ -87,6 +93,8 @@ void unload(DeviceModule &m) {
     m.mod = nullptr;
     m.fallbacks = nullptr;
     std::memset(m.fn, 0, sizeof(m.fn));
+    for (auto &o : m.occupancy) o.store(-1);
+    m.cus = 0;
     m.ready.store(false);
 }
 
@@ -133,6 +141,10 @@ DeviceModule *module_for(int device, hipError_t *err) {
         return nullptr;
     }
     m.fallbacks = ptr;
+    if (hipDeviceGetAttribute(&m.cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) {
+        (void)hipGetLastError();
+        m.cus = 0;
+    }
     m.ready.store(true, std::memory_order_release);
     return &m;
 }
@@ -173,6 +185,40 @@ void unload_code_objects() {
         if (hipSetDevice(d) == hipSuccess) unload(g_dev[d]);
     }
     if (restore) (void)hipSetDevice(current);
+}
+
+int device_cus() {
+    hipError_t err = hipSuccess;
+    DeviceModule *m = current_module(&err);
+    return m == nullptr ? 0 : m->cus;
+}
+
+int kernel_occupancy(KernelId id) {
+    hipError_t err = hipSuccess;
+    DeviceModule *m = current_module(&err);
+    if (m == nullptr) return 0;
+    int n = m->occupancy[id].load();
+    if (n < 0) {
+        if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, m->fn[id], 256, 0) != hipSuccess) {
+            (void)hipGetLastError();
+            n = 0;
+        }
+        m->occupancy[id].store(n);
+    }
+    return n;
+}
+
+int cu_balance_period(KernelId id, long long bh, long long nblocks) {
+    constexpr long long kXcds = 8;  // MI355X: 8 XCDs of 32 CUs
+    const int cus = device_cus();
+    if (cus <= 0 || cus % kXcds != 0 || bh <= 0 || bh % kXcds != 0) return 0;
+    const long long per_xcd = cus / kXcds, heads = bh / kXcds;  // a head's blocks stay on one XCD
+    if (per_xcd % heads != 0) return 0;
+    const long long period = per_xcd / heads;
+    if (period < 2 || nblocks % period != 0 || nblocks / period < 2) return 0;
+    const int occ = kernel_occupancy(id);
+    if (occ <= 0 || bh * nblocks > (long long)cus * occ) return 0;  // not all resident at once
+    return (int)period;
 }
 
 hipError_t launch_kernel(KernelId id, dim3 grid, dim3 block, void **args, hipStream_t stream) {
