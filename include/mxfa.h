@@ -170,9 +170,9 @@ int mxfa_run_bwd(const mxfa_shape *shape, const void *q, const void *k, const vo
                  void *stream);
 
 /* 1 if mxfa_run_bwd and mxfa_run_bwd_ws run the dQ and dK/dV work of this
- * shape in one launch (followed, for a GQA split through a workspace, by the
- * launch that adds the split's partial sums), else 0 (a dQ launch and a dK/dV
- * launch, or an invalid shape).
+ * shape in one launch (for a GQA split through a workspace, the adding of the
+ * split's partial sums included), else 0 (a dQ launch and a dK/dV launch, or
+ * an invalid shape).
  * The one-launch form (bf16, d = 64 or 128) runs the dQ work-groups first;
  * they publish Delta per 128-row query block, and the dK/dV work-groups of the
  * same launch wait for the blocks they need. Each wait is bounded in time
@@ -187,7 +187,7 @@ int mxfa_run_bwd(const mxfa_shape *shape, const void *q, const void *k, const vo
 int mxfa_bwd_one_launch(const mxfa_shape *shape);
 
 /* Process-wide settings of the one-launch backward, read at every launch
- * (default {1, 200}). Meant for tests and measurement; settings changed while
+ * (default {1, 200, 2000000}). Meant for tests and measurement; settings changed while
  * other threads launch take effect at their next launch.
  * No counterpart in the reference (its backward is always two launches,
  * main.rs:179-210). */
@@ -195,6 +195,9 @@ typedef struct {
     int one_launch;    /* 1: one launch where available (bf16); 0: always two */
     int delta_wait_us; /* bound of each Delta wait in microseconds; < 0: never
                           wait, always compute Delta in the dK/dV work-group */
+    int reduce_wait_us; /* bound of each wait of a GQA split's reduce work-
+                           group for its shares, microseconds, >= 0 (see
+                           mxfa_bwd_reduce_timeouts) */
 } mxfa_bwd_options;
 int mxfa_set_bwd_options(const mxfa_bwd_options *options);
 int mxfa_get_bwd_options(mxfa_bwd_options *options);
@@ -206,14 +209,26 @@ int mxfa_get_bwd_options(mxfa_bwd_options *options);
  * operation; a count does not change results (see mxfa_bwd_one_launch). */
 int mxfa_bwd_delta_fallbacks(unsigned long long *count);
 
+/* Work-groups of the one-launch backward that add a GQA split's partial sums
+ * and whose wait for them ran out, on the current device since the library
+ * was loaded (a synchronous device-to-host copy, as above). Those work-groups
+ * run after all of the split's work-groups have been dispatched, so the wait
+ * ends in normal operation and the count stays 0; a count means the dK and dV
+ * rows of those work-groups were written as NaN. The wait is bounded
+ * (mxfa_bwd_options.reduce_wait_us, default 2 s) so that a launch always
+ * ends.
+ * No counterpart in the reference (no GQA, and its backward is two launches,
+ * main.rs:179-210). */
+int mxfa_bwd_reduce_timeouts(unsigned long long *count);
+
 /* Bytes of device workspace the _ws entry points below can use (0 for an
  * invalid shape). dQ is a separate atomic-free pass and needs none. With GQA
  * (Hq > Hkv), when the key blocks alone would leave the GPU underfilled, the
  * dK/dV pass splits the work of each key block (its group's query heads, each
  * from the diagonal) over several work-groups, a causal block with more
  * queries over more of them: each writes fp32 partial dK/dV sums to the
- * workspace and a second launch adds them in a fixed order (deterministic,
- * atomic-free). The size is 2 * planes * B * Hkv * N * d * 4 bytes, planes
+ * workspace, and they are added in a fixed order (deterministic, atomic-free)
+ * by the last work-groups of the one-launch backward, else by a second launch. The size is 2 * planes * B * Hkv * N * d * 4 bytes, planes
  * being the most work-groups any key block takes; 0 when no split helps
  * (always without GQA).
  * The reference has no GQA (d = 64, one head, attention_bwd.cu:165-243); this

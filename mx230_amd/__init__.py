@@ -56,7 +56,7 @@ EXPORTS = (
     "mxfa_run_bwd_dkv_ws", "mxfa_run_bwd_ws", "mxfa_run_bwd_naive",
     "mxfa_naive_scratch_bytes", "mxfa_run_naive_fwd", "mxfa_check_prefill", "mxfa_run_prefill",
     "mxfa_run_prefill_paged", "mxfa_prefill_workspace_bytes", "mxfa_run_prefill_ws", "mxfa_run_prefill_paged_ws",
-    "mxfa_set_bwd_options", "mxfa_get_bwd_options", "mxfa_bwd_delta_fallbacks",
+    "mxfa_set_bwd_options", "mxfa_get_bwd_options", "mxfa_bwd_delta_fallbacks", "mxfa_bwd_reduce_timeouts",
     "mxfa_run_bwd_noalloc", "mxfa_bwd_noalloc_scratch_bytes",
 )
 # Every symbol include/mxfa_probes.h declares.
@@ -81,7 +81,7 @@ class MxfaShape(ctypes.Structure):
 
 
 class MxfaBwdOptions(ctypes.Structure):
-    _fields_ = [("one_launch", ctypes.c_int), ("delta_wait_us", ctypes.c_int)]
+    _fields_ = [("one_launch", ctypes.c_int), ("delta_wait_us", ctypes.c_int), ("reduce_wait_us", ctypes.c_int)]
 
 
 class MxfaPrefillShape(ctypes.Structure):
@@ -163,6 +163,7 @@ def load_library(path: str | None = None):
     lib.mxfa_set_bwd_options.argtypes = [op]
     lib.mxfa_get_bwd_options.argtypes = [op]
     lib.mxfa_bwd_delta_fallbacks.argtypes = [ctypes.POINTER(ctypes.c_ulonglong)]
+    lib.mxfa_bwd_reduce_timeouts.argtypes = [ctypes.POINTER(ctypes.c_ulonglong)]
     for name in EXPORTS + PROBE_EXPORTS:
         if name not in ("mxfa_version", "mxfa_strerror", "mxfa_bwd_workspace_bytes",
                         "mxfa_naive_scratch_bytes", "mxfa_bwd_noalloc_scratch_bytes",
@@ -335,16 +336,19 @@ def get_bwd_options() -> dict:
     """The one-launch backward's process-wide settings (mxfa_get_bwd_options)."""
     o = MxfaBwdOptions()
     _check("mxfa_get_bwd_options", load_library().mxfa_get_bwd_options(ctypes.byref(o)))
-    return {"one_launch": bool(o.one_launch), "delta_wait_us": o.delta_wait_us}
+    return {"one_launch": bool(o.one_launch), "delta_wait_us": o.delta_wait_us, "reduce_wait_us": o.reduce_wait_us}
 
 
-def set_bwd_options(one_launch: bool | None = None, delta_wait_us: int | None = None) -> dict:
+def set_bwd_options(one_launch: bool | None = None, delta_wait_us: int | None = None,
+                    reduce_wait_us: int | None = None) -> dict:
     """Changes the given settings (mxfa_set_bwd_options) and returns the
     previous ones. one_launch=False: always two launches; delta_wait_us < 0:
-    the dK/dV work-groups never wait for Delta and compute it themselves."""
+    the dK/dV work-groups never wait for Delta and compute it themselves;
+    reduce_wait_us: the bound of a GQA split's reduce wait (>= 0)."""
     old = get_bwd_options()
     o = MxfaBwdOptions(int(old["one_launch"] if one_launch is None else one_launch),
-                       old["delta_wait_us"] if delta_wait_us is None else int(delta_wait_us))
+                       old["delta_wait_us"] if delta_wait_us is None else int(delta_wait_us),
+                       old["reduce_wait_us"] if reduce_wait_us is None else int(reduce_wait_us))
     _check("mxfa_set_bwd_options", load_library().mxfa_set_bwd_options(ctypes.byref(o)))
     return old
 
@@ -355,6 +359,16 @@ def bwd_delta_fallbacks() -> int:
     launches of interest first)."""
     n = ctypes.c_ulonglong(0)
     _check("mxfa_bwd_delta_fallbacks", load_library().mxfa_bwd_delta_fallbacks(ctypes.byref(n)))
+    return int(n.value)
+
+
+def bwd_reduce_timeouts() -> int:
+    """Work-groups of the one-launch backward that add a GQA split's partial
+    sums and whose wait for them ran out (their dK/dV rows are NaN), on the
+    current device since load (mxfa_bwd_reduce_timeouts; 0 in normal operation;
+    synchronise the launches of interest first)."""
+    n = ctypes.c_ulonglong(0)
+    _check("mxfa_bwd_reduce_timeouts", load_library().mxfa_bwd_reduce_timeouts(ctypes.byref(n)))
     return int(n.value)
 
 

@@ -92,18 +92,24 @@ __device__ __forceinline__ void stage_qdo(typename Pol::T *sq, typename Pol::T *
     if (STAGE_DELTA && wave == 1) stage_vec64(sd, p.delta + bh * N + qs, N - qs, lane, p.delta + bh * N + qs);
 }
 
-// Delta flags of the one-launch backward (see Params::epoch). Zero at load;
-// launch epochs start at 1, so no flag matches before it is published. And
-// the stages whose Delta a dK/dV work-group of the one-launch backward
-// computed itself (its wait ran out), counted since the code object was
-// loaded (read by name, see module.cpp).
+// Delta and share flags of the one-launch backward (see Params::epoch and
+// Params::red_rows). Zero at load; launch epochs start at 1, so no flag
+// matches before it is published. And, counted since the code object was
+// loaded (read by name, see module.cpp): the stages whose Delta a dK/dV work-
+// group of the one-launch backward computed itself (its wait ran out), and
+// the reduce work-groups whose wait for their shares ran out (outputs NaN).
 #if defined(__HIP_DEVICE_COMPILE__)
 __device__ uint32_t g_delta_flags[kFlagSlots * kMaxFlagBlocks];
+__device__ uint32_t g_share_flags[kFlagSlots * kMaxShareFlags];
 extern "C" __device__ unsigned long long mxfa_delta_fallbacks;
 __device__ unsigned long long mxfa_delta_fallbacks;
+extern "C" __device__ unsigned long long mxfa_reduce_timeouts;
+__device__ unsigned long long mxfa_reduce_timeouts;
 #else
 extern __device__ uint32_t g_delta_flags[kFlagSlots * kMaxFlagBlocks];
+extern __device__ uint32_t g_share_flags[kFlagSlots * kMaxShareFlags];
 extern "C" __device__ unsigned long long mxfa_delta_fallbacks;
+extern "C" __device__ unsigned long long mxfa_reduce_timeouts;
 #endif
 constexpr int kFlagRows = 128;  // query rows per flag: one dQ work-group's block
 
@@ -464,7 +470,7 @@ struct DkvTile16 {
 
     // Scaled dK and dV (dst = K-shaped outputs of type T), or with SPLIT the
     // unscaled fp32 partial sums (dst = the share's workspace planes).
-    template <class U>
+    template <class U, bool WT = false>
     __device__ __forceinline__ void store(U *dK, U *dV, int kw0, int N, float kmul, int lane) const {
         const int g = lane >> 4, l16 = lane & 15;
 #pragma unroll
@@ -481,8 +487,13 @@ struct DkvTile16 {
             } else if (key < N) {
 #pragma unroll
                 for (int xt = 0; xt < XT; ++xt) {
-                    store4<U>(dK + (size_t)key * D + 16 * xt + 4 * g, accK[xt][kt], kmul);
-                    store4<U>(dV + (size_t)key * D + 16 * xt + 4 * g, accV[xt][kt], 1.0f);
+                    if constexpr (WT) {  // partial sums (kmul = 1) for a reduce in the same launch
+                        store4_wt(dK + (size_t)key * D + 16 * xt + 4 * g, accK[xt][kt]);
+                        store4_wt(dV + (size_t)key * D + 16 * xt + 4 * g, accV[xt][kt]);
+                    } else {
+                        store4<U>(dK + (size_t)key * D + 16 * xt + 4 * g, accK[xt][kt], kmul);
+                        store4<U>(dV + (size_t)key * D + 16 * xt + 4 * g, accV[xt][kt], 1.0f);
+                    }
                 }
             }
         }
@@ -779,7 +790,11 @@ __device__ __forceinline__ void dkv_body(const Params &p, const DkvWork wk, DkvS
         // block's shares and applies the scale
         const size_t plane = (size_t)p.B * p.Hkv * N * D;
         float *wK = p.dkv_ws + (size_t)wk.sp * plane + kvoff;
-        t.store(wK, wK + (size_t)p.dkv_split * plane, kw0, N, 1.0f, lane);
+        if (WAIT && p.red_rows > 0) {
+            t.template store<float, true>(wK, wK + (size_t)p.dkv_split * plane, kw0, N, 1.0f, lane);
+        } else {
+            t.store(wK, wK + (size_t)p.dkv_split * plane, kw0, N, 1.0f, lane);
+        }
     } else {
         t.store(static_cast<T *>(p.dk) + kvoff, static_cast<T *>(p.dv) + kvoff, kw0, N, -p.scale, lane);
     }
@@ -810,6 +825,94 @@ union FusedSmem {
     DkvSmem<Pol> dkv;
 };
 
+// The reduce of a GQA split inside the one-launch backward: work-group r adds
+// the shares' planes for red_rows = 1024 / d keys of one key block (one float4
+// of each plane per thread), in share order, as dkv_reduce_body does. Work-
+// groups go key block 0 first (the shares' order), then (batch, KV head),
+// then the block's chunk of rows. The shares have lower indices, so each is
+// dispatched before any reduce work-group and waits for nothing it runs; the
+// wait is bounded all the same (Params::red_wait), after which the outputs
+// are NaN and mxfa_reduce_timeouts counts the work-group.
+template <class Tile, bool CAUSAL>
+__device__ __forceinline__ void dkv_reduce_rows(const Params &p, int r, uint32_t *s_ok) {
+    using T = typename Tile::Pol::T;
+    constexpr int D = Tile::D, BKV = 4 * Tile::ROWS, BQ = Tile::Pol::ROWS;
+    constexpr int RR = 1024 / D, NCH = BKV / RR;
+    static_assert(BKV % RR == 0, "a key block is whole chunks");
+    const int N = p.N, nbkv = p.B * p.Hkv;
+    const int c = r % NCH, bkv = (r / NCH) % nbkv, kb = r / (NCH * nbkv);
+    const int key0 = kb * BKV + c * RR;
+    if (key0 >= N) return;
+    wg_time(0);
+    // the block's shares are dkv_work indices [w0, w0 + ns)
+    int w0, ns;
+    if (CAUSAL) {
+        w0 = 0;
+        for (int k = 0; k < kb; ++k) w0 += nbkv * dkv_block_shares(p, (N - k * BKV + BQ - 1) / BQ);
+        ns = dkv_block_shares(p, (N - kb * BKV + BQ - 1) / BQ);
+    } else {
+        ns = dkv_block_shares(p, (N + BQ - 1) / BQ);
+        w0 = kb * nbkv * ns;
+    }
+    w0 += bkv * ns;
+    wg_info(3, kb, ns);
+    const int tid = threadIdx.x;
+    if (tid < 64) {
+        const uint32_t *flags = g_share_flags + (size_t)p.flag_slot * kMaxShareFlags + w0;
+        bool ok = true;
+        for (int s0 = 0; s0 < ns && ok; s0 += 64) {
+            const int s = s0 + tid;
+            const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+            for (;;) {
+                const bool ready = s >= ns || load_uc_sync(flags + s) == p.epoch;
+                if (__builtin_amdgcn_ballot_w64(!ready) == 0) break;
+                if (__builtin_amdgcn_s_memrealtime() - t0 > (uint64_t)p.red_wait) {
+                    ok = false;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+        }
+        if (tid == 0) {
+            *s_ok = ok ? 1u : 0u;
+            if (!ok) atomicAdd(&mxfa_reduce_timeouts, 1ull);
+        }
+    }
+    __syncthreads();
+    wg_time(1);
+    const bool ok = *s_ok != 0;
+    const size_t plane = (size_t)p.B * p.Hkv * N * D;
+    const size_t off = ((size_t)bkv * N + key0) * D;  // the chunk's first element
+    const uint32_t bytes = (uint32_t)(min(RR, N - key0) * D * 4);
+    const uint32_t lo = 16u * tid;
+    const float *wk = p.dkv_ws + off, *wv = p.dkv_ws + (size_t)p.dkv_split * plane + off;
+    f32x4 ak = load4_uc(wk, bytes, lo), av = load4_uc(wv, bytes, lo);
+    for (int s0 = 1; s0 < ns; s0 += 8) {
+        f32x4 xk[8], xv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (s0 + j < ns) {
+                xk[j] = load4_uc(wk + (size_t)(s0 + j) * plane, bytes, lo);
+                xv[j] = load4_uc(wv + (size_t)(s0 + j) * plane, bytes, lo);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (s0 + j < ns) {
+                ak += xk[j];
+                av += xv[j];
+            }
+        }
+    }
+    wg_time(2);
+    if (!ok) ak = av = f32x4{NAN, NAN, NAN, NAN};
+    if (lo < bytes) {
+        store4<T>(static_cast<T *>(p.dk) + off + 4 * tid, ak, -p.scale);
+        store4<T>(static_cast<T *>(p.dv) + off + 4 * tid, av, 1.0f);
+    }
+    wg_time_after_stores();
+}
+
 template <class DqT, class DkvT, bool CAUSAL>
 __device__ __forceinline__ void bwd_fused_entry(const Params &p) {
     static_assert(std::is_same<typename DqT::Pol, typename DkvT::Pol>::value, "one LDS layout");
@@ -818,10 +921,20 @@ __device__ __forceinline__ void bwd_fused_entry(const Params &p) {
     if (bid < p.fused_ndq) {
         const int nbh = p.B * p.Hq;
         dq_body<DqT, CAUSAL, true, true>(p, bid % nbh, bid / nbh, sm.dq);
-    } else {
-        const DkvWork wk = dkv_work(p, bid - p.fused_ndq, 4 * DkvT::ROWS, DkvT::Pol::ROWS, CAUSAL);
+    } else if (bid < p.fused_ndq + p.fused_ndkv) {
+        const int w = bid - p.fused_ndq;
+        const DkvWork wk = dkv_work(p, w, 4 * DkvT::ROWS, DkvT::Pol::ROWS, CAUSAL);
         if (wk.kb * 4 * DkvT::ROWS >= p.N) return;
         dkv_body<DkvT, CAUSAL, true, DqT>(p, wk, sm.dkv);
+        if (p.red_rows > 0) {
+            // the share's planes are in memory once every wave's stores are
+            // acknowledged: then its flag
+            wait_stores();
+            __syncthreads();
+            if (threadIdx.x == 0) store_wt(g_share_flags + (size_t)p.flag_slot * kMaxShareFlags + w, p.epoch);
+        }
+    } else {
+        dkv_reduce_rows<DkvT, CAUSAL>(p, bid - p.fused_ndq - p.fused_ndkv, &sm.dkv.sF[0]);
     }
 }
 
@@ -1008,14 +1121,17 @@ hipError_t launch_bwd_dq(const Params &p, int dtype_bf16, int d, int causal, int
 static std::atomic<unsigned> g_epoch{0};
 static std::atomic<int> g_one_launch{1};
 static std::atomic<int> g_delta_wait_us{200};
+static std::atomic<int> g_reduce_wait_us{2000000};
 
-void set_bwd_options(int one_launch, int delta_wait_us) {
+void set_bwd_options(int one_launch, int delta_wait_us, int reduce_wait_us) {
     g_one_launch.store(one_launch);
     g_delta_wait_us.store(delta_wait_us);
+    g_reduce_wait_us.store(reduce_wait_us);
 }
-void get_bwd_options(int *one_launch, int *delta_wait_us) {
+void get_bwd_options(int *one_launch, int *delta_wait_us, int *reduce_wait_us) {
     *one_launch = g_one_launch.load();
     *delta_wait_us = g_delta_wait_us.load();
+    *reduce_wait_us = g_reduce_wait_us.load();
 }
 
 bool bwd_fused_available(const Params &p, int dtype_bf16, int d, hipStream_t stream) {
@@ -1140,10 +1256,22 @@ static hipError_t launch_fused_k(Params p, int causal, hipStream_t stream) {
     const int wait_us = g_delta_wait_us.load();
     p.delta_wait = wait_us < 0 ? -1 : (int)std::min(100LL * wait_us, 0x7fffffffLL);
     p.fused_ndq = (int)ndq;
+    p.fused_ndkv = (int)ndkv;
+    // a split's reduce runs in the same launch, after the shares, where their
+    // flags fit
+    long long nred = 0;
+    p.red_rows = 0;
+    if (p.dkv_split > 1 && ndkv <= kMaxShareFlags) {
+        constexpr int BKV = 4 * K::Dkv::ROWS, RR = 1024 / K::Dkv::D;
+        nred = (long long)p.B * p.Hkv * ((p.N + BKV - 1) / BKV) * (BKV / RR);
+        p.red_rows = RR;
+        p.red_wait = (int)std::min(100LL * g_reduce_wait_us.load(), 0x7fffffffLL);  // 100 MHz ticks
+    }
+    if (ndq + ndkv + nred > 0x7fffffffLL) return hipErrorInvalidValue;
     const KernelId id = K::kHasP2 && scale_is_pow2(p.scale) ? K::fused_p2[causal ? 1 : 0] : K::fused[causal ? 1 : 0];
     void *args[] = {&p};
-    const hipError_t err = launch_kernel(id, dim3((unsigned)(ndq + ndkv)), dim3(256), args, stream);
-    if (err != hipSuccess || p.dkv_split == 1) return err;
+    const hipError_t err = launch_kernel(id, dim3((unsigned)(ndq + ndkv + nred)), dim3(256), args, stream);
+    if (err != hipSuccess || p.dkv_split == 1 || p.red_rows > 0) return err;
     return launch_dkv_reduce<K>(p, causal, stream);
 }
 

@@ -74,6 +74,14 @@ struct Params {
     int flag_slot, delta_wait, fused_ndq;
     // Causal block order (cu_order_block): 0 = the kernel's own order.
     int qb_period;
+    // One-launch backward: work-groups [fused_ndq, fused_ndq + fused_ndkv)
+    // run the dK/dV pass. With a GQA split and red_rows > 0 the shares write
+    // their planes through to memory and then set their flag in slot
+    // flag_slot of g_share_flags (dkv_work's index) to epoch, and the work-
+    // groups after them each add the planes of red_rows keys of one key block
+    // (dkv_reduce_rows) once its shares' flags are set, polling at most
+    // red_wait ticks; red_rows = 0: a reduce launch follows instead.
+    int fused_ndkv, red_rows, red_wait;
 };
 
 // Where a grid is resident all at once, the dispatcher gives each XCD (work-
@@ -95,6 +103,9 @@ __host__ __device__ inline int cu_order_block(int y, int period) {
 // flags) of kMaxFlagBlocks flags, one per (batch, query head, 128-row block).
 constexpr int kFlagSlots = 4;
 constexpr int kMaxFlagBlocks = 1 << 18;
+// Share flags of the one-launch backward with a GQA split, kFlagSlots slots
+// (as the Delta flags) of kMaxShareFlags, one per dK/dV share.
+constexpr int kMaxShareFlags = 1 << 16;
 
 // Shares of a dK/dV key block whose queries take nqs stages per query head:
 // its group x nqs stages in runs of about dkv_share_stages, never fewer than
@@ -512,6 +523,16 @@ __device__ __forceinline__ void lds_dma4_uc(uint32_t base, const void *src) {
 __device__ __forceinline__ void store_wt(void *dst, uint32_t v) {
     asm volatile("global_store_dword %0, %1, off sc0 sc1" ::"v"(dst), "v"(v) : "memory");
 }
+// A write-through store of four floats.
+__device__ __forceinline__ void store4_wt(float *dst, f32x4 v) {
+    asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" ::"v"(dst), "v"(v) : "memory");
+}
+// Four floats at byte offset off of base (wave-uniform) past the caches;
+// offsets at or past `bytes` read as 0.
+__device__ __forceinline__ f32x4 load4_uc(const float *base, uint32_t bytes, uint32_t off) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), 0, bytes, 0x00020000);
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 17);  // cache policy sc0 | sc1
+}
 // A load past the caches, complete on return (it waits for every outstanding
 // vector-memory operation of the wave).
 __device__ __forceinline__ uint32_t load_uc_sync(const void *src) {
@@ -523,14 +544,16 @@ __device__ __forceinline__ uint32_t load_uc_sync(const void *src) {
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // Timeline build (-DMXFA_WG_TIMELINE: `make timeline`, mxfa_gfx950_timeline.hsaco):
-// thread 0 of every work-group of the forward and of the dQ and dK/dV bodies
-// stamps the 100 MHz real-time counter at its start (0), once its first stage
-// is staged (1), at the end of its loop (2) and once its stores are
+// thread 0 of every work-group of the forward, of the dQ and dK/dV bodies and
+// of the one-launch backward's reduce stamps the 100 MHz real-time counter at
+// its start (0), once its first stage is staged (1; the reduce: once its
+// shares are done), at the end of its loop (2) and once its stores are
 // acknowledged (3), into mxfa_wg_times[8 g + i] for its linear work-group
-// index g ((z Y + y) X + x over the grid, so each split of a split forward
-// has its own slot), and records what it ran: (kind << 32) | block at 8 g + 4 (kind 0 =
-// dQ, block = query block; 1 = dK/dV, block = key block; 2 = forward, block =
-// query block), its stages at 8 g + 5 and where it ran at 8 g + 6 ((XCC_ID
+// index g ((z Y + y) X + x over the grid, so each split of a split forward has
+// its own slot), and records what it ran: (kind << 32) | block at 8 g + 4
+// (kind 0 = dQ, block = query block; 1 = dK/dV, block = key block; 2 =
+// forward, block = query block; 3 = reduce, block = key block), its stages
+// (the reduce: its shares) at 8 g + 5 and where it ran at 8 g + 6 ((XCC_ID
 // << 32) | HW_ID; read by mxfa_probe_wg_times). In every other build these
 // compile to nothing.
 #if defined(__HIP_DEVICE_COMPILE__) && defined(MXFA_WG_TIMELINE)

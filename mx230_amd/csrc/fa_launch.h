@@ -66,12 +66,16 @@ hipError_t launch_bwd_fused(const Params &p, int d, int causal, hipStream_t stre
 // Process-wide settings of the one-launch backward: whether it is used where
 // available, and the bound of each Delta wait in microseconds (< 0: never
 // wait, always compute Delta); read at every launch.
-void set_bwd_options(int one_launch, int delta_wait_us);
-void get_bwd_options(int *one_launch, int *delta_wait_us);
+void set_bwd_options(int one_launch, int delta_wait_us, int reduce_wait_us);
+void get_bwd_options(int *one_launch, int *delta_wait_us, int *reduce_wait_us);
 // Delta blocks the one-launch backward's dK/dV work-groups computed
 // themselves on the current device since the library was loaded (a
 // synchronous copy).
 hipError_t read_delta_fallbacks(unsigned long long *count);
+// Reduce work-groups of the one-launch backward's GQA split whose wait for
+// their shares ran out on the current device since the library was loaded
+// (a synchronous copy).
+hipError_t read_reduce_timeouts(unsigned long long *count);
 // Timeline build only: copies up to `bytes` of the per-work-group timestamps
 // to host `dst` (none when dst is NULL) and reports their size in *avail;
 // hipErrorNotFound when the loaded code object is not the timeline build.

@@ -40,6 +40,7 @@ struct DeviceModule {
     hipModule_t mod = nullptr;
     hipFunction_t fn[kNumKernels] = {};
     void *fallbacks = nullptr;  // the code object's Delta fallback counter
+    void *timeouts = nullptr;   // and its reduce timeout counter
     int cus = 0;                // the device's CUs
     // work-groups of 256 threads of each kernel resident per CU (-1: not asked yet)
     std::atomic<int> occupancy[kNumKernels];
@@ -92,6 +93,7 @@ void unload(DeviceModule &m) {
     if (m.mod != nullptr) (void)hipModuleUnload(m.mod);
     m.mod = nullptr;
     m.fallbacks = nullptr;
+    m.timeouts = nullptr;
     std::memset(m.fn, 0, sizeof(m.fn));
     for (auto &o : m.occupancy) o.store(-1);
     m.cus = 0;
@@ -141,6 +143,14 @@ DeviceModule *module_for(int device, hipError_t *err) {
         return nullptr;
     }
     m.fallbacks = ptr;
+    if (hipModuleGetGlobal(&ptr, &bytes_g, m.mod, "mxfa_reduce_timeouts") != hipSuccess ||
+        bytes_g != sizeof(unsigned long long)) {
+        (void)hipGetLastError();
+        unload(m);
+        *err = hipErrorInvalidImage;
+        return nullptr;
+    }
+    m.timeouts = ptr;
     if (hipDeviceGetAttribute(&m.cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) {
         (void)hipGetLastError();
         m.cus = 0;
@@ -251,6 +261,13 @@ hipError_t read_delta_fallbacks(unsigned long long *count) {
     DeviceModule *m = current_module(&err);
     if (m == nullptr) return err;
     return hipMemcpyDtoH(count, m->fallbacks, sizeof(*count));
+}
+
+hipError_t read_reduce_timeouts(unsigned long long *count) {
+    hipError_t err = hipSuccess;
+    DeviceModule *m = current_module(&err);
+    if (m == nullptr) return err;
+    return hipMemcpyDtoH(count, m->timeouts, sizeof(*count));
 }
 
 }  // namespace mxfa

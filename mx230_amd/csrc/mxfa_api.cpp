@@ -318,19 +318,27 @@ int mxfa_bwd_one_launch(const mxfa_shape *shape) {
 int mxfa_set_bwd_options(const mxfa_bwd_options *options) {
     if (options == nullptr) return MXFA_ERR_NULL;
     if (options->one_launch != 0 && options->one_launch != 1) return MXFA_ERR_SHAPE;
-    mxfa::set_bwd_options(options->one_launch, options->delta_wait_us);
+    if (options->reduce_wait_us < 0) return MXFA_ERR_SHAPE;
+    mxfa::set_bwd_options(options->one_launch, options->delta_wait_us, options->reduce_wait_us);
     return MXFA_OK;
 }
 
 int mxfa_get_bwd_options(mxfa_bwd_options *options) {
     if (options == nullptr) return MXFA_ERR_NULL;
-    mxfa::get_bwd_options(&options->one_launch, &options->delta_wait_us);
+    mxfa::get_bwd_options(&options->one_launch, &options->delta_wait_us, &options->reduce_wait_us);
     return MXFA_OK;
 }
 
 int mxfa_bwd_delta_fallbacks(unsigned long long *count) {
     if (count == nullptr) return MXFA_ERR_NULL;
     const hipError_t e = mxfa::read_delta_fallbacks(count);
+    if (e == hipSuccess) return MXFA_OK;
+    return e == hipErrorInvalidImage ? MXFA_ERR_CODE_OBJECT : MXFA_ERR_DEVICE;
+}
+
+int mxfa_bwd_reduce_timeouts(unsigned long long *count) {
+    if (count == nullptr) return MXFA_ERR_NULL;
+    const hipError_t e = mxfa::read_reduce_timeouts(count);
     if (e == hipSuccess) return MXFA_OK;
     return e == hipErrorInvalidImage ? MXFA_ERR_CODE_OBJECT : MXFA_ERR_DEVICE;
 }

@@ -129,7 +129,7 @@ def test_bwd_workspace_bytes(lib, kw, nbytes):
 
 @pytest.fixture
 def default_options():
-    old = mx.set_bwd_options(one_launch=True, delta_wait_us=200)
+    old = mx.set_bwd_options(one_launch=True, delta_wait_us=200, reduce_wait_us=2000000)
     yield
     mx.set_bwd_options(**old)
 
@@ -137,13 +137,15 @@ def default_options():
 def test_bwd_options(lib, default_options):
     o = mx.MxfaBwdOptions()
     assert lib.mxfa_get_bwd_options(ctypes.byref(o)) == 0
-    assert (o.one_launch, o.delta_wait_us) == (1, 200)
+    assert (o.one_launch, o.delta_wait_us, o.reduce_wait_us) == (1, 200, 2000000)
     assert lib.mxfa_set_bwd_options(None) == mx_status("MXFA_ERR_NULL")
     assert lib.mxfa_get_bwd_options(None) == mx_status("MXFA_ERR_NULL")
-    assert lib.mxfa_set_bwd_options(ctypes.byref(mx.MxfaBwdOptions(2, 5))) == mx_status("MXFA_ERR_SHAPE")
-    assert lib.mxfa_set_bwd_options(ctypes.byref(mx.MxfaBwdOptions(0, -1))) == 0
-    assert mx.get_bwd_options() == {"one_launch": False, "delta_wait_us": -1}
+    assert lib.mxfa_set_bwd_options(ctypes.byref(mx.MxfaBwdOptions(2, 5, 0))) == mx_status("MXFA_ERR_SHAPE")
+    assert lib.mxfa_set_bwd_options(ctypes.byref(mx.MxfaBwdOptions(1, 5, -1))) == mx_status("MXFA_ERR_SHAPE")
+    assert lib.mxfa_set_bwd_options(ctypes.byref(mx.MxfaBwdOptions(0, -1, 0))) == 0
+    assert mx.get_bwd_options() == {"one_launch": False, "delta_wait_us": -1, "reduce_wait_us": 0}
     assert lib.mxfa_bwd_delta_fallbacks(None) == mx_status("MXFA_ERR_NULL")
+    assert lib.mxfa_bwd_reduce_timeouts(None) == mx_status("MXFA_ERR_NULL")
 
 
 def test_bwd_one_launch(lib, default_options):
@@ -372,7 +374,7 @@ def test_code_object_host_check(lib, tmp_path):
 
 def test_code_object_has_every_kernel():
     """Every kernel fa_kernels.h names is a global function of the code object,
-    and the Delta fallback counter the library reads by name is there."""
+    and the counters the library reads by name are there."""
     readelf = "/opt/rocm/llvm/bin/llvm-readelf"
     if not os.path.exists(readelf):
         pytest.skip("llvm-readelf is not installed")
@@ -384,7 +386,7 @@ def test_code_object_has_every_kernel():
     funcs = set(re.findall(r"FUNC\s+GLOBAL\s+\w+\s+\d+\s+(mxfa_\w+)", out))
     objects = set(re.findall(r"OBJECT\s+GLOBAL\s+\w+\s+\d+\s+(mxfa_\w+)", out))
     assert names <= funcs, sorted(names - funcs)
-    assert "mxfa_delta_fallbacks" in objects
+    assert {"mxfa_delta_fallbacks", "mxfa_reduce_timeouts"} <= objects
 
 
 def test_library_has_no_kernels():
