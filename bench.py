@@ -554,18 +554,21 @@ def timeline(a):
     out = {"shape": {"B": B, "Hq": H, "Hkv": Hkv, "N": N, "d": d, "causal": causal},
            "dkv_partial_planes": int(max(nws // (8 * B * Hkv * N * d), 1))}
     mx.run_flash_lse(q, k, v, o, lse, causal)
-    # the backward's work-groups: dQ, then dK/dV; rows past them are zero, an
-    # earlier launch's (older stamps) or the forward's
+    # the backward's work-groups: dQ, then dK/dV, then (GQA split) the reduce;
+    # rows past them are zero, an earlier launch's (older stamps) or the
+    # forward's
     warm(lambda: mx.run_bwd_ws(q, k, v, o, do, lse, delta, dq, dk, dv, ws, causal))
     mx.run_bwd_ws(q, k, v, o, do, lse, delta, dq, dk, dv, ws, causal)
     torch.cuda.synchronize()
     full = mx.probe_wg_times().astype(np.int64)
     kind = full[:, 4] >> 32
     ndq = int(np.argmin(kind == 0))
-    cur = (kind[ndq:] == 1) & (full[ndq:, 0] >= full[:ndq, 0].min())
+    cur = ((kind[ndq:] == 1) | (kind[ndq:] == 3)) & (full[ndq:, 0] >= full[:ndq, 0].min())
     nwg = len(full) if cur.all() else ndq + int(np.argmin(cur))
     full = full[:nwg]
-    out["backward"] = _timeline_launch(full, [0, 1], ["dq", "dkv"])
+    red = bool((kind[:nwg] == 3).any())
+    out["backward"] = _timeline_launch(full, [0, 1, 3] if red else [0, 1],
+                                       ["dq", "dkv", "reduce"] if red else ["dq", "dkv"])
     # the forward's work-groups: the leading rows it stamped (kind 2)
     warm(lambda: mx.run_flash_lse(q, k, v, o, lse, causal))
     mx.run_flash_lse(q, k, v, o, lse, causal)
@@ -755,6 +758,7 @@ def main():
         step(launches)
     torch.cuda.synchronize()
     fb0 = mx.bwd_delta_fallbacks() if one else 0
+    rt0 = mx.bwd_reduce_timeouts() if one else 0
 
     # timed region: exactly K backward steps, synchronised on both sides, with
     # an event on the launch stream before each step and after the last: the
@@ -850,6 +854,8 @@ def main():
         # Delta blocks whose wait ran out in the timed regions (0 expected;
         # results are the same either way)
         res["delta_fallbacks"] = mx.bwd_delta_fallbacks() - fb0
+        # GQA split reduce waits that ran out (0 expected; NaN rows otherwise)
+        res["reduce_timeouts"] = mx.bwd_reduce_timeouts() - rt0
     if passes is not None:
         res["passes_ms"] = {n: round(t, 4) for n, t in passes.items()}
     if not a.no_probe:
