@@ -11,11 +11,12 @@ themselves after a wait bounded in time.
   compute Delta from O and dO with the dQ work-groups' own arithmetic, so the
   results are still bitwise equal, and the device's fallback counter grows by
   one per stage.
-- With a GQA split through a workspace, the one launch plus the reduce equal
-  the two-launch split bitwise.
+- With a GQA split through a workspace, the one launch (whose last work-groups
+  add the shares' partial sums once the shares' flags are set) equals the
+  two-launch split (with its reduce launch) bitwise.
 - Launches in flight together on several streams, more than the flag slots,
-  so later launches see other launches' flags, still give each one its own
-  result, bitwise.
+  so later launches see other launches' flags (Delta and, with a GQA split,
+  share flags), still give each one its own result, bitwise.
 """
 from __future__ import annotations
 
@@ -141,6 +142,39 @@ def test_one_launch_concurrent_streams(opts):
         with torch.cuda.stream(s):
             outs.append(_bwd(t, True, stream=s))
     torch.cuda.synchronize()
+    for i, (got, ref) in enumerate(zip(outs, refs)):
+        for n, a, b in zip(("Delta", "dQ", "dK", "dV"), got, ref):
+            assert torch.equal(a, b), (i, n)
+
+
+def test_one_launch_concurrent_streams_gqa_split(opts):
+    """Six GQA-split launches in flight on six streams, each with its own
+    workspace (four slots of share flags)."""
+    import torch
+    import mx230_amd as mx
+    cases = [_setup(2, 6, 2, 1000 + 64 * i, 64, True, seed=40 + i) for i in range(6)]
+    wss = [torch.empty(mx.bwd_workspace_bytes(t[0], t[1], True), dtype=torch.uint8, device="cuda") for t in cases]
+    assert all(w.numel() > 0 for w in wss)
+
+    def bwd(t, ws, stream=None):
+        q, k, v, do, o, lse = t
+        delta = torch.empty_like(lse)
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        mx.run_bwd_ws(q, k, v, o, do, lse, delta, dq, dk, dv, ws, True, stream=stream)
+        return delta, dq, dk, dv
+
+    opts(one_launch=False)
+    refs = [_sync(bwd(t, w)) for t, w in zip(cases, wss)]
+    opts(one_launch=True)
+    t0 = mx.bwd_reduce_timeouts()
+    streams = [torch.cuda.Stream() for _ in cases]
+    torch.cuda.synchronize()
+    outs = []
+    for t, w, s in zip(cases, wss, streams):
+        with torch.cuda.stream(s):
+            outs.append(bwd(t, w, stream=s))
+    torch.cuda.synchronize()
+    assert mx.bwd_reduce_timeouts() == t0
     for i, (got, ref) in enumerate(zip(outs, refs)):
         for n, a, b in zip(("Delta", "dQ", "dK", "dV"), got, ref):
             assert torch.equal(a, b), (i, n)
