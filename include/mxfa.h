@@ -228,9 +228,10 @@ int mxfa_bwd_reduce_timeouts(unsigned long long *count);
  * from the diagonal) over several work-groups, a causal block with more
  * queries over more of them: each writes fp32 partial dK/dV sums to the
  * workspace, and they are added in a fixed order (deterministic, atomic-free)
- * by the last work-groups of the one-launch backward, else by a second launch. The size is 2 * planes * B * Hkv * N * d * 4 bytes, planes
- * being the most work-groups any key block takes; 0 when no split helps
- * (always without GQA).
+ * by the last work-groups of the one-launch backward, else by a second
+ * launch. The size is 2 * planes * B * Hkv * N * d * 4 bytes, planes being
+ * the most work-groups any key block takes; 0 when no split helps (always
+ * without GQA).
  * The reference has no GQA (d = 64, one head, attention_bwd.cu:165-243); this
  * sizes the scratch of its dK/dV pass generalised to GQA groups. */
 size_t mxfa_bwd_workspace_bytes(const mxfa_shape *shape);

@@ -1240,7 +1240,8 @@ int dkv_split(const Params &p, int dtype_bf16, int d, int causal) {
 template <class K>
 static hipError_t launch_fused_k(Params p, int causal, hipStream_t stream) {
     // with a workspace, GQA shapes split each group's query heads as in the
-    // dK/dV pass; the shares' partial sums are added by a second launch
+    // dK/dV pass; the shares' partial sums are added by the launch's last
+    // work-groups (dkv_reduce_rows), else by a second launch
     dkv_plan_t<typename K::Dkv>(p, causal != 0);
     if (p.dkv_ws == nullptr) p.dkv_split = 1;
     if (p.dkv_split == 1) p.dkv_ws = nullptr;

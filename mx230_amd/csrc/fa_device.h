@@ -61,7 +61,8 @@ struct Params {
     // dkv_block_shares(...) contiguous runs, one work-group each; share s
     // writes fp32 partial sums to plane s of dkv_ws ([dkv_split][B*Hkv][N][d]
     // for dK, then the same for dV; dkv_split = the most shares of any block)
-    // and a reduce launch adds each block's planes in share order.
+    // and each block's planes are added in share order, by a reduce launch
+    // or by the one-launch backward's last work-groups (red_rows below).
     float *dkv_ws;
     int dkv_split, dkv_min_shares, dkv_share_stages;
     // One-launch backward (bwd_fused_entry, kernels mxfa_bwd_*): work-groups [0, fused_ndq) run

@@ -59,8 +59,9 @@ hipError_t launch_bwd_dkv(const Params &p, int dtype_bf16, int d, int causal, hi
 // partial planes of the split (the most shares of any key block; 1: none)
 int dkv_split(const Params &p, int dtype_bf16, int d, int causal);
 // The one-launch backward from O (dQ pass with Delta + dK/dV pass, bf16;
-// with p.dkv_ws a GQA split as launch_bwd_dkv, whose reduce then follows as a
-// second launch): available for the shape, and launched with its own epoch.
+// with p.dkv_ws a GQA split as launch_bwd_dkv, whose reduce runs in the same
+// launch, or as a second launch where the share flags do not fit): available
+// for the shape, and launched with its own epoch.
 bool bwd_fused_available(const Params &p, int dtype_bf16, int d, hipStream_t stream);
 hipError_t launch_bwd_fused(const Params &p, int d, int causal, hipStream_t stream);
 // Process-wide settings of the one-launch backward: whether it is used where
