@@ -826,7 +826,7 @@ union FusedSmem {
 };
 
 // The reduce of a GQA split inside the one-launch backward: work-group r adds
-// the shares' planes for red_rows = 1024 / d keys of one key block (one float4
+// the shares' planes for red_rows = 16 keys of one key block (d / 64 float4s
 // of each plane per thread), in share order, as dkv_reduce_body does. Work-
 // groups go key block 0 first (the shares' order), then (batch, KV head),
 // then the block's chunk of rows. The shares have lower indices, so each is
@@ -837,8 +837,8 @@ template <class Tile, bool CAUSAL>
 __device__ __forceinline__ void dkv_reduce_rows(const Params &p, int r, uint32_t *s_ok) {
     using T = typename Tile::Pol::T;
     constexpr int D = Tile::D, BKV = 4 * Tile::ROWS, BQ = Tile::Pol::ROWS;
-    constexpr int RR = 1024 / D, NCH = BKV / RR;
-    static_assert(BKV % RR == 0, "a key block is whole chunks");
+    constexpr int RR = 16, NCH = BKV / RR, V = RR * D / 1024;  // V: float4s per thread per plane
+    static_assert(BKV % RR == 0 && V * 1024 == RR * D, "a key block is whole chunks of whole float4 rows");
     const int N = p.N, nbkv = p.B * p.Hkv;
     const int c = r % NCH, bkv = (r / NCH) % nbkv, kb = r / (NCH * nbkv);
     const int key0 = kb * BKV + c * RR;
@@ -884,31 +884,45 @@ __device__ __forceinline__ void dkv_reduce_rows(const Params &p, int r, uint32_t
     const size_t plane = (size_t)p.B * p.Hkv * N * D;
     const size_t off = ((size_t)bkv * N + key0) * D;  // the chunk's first element
     const uint32_t bytes = (uint32_t)(min(RR, N - key0) * D * 4);
-    const uint32_t lo = 16u * tid;
     const float *wk = p.dkv_ws + off, *wv = p.dkv_ws + (size_t)p.dkv_split * plane + off;
-    f32x4 ak = load4_uc(wk, bytes, lo), av = load4_uc(wv, bytes, lo);
+    f32x4 ak[V], av[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+        ak[v] = load4_uc(wk, bytes, 16u * (tid + 256 * v));
+        av[v] = load4_uc(wv, bytes, 16u * (tid + 256 * v));
+    }
     for (int s0 = 1; s0 < ns; s0 += 8) {
-        f32x4 xk[8], xv[8];
+        f32x4 xk[8][V], xv[8][V];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             if (s0 + j < ns) {
-                xk[j] = load4_uc(wk + (size_t)(s0 + j) * plane, bytes, lo);
-                xv[j] = load4_uc(wv + (size_t)(s0 + j) * plane, bytes, lo);
+#pragma unroll
+                for (int v = 0; v < V; ++v) {
+                    xk[j][v] = load4_uc(wk + (size_t)(s0 + j) * plane, bytes, 16u * (tid + 256 * v));
+                    xv[j][v] = load4_uc(wv + (size_t)(s0 + j) * plane, bytes, 16u * (tid + 256 * v));
+                }
             }
         }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             if (s0 + j < ns) {
-                ak += xk[j];
-                av += xv[j];
+#pragma unroll
+                for (int v = 0; v < V; ++v) {
+                    ak[v] += xk[j][v];
+                    av[v] += xv[j][v];
+                }
             }
         }
     }
     wg_time(2);
-    if (!ok) ak = av = f32x4{NAN, NAN, NAN, NAN};
-    if (lo < bytes) {
-        store4<T>(static_cast<T *>(p.dk) + off + 4 * tid, ak, -p.scale);
-        store4<T>(static_cast<T *>(p.dv) + off + 4 * tid, av, 1.0f);
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+        if (!ok) ak[v] = av[v] = f32x4{NAN, NAN, NAN, NAN};
+        const uint32_t i4 = tid + 256 * v;  // the chunk's float4 index
+        if (16u * i4 < bytes) {
+            store4<T>(static_cast<T *>(p.dk) + off + 4 * i4, ak[v], -p.scale);
+            store4<T>(static_cast<T *>(p.dv) + off + 4 * i4, av[v], 1.0f);
+        }
     }
     wg_time_after_stores();
 }
@@ -1263,7 +1277,7 @@ static hipError_t launch_fused_k(Params p, int causal, hipStream_t stream) {
     long long nred = 0;
     p.red_rows = 0;
     if (p.dkv_split > 1 && ndkv <= kMaxShareFlags) {
-        constexpr int BKV = 4 * K::Dkv::ROWS, RR = 1024 / K::Dkv::D;
+        constexpr int BKV = 4 * K::Dkv::ROWS, RR = 16;  // dkv_reduce_rows' keys per work-group
         nred = (long long)p.B * p.Hkv * ((p.N + BKV - 1) / BKV) * (BKV / RR);
         p.red_rows = RR;
         p.red_wait = (int)std::min(100LL * g_reduce_wait_us.load(), 0x7fffffffLL);  // 100 MHz ticks
