@@ -110,6 +110,14 @@ def test_split_ragged(causal, n):
     _check(f"split-n{n}", q, k, v, do, causal, True, kvh=1)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_split_d128_ragged(causal):
+    """d = 128 with a ragged N (the last 16-key chunk of the in-launch reduce
+    half past N) and an 8:1 group."""
+    q, k, v, do = make_inputs(1, 16, 2, 1000, 128, bf16=True, seeds=(71, 72, 73, 74))
+    _check(f"split-d128-n1000-{'c' if causal else 'n'}", q, k, v, do, causal, True, kvh=1)
+
+
 @pytest.mark.parametrize("hq,n", [(8, 643), (10, 836)], ids=["g4-n643", "g5-n836"])
 def test_split_share_starts_inside_the_diagonal(hq, n):
     """Shares are runs of a key block's (query head, stage) list: at these
