@@ -845,16 +845,8 @@ __device__ __forceinline__ void dkv_reduce_rows(const Params &p, int r, uint32_t
     if (key0 >= N) return;
     wg_time(0);
     // the block's shares are dkv_work indices [w0, w0 + ns)
-    int w0, ns;
-    if (CAUSAL) {
-        w0 = 0;
-        for (int k = 0; k < kb; ++k) w0 += nbkv * dkv_block_shares(p, (N - k * BKV + BQ - 1) / BQ);
-        ns = dkv_block_shares(p, (N - kb * BKV + BQ - 1) / BQ);
-    } else {
-        ns = dkv_block_shares(p, (N + BQ - 1) / BQ);
-        w0 = kb * nbkv * ns;
-    }
-    w0 += bkv * ns;
+    const int w0 = dkv_first_work(p, bkv, kb, BKV, BQ, CAUSAL);
+    const int ns = dkv_block_shares(p, (N - (CAUSAL ? kb * BKV : 0) + BQ - 1) / BQ);
     wg_info(3, kb, ns);
     const int tid = threadIdx.x;
     if (tid < 64) {

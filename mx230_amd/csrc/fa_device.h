@@ -92,7 +92,9 @@ struct Params {
 // build: per-CU stage counts 52-80 against a mean of 66 for 1024 forward work-
 // groups of a causal B1 H32 N2048, and CU end times following them). Reversing
 // every other run of S block indices gives each CU blocks whose work (affine
-// in the index) sums to the same total. period <= 1: y itself.
+// in the index) sums to the same total when the runs pair up (an even count;
+// an odd count leaves the last run's spread, under S stages). period <= 1: y
+// itself.
 __host__ __device__ inline int cu_order_block(int y, int period) {
     if (period <= 1) return y;
     const int k = y / period, r = y - k * period;
@@ -139,6 +141,17 @@ __host__ __device__ inline DkvWork dkv_work(const Params &p, int w, int bkv_rows
         w -= nbkv * ns;
     }
     return {0, nkb, 0, 1};
+}
+
+// The dkv_work index of share 0 of key block kb of (batch, KV head) bkv; the
+// block's other shares follow it.
+__host__ __device__ inline int dkv_first_work(const Params &p, int bkv, int kb, int bkv_rows, int bq, bool causal) {
+    const int nbkv = p.B * p.Hkv;
+    if (p.dkv_split <= 1) return kb * nbkv + bkv;
+    if (!causal) return (kb * nbkv + bkv) * dkv_block_shares(p, (p.N + bq - 1) / bq);
+    int w = 0;
+    for (int k = 0; k < kb; ++k) w += nbkv * dkv_block_shares(p, (p.N - k * bkv_rows + bq - 1) / bq);
+    return w + bkv * dkv_block_shares(p, (p.N - kb * bkv_rows + bq - 1) / bq);
 }
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }

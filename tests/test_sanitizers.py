@@ -2,7 +2,8 @@
 AddressSanitizer + UndefinedBehaviorSanitizer and its threaded multi-head paths
 under ThreadSanitizer (oracle/Makefile targets `sanitize` / `tsan`), and the C
 ABI's host-side argument checks under AddressSanitizer +
-UndefinedBehaviorSanitizer (tests/sanitize/Makefile; nothing is launched)."""
+UndefinedBehaviorSanitizer (tests/sanitize/Makefile; nothing is launched), and
+the kernels' shared work orders (tests/sanitize/order_selftest.cpp)."""
 from __future__ import annotations
 
 import os
@@ -40,3 +41,12 @@ def test_abi_host_asan_ubsan():
     # the HIP runtime's own allocations are not the library's: no leak check
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=1", UBSAN_OPTIONS="print_stacktrace=1")
     assert "all checks passed" in _run([os.path.join(ROOT, "tests", "sanitize", "_build", "abi_selftest")], env)
+
+
+@pytest.mark.skipif(not os.path.exists("/opt/rocm/bin/hipcc"), reason="hipcc is not installed")
+def test_work_orders_asan_ubsan():
+    """The block order of resident causal grids (cu_order_block) and the GQA
+    split's share indices (dkv_first_work against dkv_work), host side."""
+    _run(["make", "-s", "-j8", "-C", os.path.join(ROOT, "tests", "sanitize")])
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=1", UBSAN_OPTIONS="print_stacktrace=1")
+    assert "all checks passed" in _run([os.path.join(ROOT, "tests", "sanitize", "_build", "order_selftest")], env)
