@@ -83,6 +83,9 @@ struct Params {
     // (dkv_reduce_rows) once its shares' flags are set, polling at most
     // red_wait ticks; red_rows = 0: a reduce launch follows instead.
     int fused_ndkv, red_rows, red_wait;
+    // A prefill launch (contiguous or paged cache): the tiles are chosen as
+    // the paged cache's kernels allow, so both give the same bits.
+    int prefill;
 };
 
 // Where a grid is resident all at once, the dispatcher gives each XCD (work-

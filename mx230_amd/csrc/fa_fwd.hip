@@ -612,20 +612,25 @@ static hipError_t launch_fwd_qt(Params p, hipStream_t stream) {
 }
 
 // bf16 launches whose 128-query work-groups would not fill every resident
-// slot (256 CUs x 3) take 64-query work-groups (one 16-query tile per wave):
-// twice the work-groups and half the critical path (the heaviest block's keys
-// times its queries), for twice the LDS reads per MFMA. Measured on the
-// MI355X: causal B1 H12 N4096 d64 54.3 -> 40.3 us, B1 H8 N2048 d128 43.4 ->
-// 28.8 us, non-causal B1 H12 N4096 d64 74.6 -> 65.5 us; at 768 work-groups
-// (causal B1 H12 N8192 d64) 125 against 135 us keeps 128 queries. Non-causal
-// d = 128 keeps them (B1 H8 N4096: 77.2 against 80.2 us).
-constexpr long long kFwdSmallGrid = 768;
-
+// slot (256 CUs x the 128-query kernel's waves per SIMD: 3 at d = 64, 2 at
+// d = 128) take 64-query work-groups (one 16-query tile per wave): twice the
+// work-groups and half the critical path (the heaviest block's keys times its
+// queries), for twice the LDS reads per MFMA. Measured on the MI355X: causal
+// B1 H12 N4096 d64 54.3 -> 40.3 us, B1 H8 N2048 d128 43.4 -> 28.8 us,
+// non-causal B1 H12 N4096 d64 74.6 -> 65.5 us; at 768 work-groups (causal B1
+// H12 N8192 d64) 125 against 135 us keeps 128 queries, and so does d = 128 at
+// 512 (causal B1 H32 Hkv4 N2048: 44.6 against 45.5 us). Non-causal d = 128
+// keeps them (B1 H8 N4096: 77.2 against 80.2 us). A d = 128 prefill takes
+// 64-query work-groups at any grid, as its paged form must (the 128-query
+// d = 128 kernel would spill with the block-table registers): the wave's
+// rows decide when the lazy rescale redoes a stage, so both tilings must match
+// for the paged prefill to give the contiguous one's bits.
 template <class Pol, bool CAUSAL>
 static hipError_t launch_fwd_t(const Params &p, hipStream_t stream) {
     if constexpr (Pol::kExactScale && (CAUSAL || Pol::D == 64)) {
+        constexpr long long kSlots = 256LL * Pol::kWavesFwdCausal;
         const long long wg = (long long)p.B * p.Hq * ((p.N + 127) / 128);
-        if (wg < kFwdSmallGrid || (Pol::D == 128 && p.block_table != nullptr))
+        if (wg < kSlots || (Pol::D == 128 && p.prefill != 0))
             return launch_fwd_qt<Pol, CAUSAL, 1>(p, stream);
     }
     if constexpr (!Pol::kExactScale) return launch_fwd_qt<Pol, CAUSAL, 1>(p, stream);  // fp32: see the kernels

@@ -436,6 +436,7 @@ Params prefill_params(const mxfa_prefill_shape *s, const void *q, const void *kc
     p.q_bs = p.o_bs = p.kv_bs = 0;
     p.Nk = s->pos0 + s->n_tok;
     p.pos0 = s->pos0;
+    p.prefill = 1;
     if (s->n_tok == 1 && s->n_head > s->n_kv_head) {
         // A single row (decode-like): the query heads of a GQA group become the
         // rows of one block per KV head, so each K/V stage staged serves the

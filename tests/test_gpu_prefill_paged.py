@@ -104,6 +104,13 @@ def test_paged_large_grid_bf16():
     _paged_case(n_tok=3072, pos0=512, nh=32, nkv=4, hd=64, bs=16, bf16=True, seed=9)
 
 
+def test_paged_large_grid_d128_bf16():
+    """d = 128 at a grid that the training forward would run on 128-query
+    work-groups (768 of them): the prefill keeps the 64-query tiling of its
+    paged form, so the two stay bitwise equal."""
+    _paged_case(n_tok=3072, pos0=256, nh=32, nkv=4, hd=128, bs=16, bf16=True, seed=21)
+
+
 @pytest.mark.parametrize("bs", [1, 16, 256])
 @pytest.mark.parametrize("n_tok,pos0", [(512, 3584), (1, 4095), (960, 100)])
 def test_paged_split_equals_contiguous_split_bf16(bs, n_tok, pos0):
