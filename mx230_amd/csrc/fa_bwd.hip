@@ -610,8 +610,10 @@ template <class Tile, bool CAUSAL, bool DELTA>
 __device__ __forceinline__ void dq_entry(const Params &p) {
     __shared__ DqSmem<typename Tile::Pol> sm;
     const int nqb = (p.N + 4 * Tile::ROWS - 1) / (4 * Tile::ROWS);
-    const int qb = CAUSAL ? (nqb - 1 - cu_order_block((int)blockIdx.y, p.qb_period)) : (int)blockIdx.y;
-    dq_body<Tile, CAUSAL, DELTA>(p, blockIdx.x, qb, sm);
+    const int i = (int)(blockIdx.y * gridDim.x + blockIdx.x);
+    const int rank = CAUSAL ? cu_order_wg(i, p.cu_run, p.cu_runs) : i;  // heaviest first, balanced per CU
+    const int qb = CAUSAL ? nqb - 1 - rank / (int)gridDim.x : rank / (int)gridDim.x;
+    dq_body<Tile, CAUSAL, DELTA>(p, rank % (int)gridDim.x, qb, sm);
 }
 
 // ---------------------------------------------------------------- dK/dV pass
@@ -1111,7 +1113,7 @@ static hipError_t launch_dq_k(Params p, int causal, int delta, hipStream_t strea
     constexpr int BQ = 4 * K::Dq::ROWS;
     const dim3 grid(p.B * p.Hq, (p.N + BQ - 1) / BQ);
     const KernelId id = K::dq[causal ? 1 : 0][delta ? 1 : 0];
-    p.qb_period = causal ? cu_balance_period(id, grid.x, grid.y) : 0;
+    if (causal) cu_balance(&p, id, (long long)grid.x * grid.y);
     void *args[] = {&p};
     return launch_kernel(id, grid, dim3(256), args, stream);
 }

@@ -73,8 +73,10 @@ struct Params {
     // (delta_wait < 0: always compute it).
     unsigned epoch;
     int flag_slot, delta_wait, fused_ndq;
-    // Causal block order (cu_order_block): 0 = the kernel's own order.
-    int qb_period;
+    // Causal work order of a launch whose first work-groups are resident at
+    // once (cu_order_wg): runs of cu_run linear work-group indices, every
+    // other one of the first cu_runs reversed; cu_runs < 2: the kernel's own.
+    int cu_run, cu_runs;
     // One-launch backward: work-groups [fused_ndq, fused_ndq + fused_ndkv)
     // run the dK/dV pass. With a GQA split and red_rows > 0 the shares write
     // their planes through to memory and then set their flag in slot
@@ -88,20 +90,24 @@ struct Params {
     int prefill;
 };
 
-// Where a grid is resident all at once, the dispatcher gives each XCD (work-
-// groups i mod 8) its work-groups in order and places them round robin on its
-// 32 CUs, so with bh = B Hq a multiple of 8 that divides 256 one CU holds one
-// head's blocks y, y + S, y + 2S, ... for S = 256 / bh (seen in the timeline
-// build: per-CU stage counts 52-80 against a mean of 66 for 1024 forward work-
-// groups of a causal B1 H32 N2048, and CU end times following them). Reversing
-// every other run of S block indices gives each CU blocks whose work (affine
-// in the index) sums to the same total when the runs pair up (an even count;
-// an odd count leaves the last run's spread, under S stages). period <= 1: y
-// itself.
-__host__ __device__ inline int cu_order_block(int y, int period) {
-    if (period <= 1) return y;
-    const int k = y / period, r = y - k * period;
-    return (k & 1) ? k * period + period - 1 - r : y;
+// Where a launch's first work-groups are resident at once, the dispatcher
+// gives work-group i (linear index, x fastest) to XCD i mod 8, and each XCD
+// deals its work-groups round robin over its CUs, so with C CUs i and i + C
+// land on the same CU (seen in the timeline build's HW_ID and XCC_ID fields:
+// for 1024 forward work-groups of a causal B1 H32 N2048, per-CU stage counts
+// 52-80 against a mean of 66, and CU end times following them). A causal
+// launch runs its work heaviest first, so CU c's first work-groups take ranks
+// c, c + C, c + 2C, ..., whose stages all fall with c. Reversing every other
+// run of C ranks among the resident ones gives each CU one heavy and one light
+// rank per pair of runs: the same stages for every CU when the runs pair up
+// (the work falling steadily with the rank), an odd last run's spread
+// otherwise. Work-groups past `runs` runs (dispatched as slots free up) keep
+// their order. run <= 1 or runs < 2: i itself.
+__host__ __device__ inline int cu_order_wg(int i, int run, int runs) {
+    if (run <= 1 || runs < 2) return i;
+    const int k = i / run;
+    if (k >= runs || (k & 1) == 0) return i;
+    return k * run + run - 1 - (i - k * run);
 }
 
 // Delta flags of the one-launch backward: kFlagSlots slots (one per launch,

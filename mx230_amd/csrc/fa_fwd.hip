@@ -311,10 +311,13 @@ __device__ __forceinline__ void fwd_entry(const Params &p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, l16 = lane & 15;
     const int N = p.N, Nk = p.Nk, pos0 = p.pos0;
-    const int bh = blockIdx.x;
     const int nqb = (N + BQ - 1) / BQ;
-    // heaviest first (the order balanced per CU where the grid is resident at once)
-    const int qb = CAUSAL ? (nqb - 1 - cu_order_block((int)blockIdx.y, p.qb_period)) : (int)blockIdx.y;
+    // causal: heaviest first, in the order balanced per CU over the work-groups
+    // resident at once (cu_order_wg; ranks are heads fastest)
+    const int rank = CAUSAL ? cu_order_wg((int)(blockIdx.y * gridDim.x + blockIdx.x), p.cu_run, p.cu_runs)
+                            : (int)(blockIdx.y * gridDim.x + blockIdx.x);
+    const int bh = rank % (int)gridDim.x;
+    const int qb = CAUSAL ? nqb - 1 - rank / (int)gridDim.x : rank / (int)gridDim.x;
     const int b = bh / p.Hq, h = bh % p.Hq, kvh = h / p.group;
     const T *Q = static_cast<const T *>(p.q) + b * p.q_bs + h * p.q_hs;
     const size_t kvoff = b * p.kv_bs + kvh * p.kv_hs;
@@ -606,7 +609,7 @@ static hipError_t launch_fwd_qt(Params p, hipStream_t stream) {
         if ((long long)grid.x * grid.y >= 256LL * kHi && p.block_table == nullptr) wps = kHi;
     }
     const KernelId id = fwd_kernel_id<Pol, CAUSAL>(wps, QT, p.block_table != nullptr);
-    p.qb_period = CAUSAL ? cu_balance_period(id, grid.x, grid.y) : 0;
+    if (CAUSAL) cu_balance(&p, id, (long long)grid.x * grid.y);
     void *args[] = {&p};
     return launch_kernel(id, grid, dim3(256), args, stream);
 }

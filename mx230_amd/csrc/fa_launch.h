@@ -35,11 +35,13 @@ hipError_t launch_kernel(KernelId id, dim3 grid, dim3 block, void **args, hipStr
 // resident at once per CU (the runtime's occupancy); 0 when unknown.
 int device_cus();
 int kernel_occupancy(KernelId id);
-// The period of the block order (Params::qb_period) that gives every CU the
-// same work when all bh x nblocks work-groups of kernel `id` (bh fastest; a
-// block's work an affine function of its index) are resident at once; 0 when
-// that does not apply. See cu_order_block (fa_device.h).
-int cu_balance_period(KernelId id, long long bh, long long nblocks);
+// Sets p->cu_run and p->cu_runs (cu_order_wg, fa_device.h) for a causal
+// launch of `groups` work-groups of kernel `id`: the device's CUs, and the
+// whole runs of them among the work-groups resident at once (the CUs times
+// the kernel's occupancy); no reordering where the CUs are not a multiple of
+// the 8 XCDs, fewer than two runs are resident, or the launch holds more than
+// 1.5 times the resident work-groups.
+void cu_balance(Params *p, KernelId id, long long groups);
 
 hipError_t launch_fwd(const Params &p, int dtype_bf16, int d, int causal, hipStream_t stream);
 // The causal forward with its keys split over work-groups (grid.z) and a

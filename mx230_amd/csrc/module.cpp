@@ -10,6 +10,7 @@
 #include <dlfcn.h>
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cstdint>
 #include <cstring>
@@ -218,17 +219,23 @@ int kernel_occupancy(KernelId id) {
     return n;
 }
 
-int cu_balance_period(KernelId id, long long bh, long long nblocks) {
-    constexpr long long kXcds = 8;  // MI355X: 8 XCDs of 32 CUs
+void cu_balance(Params *p, KernelId id, long long groups) {
+    constexpr int kXcds = 8;  // MI355X: 8 XCDs of 32 CUs
+    p->cu_run = p->cu_runs = 0;
     const int cus = device_cus();
-    if (cus <= 0 || cus % kXcds != 0 || bh <= 0 || bh % kXcds != 0) return 0;
-    const long long per_xcd = cus / kXcds, heads = bh / kXcds;  // a head's blocks stay on one XCD
-    if (per_xcd % heads != 0) return 0;
-    const long long period = per_xcd / heads;
-    if (period < 2 || nblocks % period != 0 || nblocks / period < 2) return 0;
+    if (cus <= 0 || cus % kXcds != 0) return;
     const int occ = kernel_occupancy(id);
-    if (occ <= 0 || bh * nblocks > (long long)cus * occ) return 0;  // not all resident at once
-    return (int)period;
+    if (occ <= 0) return;
+    const long long resident = std::min(groups, (long long)cus * occ);
+    const long long runs = resident / cus;
+    // launches of more than 1.5 rounds of resident work-groups keep their
+    // order: their later rounds, handed out heaviest first as slots free up,
+    // balance the CUs already (A/B, forward, median of 6, us: north star 109.9
+    // plain against 111.5 reordered, B4 H12 N4000 108.0 against 110.4; cfg4,
+    // 1.17 rounds, 70.1 against 67.0)
+    if (runs < 2 || 2 * groups > 3 * resident) return;
+    p->cu_run = cus;
+    p->cu_runs = (int)runs;
 }
 
 hipError_t launch_kernel(KernelId id, dim3 grid, dim3 block, void **args, hipStream_t stream) {

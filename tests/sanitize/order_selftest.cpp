@@ -2,16 +2,16 @@
 // (mx230_amd/csrc/fa_device.h), under AddressSanitizer and
 // UndefinedBehaviorSanitizer; nothing touches a device. Exit status 0 = all
 // checks passed.
-//  * cu_order_block: a permutation of the block indices whenever the period
-//    divides their count; and, for a causal grid resident all at once that
-//    the dispatcher places work-group i on XCD i mod 8 and, within the XCD,
-//    round robin over its 32 CUs, every CU gets the same number of stages
-//    when the runs of `period` blocks pair up (an even count of them), and
-//    stages within period - 1 of each other otherwise (the last run alone),
-//    where the plain order spreads them by (runs) x (period - 1).
+//  * cu_order_wg: a permutation of the work-group indices; and, under the
+//    dispatcher model (work-group i on XCD i mod 8, then round robin over
+//    that XCD's CUs, so i and i + 256 share a CU), the resident work-groups of
+//    a causal launch (heaviest first, heads fastest) give every CU the same
+//    stages up to one per pair of runs of 256, plus one run's spread when
+//    their count is odd.
 //  * dkv_first_work: share 0 of each (batch, KV head, key block) is the
 //    dkv_work index whose work is that block's share 0, and the block's shares
 //    are the indices after it, for split and unsplit, causal and not.
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <vector>
@@ -32,43 +32,51 @@ static int g_fail = 0;
     } while (0)
 
 static void check_cu_order() {
-    // a permutation for every period that divides the count
-    for (int n = 1; n <= 96; ++n) {
-        for (int period = 0; period <= n; ++period) {
-            if (period > 1 && n % period != 0) continue;
-            std::vector<int> seen(n, 0);
-            for (int y = 0; y < n; ++y) {
-                const int b = cu_order_block(y, period);
-                CHECK(b >= 0 && b < n, "n %d period %d: y %d -> %d", n, period, y, b);
-                if (b >= 0 && b < n) ++seen[b];
+    // a permutation of [0, n) for every run length and count of runs inside n
+    for (int n = 1; n <= 200; n += 7) {
+        for (int run = 0; run <= n; run += 3) {
+            for (int runs = 0; run > 0 && runs * run <= n; ++runs) {
+                std::vector<int> seen(n, 0);
+                for (int i = 0; i < n; ++i) {
+                    const int r = cu_order_wg(i, run, runs);
+                    CHECK(r >= 0 && r < n, "n %d run %d runs %d: %d -> %d", n, run, runs, i, r);
+                    if (r >= 0 && r < n) ++seen[r];
+                }
+                for (int r = 0; r < n; ++r) CHECK(seen[r] == 1, "n %d run %d runs %d: rank %d seen %d times", n, run, runs, r, seen[r]);
             }
-            for (int b = 0; b < n; ++b) CHECK(seen[b] == 1, "n %d period %d: block %d seen %d times", n, period, b, seen[b]);
         }
     }
-    // per-CU stages under the dispatcher model, as cu_balance_period applies
-    // it: bh heads a multiple of 8 dividing 256, period 256 / bh, blocks a
-    // multiple of the period; block q's stages q + 1 (causal, heaviest first)
-    for (int bh : {8, 16, 32, 64, 128}) {
-        const int period = 256 / bh;
-        for (int nqb = 2 * period; nqb <= 8 * period; nqb += period) {
-            std::vector<long long> cu(256, 0);
-            for (int y = 0; y < nqb; ++y) {
-                for (int h = 0; h < bh; ++h) {
-                    const int i = y * bh + h;            // linear work-group index
-                    const int xcd = i % 8, slot = (i / 8) % 32;  // dispatch model
-                    const int q = nqb - 1 - cu_order_block(y, period);
-                    cu[xcd * 32 + slot] += q + 1;
+    // per-CU stages of the resident work-groups under the dispatcher model:
+    // bh heads, nqb blocks, occ work-groups per CU (the kernel's occupancy);
+    // the launcher balances the whole runs of 256 among the resident ones
+    constexpr int C = 256;
+    for (int bh : {8, 14, 28, 32, 48, 64, 96, 128}) {
+        for (int nqb : {16, 24, 32, 48, 64}) {
+            for (int occ : {2, 3, 4}) {
+                const long long total = (long long)bh * nqb, resident = std::min<long long>(total, C * occ);
+                const int runs = (int)(resident / C);
+                if (runs < 2) continue;
+                std::vector<long long> cu(C, 0), plain(C, 0);
+                for (int i = 0; i < runs * C; ++i) {
+                    const int xcd = i % 8, slot = (i / 8) % (C / 8);  // dispatch model
+                    const int r = cu_order_wg(i, C, runs);
+                    cu[xcd * (C / 8) + slot] += nqb - r / bh;    // stages of the rank's block (heaviest first)
+                    plain[xcd * (C / 8) + slot] += nqb - i / bh;
                 }
+                const auto spread = [](const std::vector<long long> &v) {
+                    long long lo = v[0], hi = v[0];
+                    for (long long x : v) {
+                        lo = x < lo ? x : lo;
+                        hi = x > hi ? x : hi;
+                    }
+                    return hi - lo;
+                };
+                const long long bound = runs / 2 + (runs % 2 ? (C - 1) / bh + 1 : 0);
+                CHECK(spread(cu) <= bound, "bh %d nqb %d occ %d: per-CU stages spread %lld (bound %lld, plain order %lld)",
+                      bh, nqb, occ, spread(cu), bound, spread(plain));
+                CHECK(spread(cu) <= spread(plain), "bh %d nqb %d occ %d: balanced %lld against plain %lld", bh, nqb, occ,
+                      spread(cu), spread(plain));
             }
-            long long lo = cu[0], hi = cu[0];
-            for (int c = 1; c < 256; ++c) {
-                lo = cu[c] < lo ? cu[c] : lo;
-                hi = cu[c] > hi ? cu[c] : hi;
-            }
-            const int runs = nqb / period;
-            const long long bound = runs % 2 == 0 ? 0 : period - 1;
-            CHECK(hi - lo <= bound, "bh %d nqb %d: stages per CU from %lld to %lld (bound %lld)", bh, nqb, lo, hi,
-                  bound);
         }
     }
 }
