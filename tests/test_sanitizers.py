@@ -45,7 +45,7 @@ def test_abi_host_asan_ubsan():
 
 @pytest.mark.skipif(not os.path.exists("/opt/rocm/bin/hipcc"), reason="hipcc is not installed")
 def test_work_orders_asan_ubsan():
-    """The block order of resident causal grids (cu_order_block) and the GQA
+    """The work order of resident causal grids (cu_order_wg) and the GQA
     split's share indices (dkv_first_work against dkv_work), host side."""
     _run(["make", "-s", "-j8", "-C", os.path.join(ROOT, "tests", "sanitize")])
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=1", UBSAN_OPTIONS="print_stacktrace=1")
