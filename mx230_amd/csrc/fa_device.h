@@ -99,15 +99,22 @@ struct Params {
 // launch runs its work heaviest first, so CU c's first work-groups take ranks
 // c, c + C, c + 2C, ..., whose stages all fall with c. Reversing every other
 // run of C ranks among the resident ones gives each CU one heavy and one light
-// rank per pair of runs: the same stages for every CU when the runs pair up
-// (the work falling steadily with the rank), an odd last run's spread
-// otherwise. Work-groups past `runs` runs (dispatched as slots free up) keep
+// rank per pair of runs; with an odd count of runs (C even) the last three go
+// as a triple, position c of them taking c, C - 1 - 2c (c < C/2) or
+// 2C - 2 - 2c, and (c + C/2) mod C, which sum to 3(C - 1)/2 rounded. So every
+// CU gets the same stages up to rounding (the work falling steadily with the
+// rank). Work-groups past `runs` runs (dispatched as slots free up) keep
 // their order. run <= 1 or runs < 2: i itself.
 __host__ __device__ inline int cu_order_wg(int i, int run, int runs) {
     if (run <= 1 || runs < 2) return i;
-    const int k = i / run;
-    if (k >= runs || (k & 1) == 0) return i;
-    return k * run + run - 1 - (i - k * run);
+    const int k = i / run, c = i - k * run;
+    if (k >= runs) return i;
+    const int t = (runs & 1) && (run & 1) == 0 ? runs - 3 : runs;  // runs [t, runs): the triple
+    if (k < t) return (k & 1) ? k * run + run - 1 - c : i;
+    const int half = run / 2;
+    if (k == t) return i;
+    if (k == t + 1) return k * run + (c < half ? run - 1 - 2 * c : 2 * run - 2 - 2 * c);
+    return k * run + (c + half) % run;
 }
 
 // Delta flags of the one-launch backward: kFlagSlots slots (one per launch,

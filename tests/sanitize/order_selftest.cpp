@@ -6,8 +6,8 @@
 //    dispatcher model (work-group i on XCD i mod 8, then round robin over
 //    that XCD's CUs, so i and i + 256 share a CU), the resident work-groups of
 //    a causal launch (heaviest first, heads fastest) give every CU the same
-//    stages up to one per pair of runs of 256, plus one run's spread when
-//    their count is odd.
+//    stages up to one per pair of runs of 256 and two for a triple (an odd
+//    count of runs), the rounding of each block's stages to its rank.
 //  * dkv_first_work: share 0 of each (batch, KV head, key block) is the
 //    dkv_work index whose work is that block's share 0, and the block's shares
 //    are the indices after it, for split and unsplit, causal and not.
@@ -71,7 +71,7 @@ static void check_cu_order() {
                     }
                     return hi - lo;
                 };
-                const long long bound = runs / 2 + (runs % 2 ? (C - 1) / bh + 1 : 0);
+                const long long bound = runs % 2 ? (runs - 3) / 2 + 2 : runs / 2;
                 CHECK(spread(cu) <= bound, "bh %d nqb %d occ %d: per-CU stages spread %lld (bound %lld, plain order %lld)",
                       bh, nqb, occ, spread(cu), bound, spread(plain));
                 CHECK(spread(cu) <= spread(plain), "bh %d nqb %d occ %d: balanced %lld against plain %lld", bh, nqb, occ,
