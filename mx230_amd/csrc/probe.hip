@@ -157,7 +157,7 @@ constexpr int kMixSlots = 32;
 __device__ __forceinline__ constexpr int mix_first(int count, int slot) {
     return (slot * count + kMixSlots - 1) / kMixSlots;  // first j with 32 j / count >= slot
 }
-__device__ __forceinline__ constexpr int mix_reads(int b, int r, int s0, int s1) {
+[[maybe_unused]] __device__ __forceinline__ constexpr int mix_reads(int b, int r, int s0, int s1) {
     return mix_first(b, s1) - mix_first(b, s0) + mix_first(r, s1) - mix_first(r, s0);
 }
 
