@@ -133,7 +133,7 @@ def naive_table():
         gen.manual_seed(n)
         q, k, v, do = (torch.randn((1, 1, n, 64), generator=gen, device=dev) for _ in range(4))
         o = torch.empty_like(q)
-        flash = median_ms(lambda: mx.run_flash(q, k, v, o, False))
+        flash = median_ms(mx.prepare(mx.run_flash, q, k, v, o, False))
         naive = None
         if n <= 16384:
             s = torch.empty(mx.naive_scratch_bytes(q, k, False) // 4, device=dev)
@@ -150,7 +150,7 @@ def naive_table():
             mx.run_flash_lse(q, k, v, o, lse, True)
             mx.run_preprocess(do, o, delta)
             dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-            flash = median_ms(lambda: mx.run_bwd_flash(q, k, v, do, lse, delta, dq, dk, dv, True))
+            flash = median_ms(mx.prepare(mx.run_bwd_flash, q, k, v, do, lse, delta, dq, dk, dv, True))
 
             def naive_bwd():
                 dq.zero_()
@@ -338,10 +338,10 @@ def config_table(cpu=False):
         lse = torch.empty((B, H, N), device=dev)
         delta = torch.empty_like(lse)
         dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-        fwd = median_ms(lambda: mx.run_flash_lse(q, k, v, o, lse, causal))
+        fwd = median_ms(mx.prepare(mx.run_flash_lse, q, k, v, o, lse, causal))
         nws = mx.bwd_workspace_bytes(q, k, causal)
         ws = torch.empty(nws, dtype=torch.uint8, device=dev) if nws else None
-        bwd = median_ms(lambda: mx.run_bwd_ws(q, k, v, o, do, lse, delta, dq, dk, dv, ws, causal))
+        bwd = median_ms(mx.prepare(mx.run_bwd_ws, q, k, v, o, do, lse, delta, dq, dk, dv, ws, causal))
         peak = PEAK_TFLOPS[dtype]
         ftf = mx.fwd_flops(B, H, N, d, causal) / (fwd * 1e-3) / 1e12
         btf = mx.bwd_flops(B, H, N, d, causal) / (bwd * 1e-3) / 1e12
@@ -443,10 +443,10 @@ def mix_probe(a):
     delta = torch.empty_like(lse)
     mx.run_flash_lse(q, k, v, o, lse, causal)
     unit = N * N * d * B * H * (0.5 if causal else 1.0)  # x k N^2 d flops per (b, h)
-    kern = {"fwd": (4, lambda: mx.run_flash_lse(q, k, v, o, lse, causal)),
-            "dq": (6, lambda: mx.run_bwd_dq_delta(q, k, v, o, do, lse, delta, dq, causal)),
-            "dkv": (8, lambda: mx.run_bwd_dkv(q, k, v, do, lse, delta, dk, dv, causal)),
-            "bwd_one_launch": (14, lambda: mx.run_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, causal))}
+    kern = {"fwd": (4, mx.prepare(mx.run_flash_lse, q, k, v, o, lse, causal)),
+            "dq": (6, mx.prepare(mx.run_bwd_dq_delta, q, k, v, o, do, lse, delta, dq, causal)),
+            "dkv": (8, mx.prepare(mx.run_bwd_dkv, q, k, v, do, lse, delta, dk, dv, causal)),
+            "bwd_one_launch": (14, mx.prepare(mx.run_bwd, q, k, v, o, do, lse, delta, dq, dk, dv, causal))}
     kernels = {}
     for name, (mult, fn) in kern.items():
         ms = median_ms(fn)
@@ -715,14 +715,14 @@ def main():
     # --separate-delta the reference-shaped sequence preprocess, dQ, dK/dV
     one = not a.separate_delta and mx.bwd_one_launch(q, k, causal)
     if a.separate_delta:
-        launches = [("preprocess", lambda: mx.run_preprocess(do, o, delta)),
-                    ("dq", lambda: mx.run_bwd_dq(q, k, v, do, lse, delta, dq, causal)),
-                    ("dkv", lambda: mx.run_bwd_dkv(q, k, v, do, lse, delta, dk, dv, causal))]
+        launches = [("preprocess", mx.prepare(mx.run_preprocess, do, o, delta)),
+                    ("dq", mx.prepare(mx.run_bwd_dq, q, k, v, do, lse, delta, dq, causal)),
+                    ("dkv", mx.prepare(mx.run_bwd_dkv, q, k, v, do, lse, delta, dk, dv, causal))]
     elif one:
-        launches = [("bwd", lambda: mx.run_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, causal))]
+        launches = [("bwd", mx.prepare(mx.run_bwd, q, k, v, o, do, lse, delta, dq, dk, dv, causal))]
     else:
-        launches = [("dq", lambda: mx.run_bwd_dq_delta(q, k, v, o, do, lse, delta, dq, causal)),
-                    ("dkv", lambda: mx.run_bwd_dkv(q, k, v, do, lse, delta, dk, dv, causal))]
+        launches = [("dq", mx.prepare(mx.run_bwd_dq_delta, q, k, v, o, do, lse, delta, dq, causal)),
+                    ("dkv", mx.prepare(mx.run_bwd_dkv, q, k, v, do, lse, delta, dk, dv, causal))]
 
     def step(seq, evs=None):
         # evs: events recorded on the launch stream before each launch and after the last
@@ -786,18 +786,19 @@ def main():
     # the two passes on their own (two launches), for the breakdown
     passes = None
     if one:
-        passes = per_launch_ms([("dq", lambda: mx.run_bwd_dq_delta(q, k, v, o, do, lse, delta, dq, causal)),
-                                ("dkv", lambda: mx.run_bwd_dkv(q, k, v, do, lse, delta, dk, dv, causal))])
+        passes = per_launch_ms([("dq", mx.prepare(mx.run_bwd_dq_delta, q, k, v, o, do, lse, delta, dq, causal)),
+                                ("dkv", mx.prepare(mx.run_bwd_dkv, q, k, v, do, lse, delta, dk, dv, causal))])
 
     # the forward: K launches back to back after a few warm-up ones, one event
     # pair around them (O and LSE are rewritten with the same values)
+    fwd_call = mx.prepare(mx.run_flash_lse, q, k, v, o, lse, causal)
     for _ in range(5):
-        mx.run_flash_lse(q, k, v, o, lse, causal)
+        fwd_call()
     f0, f1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     f0.record(stream)
     for _ in range(a.steps):
-        mx.run_flash_lse(q, k, v, o, lse, causal)
+        fwd_call()
     f1.record(stream)
     torch.cuda.synchronize()
     fwd_avg = f0.elapsed_time(f1) / a.steps

@@ -179,6 +179,10 @@ def _check(func: str, rc: int):
         raise MxfaError(func, rc, load_library().mxfa_strerror(rc).decode())
 
 
+def _invoke(func: str, args):
+    _check(func, getattr(load_library(), func)(*args))
+
+
 @dataclass(frozen=True)
 class Shape:
     B: int
@@ -265,32 +269,42 @@ def _vec_ptr(t, name, sh: Shape):
 
 # ------------------------------------------- reference-shaped entry points --
 
-def run_flash(q, k, v, o, causal: bool, scale: float = 0.0, stream=None):
-    """Forward, O only (main.rs:68-88)."""
+def _call_flash(q, k, v, o, causal: bool, scale: float = 0.0, stream=None):
     sh = shape_of(q, k, causal, scale)
     dt, qs, ks = _io(sh)
     args = (_expect(q, "q", qs, dt), _expect(k, "k", ks, dt), _expect(v, "v", ks, dt),
             _expect(o, "o", qs, dt))
-    _check("mxfa_run_flash", load_library().mxfa_run_flash(ctypes.byref(sh.c()), *args, _stream(stream)))
+    return "mxfa_run_flash", (ctypes.byref(sh.c()), *args, _stream(stream))
 
 
-def run_flash_lse(q, k, v, o, lse, causal: bool, scale: float = 0.0, stream=None):
-    """Forward with the log-sum-exp the backward needs (main.rs:102-123)."""
+def run_flash(q, k, v, o, causal: bool, scale: float = 0.0, stream=None):
+    """Forward, O only (main.rs:68-88)."""
+    _invoke(*_call_flash(q, k, v, o, causal, scale, stream))
+
+
+def _call_flash_lse(q, k, v, o, lse, causal: bool, scale: float = 0.0, stream=None):
     sh = shape_of(q, k, causal, scale)
     dt, qs, ks = _io(sh)
     args = (_expect(q, "q", qs, dt), _expect(k, "k", ks, dt), _expect(v, "v", ks, dt),
             _expect(o, "o", qs, dt), _vec_ptr(lse, "lse", sh))
-    _check("mxfa_run_flash_lse",
-           load_library().mxfa_run_flash_lse(ctypes.byref(sh.c()), *args, _stream(stream)))
+    return "mxfa_run_flash_lse", (ctypes.byref(sh.c()), *args, _stream(stream))
+
+
+def run_flash_lse(q, k, v, o, lse, causal: bool, scale: float = 0.0, stream=None):
+    """Forward with the log-sum-exp the backward needs (main.rs:102-123)."""
+    _invoke(*_call_flash_lse(q, k, v, o, lse, causal, scale, stream))
+
+
+def _call_preprocess(do, o, delta, stream=None):
+    sh = shape_of(do, do, False)
+    dt, qs, _ = _io(sh)
+    args = (_expect(do, "do", qs, dt), _expect(o, "o", qs, dt), _vec_ptr(delta, "delta", sh))
+    return "mxfa_run_preprocess", (ctypes.byref(sh.c()), *args, _stream(stream))
 
 
 def run_preprocess(do, o, delta, stream=None):
     """Delta = rowsum(dO * O) (main.rs:126-143)."""
-    sh = shape_of(do, do, False)
-    dt, qs, _ = _io(sh)
-    args = (_expect(do, "do", qs, dt), _expect(o, "o", qs, dt), _vec_ptr(delta, "delta", sh))
-    _check("mxfa_run_preprocess",
-           load_library().mxfa_run_preprocess(ctypes.byref(sh.c()), *args, _stream(stream)))
+    _invoke(*_call_preprocess(do, o, delta, stream))
 
 
 def _bwd_args(q, k, v, do, lse, delta, causal, scale):
@@ -301,14 +315,27 @@ def _bwd_args(q, k, v, do, lse, delta, causal, scale):
     return sh, dt, qs, ks, args
 
 
+def _call_bwd_flash(q, k, v, do, lse, delta, dq, dk, dv, causal: bool, scale: float = 0.0,
+                  stream=None):
+    sh, dt, qs, ks, args = _bwd_args(q, k, v, do, lse, delta, causal, scale)
+    args += [_expect(dq, "dq", qs, dt), _expect(dk, "dk", ks, dt), _expect(dv, "dv", ks, dt)]
+    return "mxfa_run_bwd_flash", (ctypes.byref(sh.c()), *args, _stream(stream))
+
+
 def run_bwd_flash(q, k, v, do, lse, delta, dq, dk, dv, causal: bool, scale: float = 0.0,
                   stream=None):
     """Tiled atomic-free backward: dK/dV pass then dQ pass (main.rs:179-210).
     Outputs are overwritten."""
-    sh, dt, qs, ks, args = _bwd_args(q, k, v, do, lse, delta, causal, scale)
-    args += [_expect(dq, "dq", qs, dt), _expect(dk, "dk", ks, dt), _expect(dv, "dv", ks, dt)]
-    _check("mxfa_run_bwd_flash",
-           load_library().mxfa_run_bwd_flash(ctypes.byref(sh.c()), *args, _stream(stream)))
+    _invoke(*_call_bwd_flash(q, k, v, do, lse, delta, dq, dk, dv, causal, scale, stream))
+
+
+def _call_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, causal: bool, scale: float = 0.0, stream=None):
+    sh = shape_of(q, k, causal, scale)
+    dt, qs, ks = _io(sh)
+    args = [_expect(q, "q", qs, dt), _expect(k, "k", ks, dt), _expect(v, "v", ks, dt), _expect(o, "o", qs, dt),
+            _expect(do, "do", qs, dt), _vec_ptr(lse, "lse", sh), _vec_ptr(delta, "delta", sh),
+            _expect(dq, "dq", qs, dt), _expect(dk, "dk", ks, dt), _expect(dv, "dv", ks, dt)]
+    return "mxfa_run_bwd", (ctypes.byref(sh.c()), *args, _stream(stream))
 
 
 def run_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, causal: bool, scale: float = 0.0, stream=None):
@@ -316,12 +343,7 @@ def run_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, causal: bool, scale: float =
     Delta = rowsum(dO * O) itself and writes it to ``delta`` for the dK/dV
     work (run_preprocess + run_bwd_flash with the preprocess launch folded in);
     one launch for bf16 (bwd_one_launch), else two. Outputs are overwritten."""
-    sh = shape_of(q, k, causal, scale)
-    dt, qs, ks = _io(sh)
-    args = [_expect(q, "q", qs, dt), _expect(k, "k", ks, dt), _expect(v, "v", ks, dt), _expect(o, "o", qs, dt),
-            _expect(do, "do", qs, dt), _vec_ptr(lse, "lse", sh), _vec_ptr(delta, "delta", sh),
-            _expect(dq, "dq", qs, dt), _expect(dk, "dk", ks, dt), _expect(dv, "dv", ks, dt)]
-    _check("mxfa_run_bwd", load_library().mxfa_run_bwd(ctypes.byref(sh.c()), *args, _stream(stream)))
+    _invoke(*_call_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, causal, scale, stream))
 
 
 def bwd_one_launch(q, k, causal: bool) -> bool:
@@ -389,75 +411,141 @@ def _ws_args(workspace):
     return [ctypes.c_void_p(workspace.data_ptr()), workspace.numel() * workspace.element_size()]
 
 
-def run_bwd_ws(q, k, v, o, do, lse, delta, dq, dk, dv, workspace, causal: bool, scale: float = 0.0,
+def _call_bwd_ws(q, k, v, o, do, lse, delta, dq, dk, dv, workspace, causal: bool, scale: float = 0.0,
                stream=None):
-    """run_bwd with a workspace (a device tensor of at least
-    bwd_workspace_bytes(q, k, causal) bytes, or None) for the split dK/dV pass
-    of GQA shapes (mxfa_run_bwd_ws)."""
     sh = shape_of(q, k, causal, scale)
     dt, qs, ks = _io(sh)
     args = [_expect(q, "q", qs, dt), _expect(k, "k", ks, dt), _expect(v, "v", ks, dt), _expect(o, "o", qs, dt),
             _expect(do, "do", qs, dt), _vec_ptr(lse, "lse", sh), _vec_ptr(delta, "delta", sh),
             _expect(dq, "dq", qs, dt), _expect(dk, "dk", ks, dt), _expect(dv, "dv", ks, dt)]
     args += _ws_args(workspace)
-    _check("mxfa_run_bwd_ws", load_library().mxfa_run_bwd_ws(ctypes.byref(sh.c()), *args, _stream(stream)))
+    return "mxfa_run_bwd_ws", (ctypes.byref(sh.c()), *args, _stream(stream))
+
+
+def run_bwd_ws(q, k, v, o, do, lse, delta, dq, dk, dv, workspace, causal: bool, scale: float = 0.0,
+               stream=None):
+    """run_bwd with a workspace (a device tensor of at least
+    bwd_workspace_bytes(q, k, causal) bytes, or None) for the split dK/dV pass
+    of GQA shapes (mxfa_run_bwd_ws)."""
+    _invoke(*_call_bwd_ws(q, k, v, o, do, lse, delta, dq, dk, dv, workspace, causal, scale, stream))
+
+
+def _call_bwd_noalloc(q, k, v, o, do, lse, delta, dq, dk, dv, causal: bool, scale: float = 0.0, stream=None):
+    sh = shape_of(q, k, causal, scale)
+    dt, qs, ks = _io(sh)
+    args = [_expect(q, "q", qs, dt), _expect(k, "k", ks, dt), _expect(v, "v", ks, dt), _expect(o, "o", qs, dt),
+            _expect(do, "do", qs, dt), _vec_ptr(lse, "lse", sh), _vec_ptr(delta, "delta", sh),
+            _expect(dq, "dq", qs, dt), _expect(dk, "dk", ks, dt), _expect(dv, "dv", ks, dt)]
+    return "mxfa_run_bwd_noalloc", (ctypes.byref(sh.c()), *args, _stream(stream))
 
 
 def run_bwd_noalloc(q, k, v, o, do, lse, delta, dq, dk, dv, causal: bool, scale: float = 0.0, stream=None):
     """run_bwd_ws with the library's static scratch in place of a workspace
     (mxfa_run_bwd_noalloc): allocates nothing; calls overlapping on one device
     race on the scratch."""
-    sh = shape_of(q, k, causal, scale)
-    dt, qs, ks = _io(sh)
-    args = [_expect(q, "q", qs, dt), _expect(k, "k", ks, dt), _expect(v, "v", ks, dt), _expect(o, "o", qs, dt),
-            _expect(do, "do", qs, dt), _vec_ptr(lse, "lse", sh), _vec_ptr(delta, "delta", sh),
-            _expect(dq, "dq", qs, dt), _expect(dk, "dk", ks, dt), _expect(dv, "dv", ks, dt)]
-    _check("mxfa_run_bwd_noalloc", load_library().mxfa_run_bwd_noalloc(ctypes.byref(sh.c()), *args,
-                                                                        _stream(stream)))
+    _invoke(*_call_bwd_noalloc(q, k, v, o, do, lse, delta, dq, dk, dv, causal, scale, stream))
 
 
-def run_bwd_dq_delta(q, k, v, o, do, lse, delta, dq, causal: bool, scale: float = 0.0, stream=None):
-    """dQ pass that computes Delta from O itself and writes it to ``delta``."""
+def _call_bwd_dq_delta(q, k, v, o, do, lse, delta, dq, causal: bool, scale: float = 0.0, stream=None):
     sh = shape_of(q, k, causal, scale)
     dt, qs, ks = _io(sh)
     args = [_expect(q, "q", qs, dt), _expect(k, "k", ks, dt), _expect(v, "v", ks, dt), _expect(o, "o", qs, dt),
             _expect(do, "do", qs, dt), _vec_ptr(lse, "lse", sh), _vec_ptr(delta, "delta", sh),
             _expect(dq, "dq", qs, dt)]
-    _check("mxfa_run_bwd_dq_delta", load_library().mxfa_run_bwd_dq_delta(ctypes.byref(sh.c()), *args,
-                                                                          _stream(stream)))
+    return "mxfa_run_bwd_dq_delta", (ctypes.byref(sh.c()), *args, _stream(stream))
+
+
+def run_bwd_dq_delta(q, k, v, o, do, lse, delta, dq, causal: bool, scale: float = 0.0, stream=None):
+    """dQ pass that computes Delta from O itself and writes it to ``delta``."""
+    _invoke(*_call_bwd_dq_delta(q, k, v, o, do, lse, delta, dq, causal, scale, stream))
+
+
+def _call_bwd_dq(q, k, v, do, lse, delta, dq, causal: bool, scale: float = 0.0, stream=None):
+    sh, dt, qs, ks, args = _bwd_args(q, k, v, do, lse, delta, causal, scale)
+    args += [_expect(dq, "dq", qs, dt)]
+    return "mxfa_run_bwd_dq", (ctypes.byref(sh.c()), *args, _stream(stream))
 
 
 def run_bwd_dq(q, k, v, do, lse, delta, dq, causal: bool, scale: float = 0.0, stream=None):
     """dQ pass alone (attention_bwd.cu:96-158)."""
+    _invoke(*_call_bwd_dq(q, k, v, do, lse, delta, dq, causal, scale, stream))
+
+
+def _call_bwd_dkv(q, k, v, do, lse, delta, dk, dv, causal: bool, scale: float = 0.0, stream=None):
     sh, dt, qs, ks, args = _bwd_args(q, k, v, do, lse, delta, causal, scale)
-    args += [_expect(dq, "dq", qs, dt)]
-    _check("mxfa_run_bwd_dq", load_library().mxfa_run_bwd_dq(ctypes.byref(sh.c()), *args, _stream(stream)))
+    args += [_expect(dk, "dk", ks, dt), _expect(dv, "dv", ks, dt)]
+    return "mxfa_run_bwd_dkv", (ctypes.byref(sh.c()), *args, _stream(stream))
 
 
 def run_bwd_dkv(q, k, v, do, lse, delta, dk, dv, causal: bool, scale: float = 0.0, stream=None):
     """dK/dV pass alone (attention_bwd.cu:165-243)."""
+    _invoke(*_call_bwd_dkv(q, k, v, do, lse, delta, dk, dv, causal, scale, stream))
+
+
+def _call_bwd_dkv_ws(q, k, v, do, lse, delta, dk, dv, workspace, causal: bool, scale: float = 0.0,
+                   stream=None):
     sh, dt, qs, ks, args = _bwd_args(q, k, v, do, lse, delta, causal, scale)
-    args += [_expect(dk, "dk", ks, dt), _expect(dv, "dv", ks, dt)]
-    _check("mxfa_run_bwd_dkv",
-           load_library().mxfa_run_bwd_dkv(ctypes.byref(sh.c()), *args, _stream(stream)))
+    args += [_expect(dk, "dk", ks, dt), _expect(dv, "dv", ks, dt)] + _ws_args(workspace)
+    return "mxfa_run_bwd_dkv_ws", (ctypes.byref(sh.c()), *args, _stream(stream))
 
 
 def run_bwd_dkv_ws(q, k, v, do, lse, delta, dk, dv, workspace, causal: bool, scale: float = 0.0,
                    stream=None):
     """dK/dV pass with a workspace for the split GQA form (mxfa_run_bwd_dkv_ws)."""
+    _invoke(*_call_bwd_dkv_ws(q, k, v, do, lse, delta, dk, dv, workspace, causal, scale, stream))
+
+
+def _call_bwd_naive(q, k, v, do, lse, delta, dq, dk, dv, causal: bool, scale: float = 0.0,
+                  stream=None):
     sh, dt, qs, ks, args = _bwd_args(q, k, v, do, lse, delta, causal, scale)
-    args += [_expect(dk, "dk", ks, dt), _expect(dv, "dv", ks, dt)] + _ws_args(workspace)
-    _check("mxfa_run_bwd_dkv_ws",
-           load_library().mxfa_run_bwd_dkv_ws(ctypes.byref(sh.c()), *args, _stream(stream)))
+    args += [_expect(dq, "dq", qs, dt), _expect(dk, "dk", ks, dt), _expect(dv, "dv", ks, dt)]
+    return "mxfa_run_bwd_naive", (ctypes.byref(sh.c()), *args, _stream(stream))
 
 
 def run_bwd_naive(q, k, v, do, lse, delta, dq, dk, dv, causal: bool, scale: float = 0.0,
                   stream=None):
     """Naive atomic backward baseline, fp32; outputs must be zeroed (main.rs:147-173)."""
-    sh, dt, qs, ks, args = _bwd_args(q, k, v, do, lse, delta, causal, scale)
-    args += [_expect(dq, "dq", qs, dt), _expect(dk, "dk", ks, dt), _expect(dv, "dv", ks, dt)]
-    _check("mxfa_run_bwd_naive",
-           load_library().mxfa_run_bwd_naive(ctypes.byref(sh.c()), *args, _stream(stream)))
+    _invoke(*_call_bwd_naive(q, k, v, do, lse, delta, dq, dk, dv, causal, scale, stream))
+
+
+class Prepared:
+    """One entry point with its arguments checked and marshalled once
+    (prepare()): calling it enqueues the same launch again (the same tensors,
+    shape, scale and stream) for the cost of one foreign call. It keeps the
+    tensors referenced; they must keep their storage (no resize or
+    reallocation) while it is in use, as their device addresses are fixed
+    in it. The library validates the call again each time, as for any call."""
+    __slots__ = ("func", "_fn", "_args", "_keep")
+
+    def __init__(self, func: str, args, keep):
+        self.func = func
+        self._fn = getattr(load_library(), func)
+        self._args = tuple(args)
+        self._keep = keep
+
+    def __call__(self):
+        rc = self._fn(*self._args)
+        if rc != 0:
+            _check(self.func, rc)
+
+
+def prepare(fn, *args, **kwargs) -> Prepared:
+    """fn(*args, **kwargs) as a Prepared call, for one of run_flash,
+    run_flash_lse, run_preprocess, run_bwd, run_bwd_ws, run_bwd_noalloc,
+    run_bwd_flash, run_bwd_dq, run_bwd_dq_delta, run_bwd_dkv, run_bwd_dkv_ws
+    and run_bwd_naive: the argument checks of fn run here, once (and raise
+    here), so a loop of calls pays only the launch."""
+    marshal = _MARSHAL.get(fn)
+    if marshal is None:
+        raise ValueError(f"prepare: {getattr(fn, '__name__', fn)!r} is not a preparable entry point")
+    func, cargs = marshal(*args, **kwargs)
+    return Prepared(func, cargs, (args, kwargs))
+
+
+_MARSHAL = {run_flash: _call_flash, run_flash_lse: _call_flash_lse, run_preprocess: _call_preprocess,
+            run_bwd: _call_bwd, run_bwd_ws: _call_bwd_ws, run_bwd_noalloc: _call_bwd_noalloc,
+            run_bwd_flash: _call_bwd_flash, run_bwd_dq: _call_bwd_dq, run_bwd_dq_delta: _call_bwd_dq_delta,
+            run_bwd_dkv: _call_bwd_dkv, run_bwd_dkv_ws: _call_bwd_dkv_ws, run_bwd_naive: _call_bwd_naive}
 
 
 def naive_scratch_bytes(q, k, causal: bool) -> int:

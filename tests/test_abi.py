@@ -433,3 +433,20 @@ def test_integration_rust_block_binds_every_entry_point():
     bound = set(re.findall(r"pub fn (mxfa_\w+)\(", block))
     assert names, "no declarations parsed"
     assert names == bound, (sorted(names - bound), sorted(bound - names))
+
+
+def test_prepare_checks_arguments_once_and_rejects_other_functions():
+    """mx.prepare runs the wrapper's argument checks at preparation (a host
+    tensor is refused there, before any launch) and covers exactly the
+    launch wrappers it names."""
+    import torch
+    q = torch.zeros(1, 2, 16, 64, dtype=torch.bfloat16)
+    lse = torch.zeros(1, 2, 16)
+    with pytest.raises(ValueError, match="device tensor"):
+        mx.prepare(mx.run_flash_lse, q, q, q, q, lse, True)
+    with pytest.raises(ValueError, match="not a preparable"):
+        mx.prepare(mx.time_median_ms, lambda: None)
+    names = sorted(f.__name__ for f in mx._MARSHAL)
+    assert names == sorted(["run_flash", "run_flash_lse", "run_preprocess", "run_bwd", "run_bwd_ws",
+                            "run_bwd_noalloc", "run_bwd_flash", "run_bwd_dq", "run_bwd_dq_delta",
+                            "run_bwd_dkv", "run_bwd_dkv_ws", "run_bwd_naive"])

@@ -259,6 +259,37 @@ def test_runs_on_the_callers_stream():
     assert not bad, errs
 
 
+def test_prepared_calls_match_direct_calls():
+    """mx.prepare: the forward and the backward (GQA, through its workspace)
+    as prepared calls, each run twice, give the direct calls' bits."""
+    import torch
+    import mx230_amd as mx
+    q, k, v, do = make_inputs(1, 8, 2, 300, 64, bf16=True, seeds=(41, 42, 43, 44))
+    tq, tk, tv, tdo = (to_dev(x, True) for x in (q, k, v, do))
+    B, H, N, d = q.shape
+    outs = []
+    for prepared in (False, True):
+        o, lse = torch.empty_like(tq), torch.empty((B, H, N), device="cuda")
+        delta = torch.empty_like(lse)
+        dq, dk, dv = torch.empty_like(tq), torch.empty_like(tk), torch.empty_like(tv)
+        nws = mx.bwd_workspace_bytes(tq, tk, True)
+        ws = torch.empty(nws, dtype=torch.uint8, device="cuda") if nws else None
+        fwd_args = (tq, tk, tv, o, lse, True)
+        bwd_args = (tq, tk, tv, o, tdo, lse, delta, dq, dk, dv, ws, True)
+        if prepared:
+            fwd, bwd = mx.prepare(mx.run_flash_lse, *fwd_args), mx.prepare(mx.run_bwd_ws, *bwd_args)
+            for _ in range(2):
+                fwd()
+                bwd()
+        else:
+            mx.run_flash_lse(*fwd_args)
+            mx.run_bwd_ws(*bwd_args)
+        torch.cuda.synchronize()
+        outs.append((o, lse, dq, dk, dv))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
 def test_code_object_load_errors_and_reload(tmp_path):
     """The kernels are a code object loaded per device: with it unloaded and
     pointed at a missing or malformed file, launches return
