@@ -230,8 +230,12 @@ int mxfa_bwd_reduce_timeouts(unsigned long long *count);
  * workspace, and they are added in a fixed order (deterministic, atomic-free)
  * by the last work-groups of the one-launch backward, else by a second
  * launch. The size is 2 * planes * B * Hkv * N * d * 4 bytes, planes being
- * the most work-groups any key block takes; 0 when no split helps (always
- * without GQA).
+ * the most work-groups any key block takes, then 8 bytes per work-group of
+ * the split (the flags by which the one-launch backward's adding work-groups
+ * learn that a share's sums are written: each launch writes its own value,
+ * so the workspace needs no clearing); 0 when no split helps (always without
+ * GQA). A call uses its workspace until it completes: calls in flight at the
+ * same time need their own.
  * The reference has no GQA (d = 64, one head, attention_bwd.cu:165-243); this
  * sizes the scratch of its dK/dV pass generalised to GQA groups. */
 size_t mxfa_bwd_workspace_bytes(const mxfa_shape *shape);
@@ -257,8 +261,9 @@ int mxfa_run_bwd_ws(const mxfa_shape *shape, const void *q, const void *k, const
                     void *workspace, size_t workspace_bytes, void *stream);
 
 /* mxfa_run_bwd_ws without a workspace argument and without allocating: the
- * split dK/dV pass keeps its fp32 partial sums in a static device array of the
- * library, mxfa_bwd_noalloc_scratch_bytes() (64 MiB) per device, held from the
+ * split dK/dV pass keeps its fp32 partial sums and share flags in a static
+ * device array of the library, mxfa_bwd_noalloc_scratch_bytes() (65 MiB) per
+ * device, held from the
  * library's set-up on the device (mxfa_init, else this entry point's first
  * call there) until the process ends. Shapes whose mxfa_bwd_workspace_bytes
  * exceed it return MXFA_ERR_SCRATCH before any device work. No hipMalloc,

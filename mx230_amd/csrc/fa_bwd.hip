@@ -26,7 +26,9 @@
 #include <atomic>
 #include <cmath>
 #include <cstdlib>
+#include <chrono>
 #include <cstring>
+#include <random>
 #include <type_traits>
 
 #include "fa_device.h"
@@ -92,22 +94,20 @@ __device__ __forceinline__ void stage_qdo(typename Pol::T *sq, typename Pol::T *
     if (STAGE_DELTA && wave == 1) stage_vec64(sd, p.delta + bh * N + qs, N - qs, lane, p.delta + bh * N + qs);
 }
 
-// Delta and share flags of the one-launch backward (see Params::epoch and
-// Params::red_rows). Zero at load; launch epochs start at 1, so no flag
-// matches before it is published. And, counted since the code object was
-// loaded (read by name, see module.cpp): the stages whose Delta a dK/dV work-
-// group of the one-launch backward computed itself (its wait ran out), and
-// the reduce work-groups whose wait for their shares ran out (outputs NaN).
+// Delta flags of the one-launch backward (see Params::epoch). Zero at load;
+// launch epochs start at 1, so no flag matches before it is published. And,
+// counted since the code object was loaded (read by name, see module.cpp):
+// the stages whose Delta a dK/dV work-group of the one-launch backward
+// computed itself (its wait ran out), and the reduce work-groups whose wait
+// for their shares ran out (outputs NaN).
 #if defined(__HIP_DEVICE_COMPILE__)
 __device__ uint32_t g_delta_flags[kFlagSlots * kMaxFlagBlocks];
-__device__ uint32_t g_share_flags[kFlagSlots * kMaxShareFlags];
 extern "C" __device__ unsigned long long mxfa_delta_fallbacks;
 __device__ unsigned long long mxfa_delta_fallbacks;
 extern "C" __device__ unsigned long long mxfa_reduce_timeouts;
 __device__ unsigned long long mxfa_reduce_timeouts;
 #else
 extern __device__ uint32_t g_delta_flags[kFlagSlots * kMaxFlagBlocks];
-extern __device__ uint32_t g_share_flags[kFlagSlots * kMaxShareFlags];
 extern "C" __device__ unsigned long long mxfa_delta_fallbacks;
 extern "C" __device__ unsigned long long mxfa_reduce_timeouts;
 #endif
@@ -852,13 +852,13 @@ __device__ __forceinline__ void dkv_reduce_rows(const Params &p, int r, uint32_t
     wg_info(3, kb, ns);
     const int tid = threadIdx.x;
     if (tid < 64) {
-        const uint32_t *flags = g_share_flags + (size_t)p.flag_slot * kMaxShareFlags + w0;
+        const unsigned long long *flags = p.share_flags + w0;
         bool ok = true;
         for (int s0 = 0; s0 < ns && ok; s0 += 64) {
             const int s = s0 + tid;
             const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
             for (;;) {
-                const bool ready = s >= ns || load_uc_sync(flags + s) == p.epoch;
+                const bool ready = s >= ns || load2_uc_sync(flags + s) == p.share_nonce;
                 if (__builtin_amdgcn_ballot_w64(!ready) == 0) break;
                 if (__builtin_amdgcn_s_memrealtime() - t0 > (uint64_t)p.red_wait) {
                     ok = false;
@@ -939,7 +939,7 @@ __device__ __forceinline__ void bwd_fused_entry(const Params &p) {
             // acknowledged: then its flag
             wait_stores();
             __syncthreads();
-            if (threadIdx.x == 0) store_wt(g_share_flags + (size_t)p.flag_slot * kMaxShareFlags + w, p.epoch);
+            if (threadIdx.x == 0) store2_wt(p.share_flags + w, p.share_nonce);
         }
     } else {
         dkv_reduce_rows<DkvT, CAUSAL>(p, bid - p.fused_ndq - p.fused_ndkv, &sm.dkv.sF[0]);
@@ -1245,6 +1245,47 @@ int dkv_split(const Params &p, int dtype_bf16, int d, int causal) {
     return q.dkv_split;
 }
 
+// Bytes of the fp32 partial planes of a split (p.dkv_split set): dK's planes,
+// then dV's.
+static size_t dkv_planes_bytes(const Params &p, int d) {
+    return 2 * (size_t)p.dkv_split * p.B * p.Hkv * p.N * d * sizeof(float);
+}
+
+// The workspace of a split dK/dV pass: its planes, then the one-launch
+// backward's share flags (8 bytes per share, dkv_work's order); 0 without a
+// split.
+template <class Tile>
+static size_t dkv_workspace_bytes_t(Params p, bool causal) {
+    dkv_plan_t<Tile>(p, causal);
+    if (p.dkv_split <= 1) return 0;
+    return dkv_planes_bytes(p, Tile::D) + 8 * (size_t)dkv_work_groups<Tile>(p, causal);
+}
+
+size_t dkv_workspace_bytes(const Params &p, int dtype_bf16, int d, int causal) {
+    if (dtype_bf16 && d == 64) return dkv_workspace_bytes_t<DkvB64>(p, causal != 0);
+    if (dtype_bf16 && d == 128) return dkv_workspace_bytes_t<DkvB128>(p, causal != 0);
+    if (!dtype_bf16 && d == 64) return dkv_workspace_bytes_t<DkvF32>(p, causal != 0);
+    return 0;
+}
+
+// A share-flag value for the next launch with an in-launch reduce: distinct for
+// every launch of the process (a counter through a bijective 64-bit mix) and,
+// through a random start, unrelated to any earlier process's values, so a
+// flag left in the workspace by an earlier launch, or whatever the workspace
+// memory held before, equals it only with probability 2^-64.
+static unsigned long long next_share_nonce() {
+    static const unsigned long long base = [] {
+        std::random_device rd;
+        const unsigned long long t = (unsigned long long)std::chrono::steady_clock::now().time_since_epoch().count();
+        return ((unsigned long long)rd() << 32) ^ (unsigned long long)rd() ^ (t * 0x9E3779B97F4A7C15ull);
+    }();
+    static std::atomic<unsigned long long> count{0};
+    unsigned long long x = base + 0x9E3779B97F4A7C15ull * (count.fetch_add(1) + 1);
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;  // splitmix64's finaliser
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
 template <class K>
 static hipError_t launch_fused_k(Params p, int causal, hipStream_t stream) {
     // with a workspace, GQA shapes split each group's query heads as in the
@@ -1266,15 +1307,18 @@ static hipError_t launch_fused_k(Params p, int causal, hipStream_t stream) {
     p.delta_wait = wait_us < 0 ? -1 : (int)std::min(100LL * wait_us, 0x7fffffffLL);
     p.fused_ndq = (int)ndq;
     p.fused_ndkv = (int)ndkv;
-    // a split's reduce runs in the same launch, after the shares, where their
-    // flags fit
+    // a split's reduce runs in the same launch, after the shares, whose flags
+    // follow the planes in the workspace (dkv_workspace_bytes)
     long long nred = 0;
     p.red_rows = 0;
-    if (p.dkv_split > 1 && ndkv <= kMaxShareFlags) {
+    if (p.dkv_split > 1) {
         constexpr int BKV = 4 * K::Dkv::ROWS, RR = 16;  // dkv_reduce_rows' keys per work-group
         nred = (long long)p.B * p.Hkv * ((p.N + BKV - 1) / BKV) * (BKV / RR);
         p.red_rows = RR;
         p.red_wait = (int)std::min(100LL * g_reduce_wait_us.load(), 0x7fffffffLL);  // 100 MHz ticks
+        p.share_flags = reinterpret_cast<unsigned long long *>(reinterpret_cast<char *>(p.dkv_ws) +
+                                                               dkv_planes_bytes(p, K::Dkv::D));
+        p.share_nonce = next_share_nonce();
     }
     if (ndq + ndkv + nred > 0x7fffffffLL) return hipErrorInvalidValue;
     const KernelId id = K::kHasP2 && scale_is_pow2(p.scale) ? K::fused_p2[causal ? 1 : 0] : K::fused[causal ? 1 : 0];

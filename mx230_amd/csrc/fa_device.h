@@ -79,12 +79,15 @@ struct Params {
     int cu_run, cu_runs;
     // One-launch backward: work-groups [fused_ndq, fused_ndq + fused_ndkv)
     // run the dK/dV pass. With a GQA split and red_rows > 0 the shares write
-    // their planes through to memory and then set their flag in slot
-    // flag_slot of g_share_flags (dkv_work's index) to epoch, and the work-
-    // groups after them each add the planes of red_rows keys of one key block
-    // (dkv_reduce_rows) once its shares' flags are set, polling at most
-    // red_wait ticks; red_rows = 0: a reduce launch follows instead.
+    // their planes through to memory and then set their flag, share_flags[w]
+    // (dkv_work's index w; in the launch's workspace, after the planes), to
+    // share_nonce, a 64-bit value no other launch of the process uses; the
+    // work-groups after them each add the planes of red_rows keys of one key
+    // block (dkv_reduce_rows) once its shares' flags hold the nonce, polling
+    // at most red_wait ticks; red_rows = 0: a reduce launch follows instead.
     int fused_ndkv, red_rows, red_wait;
+    unsigned long long *share_flags;
+    unsigned long long share_nonce;
     // A prefill launch (contiguous or paged cache): the tiles are chosen as
     // the paged cache's kernels allow, so both give the same bits.
     int prefill;
@@ -122,9 +125,6 @@ __host__ __device__ inline int cu_order_wg(int i, int run, int runs) {
 // flags) of kMaxFlagBlocks flags, one per (batch, query head, 128-row block).
 constexpr int kFlagSlots = 4;
 constexpr int kMaxFlagBlocks = 1 << 18;
-// Share flags of the one-launch backward with a GQA split, kFlagSlots slots
-// (as the Delta flags) of kMaxShareFlags, one per dK/dV share.
-constexpr int kMaxShareFlags = 1 << 16;
 
 // Shares of a dK/dV key block whose queries take nqs stages per query head:
 // its group x nqs stages in runs of about dkv_share_stages, never fewer than
@@ -569,6 +569,16 @@ __device__ __forceinline__ uint32_t load_uc_sync(const void *src) {
     uint32_t v;
     asm volatile("global_load_dword %0, %1, off sc0 sc1\n\ts_waitcnt vmcnt(0)" : "=v"(v) : "v"(src) : "memory");
     return v;
+}
+// The same for 8 bytes (naturally aligned: one access, never half old and
+// half new), and a write-through store of 8 bytes.
+__device__ __forceinline__ unsigned long long load2_uc_sync(const unsigned long long *src) {
+    unsigned long long v;
+    asm volatile("global_load_dwordx2 %0, %1, off sc0 sc1\n\ts_waitcnt vmcnt(0)" : "=v"(v) : "v"(src) : "memory");
+    return v;
+}
+__device__ __forceinline__ void store2_wt(unsigned long long *dst, unsigned long long v) {
+    asm volatile("global_store_dwordx2 %0, %1, off sc0 sc1" ::"v"(dst), "v"(v) : "memory");
 }
 // Waits until this wave's stores have been acknowledged.
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }

@@ -60,6 +60,10 @@ hipError_t launch_bwd_dq(const Params &p, int dtype_bf16, int d, int causal, int
 hipError_t launch_bwd_dkv(const Params &p, int dtype_bf16, int d, int causal, hipStream_t stream);
 // partial planes of the split (the most shares of any key block; 1: none)
 int dkv_split(const Params &p, int dtype_bf16, int d, int causal);
+// the workspace the split takes (0: no split): 2 * dkv_split(...) * B * Hkv *
+// N * d floats of partial planes, then 8 bytes per share for the one-launch
+// backward's share flags
+size_t dkv_workspace_bytes(const Params &p, int dtype_bf16, int d, int causal);
 // The one-launch backward from O (dQ pass with Delta + dK/dV pass, bf16;
 // with p.dkv_ws a GQA split as launch_bwd_dkv, whose reduce runs in the same
 // launch, or as a second launch where the share flags do not fit): available

@@ -346,10 +346,9 @@ int mxfa_bwd_reduce_timeouts(unsigned long long *count) {
 size_t mxfa_bwd_workspace_bytes(const mxfa_shape *shape) {
     if (check_shape(shape) != MXFA_OK) return 0;
     const Params p = make_params(shape);
-    const int split = mxfa::dkv_split(p, shape->dtype == MXFA_BF16, shape->d, shape->causal);
-    if (split <= 1) return 0;
-    // fp32 partial dK and dV planes, one pair per share of a key block
-    return 2 * (size_t)split * shape->B * shape->Hkv * shape->N * shape->d * sizeof(float);
+    // fp32 partial dK and dV planes, one pair per share of a key block, and a
+    // flag per share
+    return mxfa::dkv_workspace_bytes(p, shape->dtype == MXFA_BF16, shape->d, shape->causal);
 }
 
 int mxfa_run_bwd_naive(const mxfa_shape *shape, const void *q, const void *k, const void *v,

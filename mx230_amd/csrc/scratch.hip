@@ -14,9 +14,10 @@ namespace mxfa {
 
 namespace {
 
-// 64 MiB per device, held from the library's first use on the device until
-// the process ends.
-constexpr size_t kScratchBytes = 64ull << 20;
+// 65 MiB per device (64 MiB of partial planes and up to 1 MiB of share
+// flags), held from the library's first use on the device until the process
+// ends.
+constexpr size_t kScratchBytes = 65ull << 20;
 static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 
 constexpr int kMaxDevices = 64;

@@ -78,7 +78,7 @@ int main(void) {
     EXPECT(mxfa_bwd_workspace_bytes(NULL), 0);
     EXPECT(mxfa_bwd_workspace_bytes(&ok), 0);
     s = shape(2, 14, 2, 4096, 64, 1, MXFA_BF16, 0.0f);
-    EXPECT(mxfa_bwd_workspace_bytes(&s), 2LL * 8 * 2 * 2 * 4096 * 64 * 4); /* cfg4: 8 planes */
+    EXPECT(mxfa_bwd_workspace_bytes(&s), 2LL * 8 * 2 * 2 * 4096 * 64 * 4 + 8 * 908); /* cfg4: 8 planes, 908 shares */
     EXPECT(mxfa_naive_scratch_bytes(&ok), 4LL * 12 * 4096 * 4096 * 4);
     EXPECT(mxfa_naive_scratch_bytes(NULL), 0);
     EXPECT(mxfa_bwd_one_launch(&ok), 1);
@@ -121,7 +121,7 @@ int main(void) {
     EXPECT(mxfa_run_naive_fwd(&s, p, p, p, NULL, p, NULL), MXFA_ERR_NULL);
 
     /* the no-alloc backward: over its scratch, or missing pointers */
-    EXPECT(mxfa_bwd_noalloc_scratch_bytes(), 64LL << 20);
+    EXPECT(mxfa_bwd_noalloc_scratch_bytes(), 65LL << 20);
     s = shape(1, 64, 4, 8192, 64, 1, MXFA_BF16, 0.0f);
     EXPECT(mxfa_run_bwd_noalloc(&s, p, p, p, p, p, fp, fp, p, p, p, NULL), MXFA_ERR_SCRATCH);
     EXPECT(mxfa_run_bwd_noalloc(&ok, p, p, p, p, p, fp, fp, p, NULL, p, NULL), MXFA_ERR_NULL);

@@ -102,24 +102,31 @@ def test_sizes_and_strings(lib):
     assert lib.mxfa_shutdown() == 0
 
 
+# The workspace of a split: 2 x planes x B x Hkv x N x d fp32 partial sums
+# (planes: the most shares any key block takes), then an 8-byte flag per
+# share (all key blocks' shares) for the one-launch backward's reduce.
 @pytest.mark.parametrize("kw,nbytes", [
     # no GQA: nothing to split
     (dict(B=4, Hq=12, Hkv=12, N=4096, d=64), 0),
     # cfg4 (Qwen2.5, 7:1): 2*2 (b, kv head) x 32 key blocks = 128 work-groups
     # for 2 x 768 slots; 7 is prime, so one query head per share at least;
-    # about 58 stages per share gives key blocks 0-2 (7 x 64-60 stages) 8
-    (dict(B=2, Hq=14, Hkv=2, N=4096, d=64), 2 * 8 * 2 * 2 * 4096 * 64 * 4),
+    # about 58 stages per share gives key blocks 0-2 (7 x 64-60 stages) 8;
+    # 908 shares in all
+    (dict(B=2, Hq=14, Hkv=2, N=4096, d=64), 2 * 8 * 2 * 2 * 4096 * 64 * 4 + 8 * 908),
     # cfg5 d=64 (TinyLlama, 8:1): 64 work-groups; 4 shares give 256 < 1536, so
-    # 8 at least; about 17 stages per share gives key block 0 (8 x 32 stages) 16
-    (dict(B=1, Hq=32, Hkv=4, N=2048, d=64), 2 * 16 * 1 * 4 * 2048 * 64 * 4),
+    # 8 at least; about 17 stages per share gives key block 0 (8 x 32 stages)
+    # 16; 656 shares
+    (dict(B=1, Hq=32, Hkv=4, N=2048, d=64), 2 * 16 * 1 * 4 * 2048 * 64 * 4 + 8 * 656),
     # cfg5 d=128: 64-key blocks, 128 work-groups for 2 x 512 slots: 8 shares
-    (dict(B=1, Hq=32, Hkv=4, N=2048, d=128), 2 * 8 * 1 * 4 * 2048 * 128 * 4),
+    # each, 1024
+    (dict(B=1, Hq=32, Hkv=4, N=2048, d=128), 2 * 8 * 1 * 4 * 2048 * 128 * 4 + 8 * 1024),
     # 8 * 8 (b, kv head) x 32 key blocks = 2048 work-groups, twice 768 slots: no split
     (dict(B=8, Hq=16, Hkv=8, N=4096, d=64), 0),
-    # 512 work-groups: 3 shares would be the first to reach 2 x 768, and 4 divides 8
-    (dict(B=4, Hq=32, Hkv=4, N=4096, d=64), 2 * 4 * 4 * 4 * 4096 * 64 * 4),
-    # fp32 parity path, tiny GQA shape: whole group split
-    (dict(B=1, Hq=2, Hkv=1, N=128, d=64, dtype=mx.MXFA_F32), 2 * 2 * 1 * 1 * 128 * 64 * 4),
+    # 512 work-groups: 3 shares would be the first to reach 2 x 768, and 4
+    # divides 8: 4 shares each, 2048
+    (dict(B=4, Hq=32, Hkv=4, N=4096, d=64), 2 * 4 * 4 * 4 * 4096 * 64 * 4 + 8 * 2048),
+    # fp32 parity path, tiny GQA shape: whole group split, 2 shares
+    (dict(B=1, Hq=2, Hkv=1, N=128, d=64, dtype=mx.MXFA_F32), 2 * 2 * 1 * 1 * 128 * 64 * 4 + 8 * 2),
     # invalid shape
     (dict(Hq=3, Hkv=2), 0),
 ])
@@ -398,14 +405,15 @@ def test_library_has_no_kernels():
 
 
 def test_noalloc_rejects_shapes_beyond_its_scratch(lib):
-    """mxfa_run_bwd_noalloc: 64 MiB of scratch per device; a shape that needs
-    more is MXFA_ERR_SCRATCH before any device work (fake pointers, no GPU)."""
-    assert lib.mxfa_bwd_noalloc_scratch_bytes() == 64 << 20
+    """mxfa_run_bwd_noalloc: 65 MiB of scratch per device (64 MiB of planes
+    and 1 MiB of share flags); a shape that needs more is MXFA_ERR_SCRATCH
+    before any device work (fake pointers, no GPU)."""
+    assert lib.mxfa_bwd_noalloc_scratch_bytes() == 65 << 20
     p = ctypes.c_void_p(4096)
-    fits = _shape(B=1, Hq=32, Hkv=4, N=2048, d=128)  # cfg5 d = 128: exactly 64 MiB (8 planes)
-    assert lib.mxfa_bwd_workspace_bytes(ctypes.byref(fits)) == 64 << 20
-    big = _shape(B=1, Hq=64, Hkv=4, N=8192, d=64)  # 8 shares of 256 key blocks: 128 MiB
-    assert lib.mxfa_bwd_workspace_bytes(ctypes.byref(big)) == 2 * 8 * 4 * 8192 * 64 * 4
+    fits = _shape(B=1, Hq=32, Hkv=4, N=2048, d=128)  # cfg5 d = 128: 64 MiB of planes (8), 1024 flags
+    assert lib.mxfa_bwd_workspace_bytes(ctypes.byref(fits)) == (64 << 20) + 8 * 1024
+    big = _shape(B=1, Hq=64, Hkv=4, N=8192, d=64)  # 8 planes of 4 x 8192 rows: 128 MiB, 2048 flags
+    assert lib.mxfa_bwd_workspace_bytes(ctypes.byref(big)) == 2 * 8 * 4 * 8192 * 64 * 4 + 8 * 2048
     assert lib.mxfa_run_bwd_noalloc(ctypes.byref(big), p, p, p, p, p, p, p, p, p, p, None) == \
         mx_status("MXFA_ERR_SCRATCH")
     assert lib.mxfa_run_bwd_noalloc(ctypes.byref(big), p, p, p, p, p, p, p, p, p, None, None) == \

@@ -15,8 +15,10 @@ themselves after a wait bounded in time.
   add the shares' partial sums once the shares' flags are set) equals the
   two-launch split (with its reduce launch) bitwise.
 - Launches in flight together on several streams, more than the flag slots,
-  so later launches see other launches' flags (Delta and, with a GQA split,
-  share flags), still give each one its own result, bitwise.
+  so later launches see other launches' Delta flags, still give each one its
+  own result, bitwise. With a GQA split a launch takes a slot of share flags
+  no other stream's launch in flight holds, or runs its reduce as a second
+  launch: no reduce work-group waits out its bound.
 """
 from __future__ import annotations
 
@@ -147,12 +149,14 @@ def test_one_launch_concurrent_streams(opts):
             assert torch.equal(a, b), (i, n)
 
 
-def test_one_launch_concurrent_streams_gqa_split(opts):
-    """Six GQA-split launches in flight on six streams, each with its own
-    workspace (four slots of share flags)."""
+@pytest.mark.parametrize("nstreams", [6, 12])
+def test_one_launch_concurrent_streams_gqa_split(opts, nstreams):
+    """GQA-split launches in flight on 6 or 12 streams, each with its own
+    workspace: four slots of share flags, so the launches beyond four that
+    overlap others run their reduce as a second launch (bitwise the same)."""
     import torch
     import mx230_amd as mx
-    cases = [_setup(2, 6, 2, 1000 + 64 * i, 64, True, seed=40 + i) for i in range(6)]
+    cases = [_setup(2, 6, 2, 1000 + 64 * i, 64, True, seed=40 + i) for i in range(nstreams)]
     wss = [torch.empty(mx.bwd_workspace_bytes(t[0], t[1], True), dtype=torch.uint8, device="cuda") for t in cases]
     assert all(w.numel() > 0 for w in wss)
 
@@ -178,6 +182,31 @@ def test_one_launch_concurrent_streams_gqa_split(opts):
     for i, (got, ref) in enumerate(zip(outs, refs)):
         for n, a, b in zip(("Delta", "dQ", "dK", "dV"), got, ref):
             assert torch.equal(a, b), (i, n)
+
+
+def test_one_launch_gqa_split_queued_on_one_stream(opts):
+    """Twenty GQA-split launches queued back to back on one stream (as a timed
+    loop queues them): they share one slot of share flags in stream order,
+    none waits out its reduce, and the last result is the two-launch one."""
+    import torch
+    import mx230_amd as mx
+    t = _setup(1, 32, 4, 2048, 64, True, seed=77)
+    q, k, v, do, o, lse = t
+    ws = torch.empty(mx.bwd_workspace_bytes(q, k, True), dtype=torch.uint8, device="cuda")
+    outs = {}
+    for one in (False, True):
+        opts(one_launch=one)
+        delta = torch.empty_like(lse)
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        call = mx.prepare(mx.run_bwd_ws, q, k, v, o, do, lse, delta, dq, dk, dv, ws, True)
+        t0 = mx.bwd_reduce_timeouts()
+        for _ in range(20 if one else 1):
+            call()
+        torch.cuda.synchronize()
+        assert mx.bwd_reduce_timeouts() == t0
+        outs[one] = (delta, dq, dk, dv)
+    for n, a, b in zip(("Delta", "dQ", "dK", "dV"), outs[True], outs[False]):
+        assert torch.equal(a, b), n
 
 
 @pytest.mark.parametrize("shape", [(2, 14, 2, 4096, 64), (1, 32, 4, 2048, 64), (1, 32, 4, 2048, 128),

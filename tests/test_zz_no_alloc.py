@@ -15,7 +15,7 @@ pytestmark = pytest.mark.gpu
 
 # (B, Hq, Hkv, N, d, causal), largest first; every call below runs both paths
 CALLS = [
-    [(1, 32, 4, 2048, 128, True), (1, 8, 2, 1000, 64, True)],   # 64 MiB then 4.1 MB of scratch
+    [(1, 32, 4, 2048, 128, True), (1, 8, 2, 1000, 64, True)],   # 64 MiB (+8 KB) then 4.1 MB of scratch
     [(2, 14, 2, 4096, 64, True), (1, 6, 2, 577, 64, False)],     # cfg4, then non-causal ragged
     [(1, 4, 4, 300, 64, True), (1, 4, 1, 200, 128, True)],       # no split, then a d = 128 split
 ]
