@@ -16,9 +16,8 @@ themselves after a wait bounded in time.
   two-launch split (with its reduce launch) bitwise.
 - Launches in flight together on several streams, more than the flag slots,
   so later launches see other launches' Delta flags, still give each one its
-  own result, bitwise. With a GQA split a launch takes a slot of share flags
-  no other stream's launch in flight holds, or runs its reduce as a second
-  launch: no reduce work-group waits out its bound.
+  own result, bitwise. With a GQA split each launch's share flags are in its
+  own workspace, with its own value: no reduce work-group waits out its bound.
 """
 from __future__ import annotations
 
@@ -152,8 +151,8 @@ def test_one_launch_concurrent_streams(opts):
 @pytest.mark.parametrize("nstreams", [6, 12])
 def test_one_launch_concurrent_streams_gqa_split(opts, nstreams):
     """GQA-split launches in flight on 6 or 12 streams, each with its own
-    workspace: four slots of share flags, so the launches beyond four that
-    overlap others run their reduce as a second launch (bitwise the same)."""
+    workspace (and so its own share flags): each result is the two-launch
+    one bitwise, and no reduce work-group waits out its bound."""
     import torch
     import mx230_amd as mx
     cases = [_setup(2, 6, 2, 1000 + 64 * i, 64, True, seed=40 + i) for i in range(nstreams)]
@@ -186,8 +185,9 @@ def test_one_launch_concurrent_streams_gqa_split(opts, nstreams):
 
 def test_one_launch_gqa_split_queued_on_one_stream(opts):
     """Twenty GQA-split launches queued back to back on one stream (as a timed
-    loop queues them): they share one slot of share flags in stream order,
-    none waits out its reduce, and the last result is the two-launch one."""
+    loop queues them) through one workspace: each finds the flags of the one
+    before (another value) and waits for its own, none waits out its bound,
+    and the last result is the two-launch one."""
     import torch
     import mx230_amd as mx
     t = _setup(1, 32, 4, 2048, 64, True, seed=77)
