@@ -1275,9 +1275,16 @@ size_t dkv_workspace_bytes(const Params &p, int dtype_bf16, int d, int causal) {
 // memory held before, equals it only with probability 2^-64.
 static unsigned long long next_share_nonce() {
     static const unsigned long long base = [] {
-        std::random_device rd;
+        unsigned long long r = 0;
+        try {  // no exception may leave the C ABI: without an entropy source, the clocks alone
+            std::random_device rd;
+            r = ((unsigned long long)rd() << 32) ^ (unsigned long long)rd();
+        } catch (...) {
+        }
         const unsigned long long t = (unsigned long long)std::chrono::steady_clock::now().time_since_epoch().count();
-        return ((unsigned long long)rd() << 32) ^ (unsigned long long)rd() ^ (t * 0x9E3779B97F4A7C15ull);
+        const unsigned long long w =
+            (unsigned long long)std::chrono::system_clock::now().time_since_epoch().count();
+        return r ^ (t * 0x9E3779B97F4A7C15ull) ^ (w * 0xC2B2AE3D27D4EB4Full);
     }();
     static std::atomic<unsigned long long> count{0};
     unsigned long long x = base + 0x9E3779B97F4A7C15ull * (count.fetch_add(1) + 1);
