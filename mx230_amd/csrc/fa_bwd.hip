@@ -488,8 +488,11 @@ struct DkvTile16 {
 #pragma unroll
                 for (int xt = 0; xt < XT; ++xt) {
                     if constexpr (WT) {  // partial sums (kmul = 1) for a reduce in the same launch
-                        store4_wt(dK + (size_t)key * D + 16 * xt + 4 * g, accK[xt][kt]);
-                        store4_wt(dV + (size_t)key * D + 16 * xt + 4 * g, accV[xt][kt]);
+                        // from the wave's first key row (a wave-uniform base), within its rows
+                        const uint32_t bytes = (uint32_t)(min(ROWS, N - kw0) * D * 4);
+                        const uint32_t off = (uint32_t)(((key - kw0) * D + 16 * xt + 4 * g) * 4);
+                        store4_wt(reinterpret_cast<float *>(dK + (size_t)kw0 * D), bytes, off, accK[xt][kt]);
+                        store4_wt(reinterpret_cast<float *>(dV + (size_t)kw0 * D), bytes, off, accV[xt][kt]);
                     } else {
                         store4<U>(dK + (size_t)key * D + 16 * xt + 4 * g, accK[xt][kt], kmul);
                         store4<U>(dV + (size_t)key * D + 16 * xt + 4 * g, accV[xt][kt], 1.0f);

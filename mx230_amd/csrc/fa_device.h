@@ -553,9 +553,16 @@ __device__ __forceinline__ void lds_dma4_uc(uint32_t base, const void *src) {
 __device__ __forceinline__ void store_wt(void *dst, uint32_t v) {
     asm volatile("global_store_dword %0, %1, off sc0 sc1" ::"v"(dst), "v"(v) : "memory");
 }
-// A write-through store of four floats.
-__device__ __forceinline__ void store4_wt(float *dst, f32x4 v) {
-    asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" ::"v"(dst), "v"(v) : "memory");
+// A write-through store of four floats at byte offset off of base (wave-
+// uniform); offsets at or past `bytes` are dropped. A builtin, not inline asm:
+// a store of more than 64 bits whose data registers a VALU instruction
+// overwrites within two wait states needs the compiler's hazard padding, and
+// the compiler cannot see inside an asm statement (a build that kept the dK/dV
+// accumulators in AGPRs moved the next one into the data registers right after
+// such an asm store, and the stored partial sums were wrong).
+__device__ __forceinline__ void store4_wt(float *base, uint32_t bytes, uint32_t off, f32x4 v) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, 0, bytes, 0x00020000);
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 17);  // cache policy sc0 | sc1
 }
 // Four floats at byte offset off of base (wave-uniform) past the caches;
 // offsets at or past `bytes` read as 0.

@@ -396,6 +396,55 @@ def test_code_object_has_every_kernel():
     assert {"mxfa_delta_fallbacks", "mxfa_reduce_timeouts"} <= objects
 
 
+def _vgpr_range(op: str):
+    m = re.fullmatch(r"v\[(\d+):(\d+)\]", op) or re.fullmatch(r"v(\d+)", op)
+    if not m:
+        return None
+    lo = int(m.group(1))
+    return lo, int(m.group(m.lastindex))
+
+
+@pytest.mark.parametrize("which", ["CODE_OBJECT_PATH", "TIMELINE_CODE_OBJECT_PATH"])
+def test_code_object_store_data_hazard(which):
+    """No store of more than 64 bits has its data registers overwritten by a
+    VALU instruction within the two wait states gfx950 requires. The compiler
+    pads its own stores; a store it cannot see (inline asm) gets no padding,
+    which is how a build with the dK/dV accumulators in AGPRs came to write
+    wrong partial sums."""
+    objdump = "/opt/rocm/llvm/bin/llvm-objdump"
+    path = getattr(mx, which)
+    if not os.path.exists(objdump) or not os.path.exists(path):
+        pytest.skip("llvm-objdump or the code object is missing")
+    lines = subprocess.run([objdump, "-d", "--mcpu=gfx950", path], capture_output=True, text=True,
+                           check=True).stdout.splitlines()
+    insts = [ln.split("//")[0].strip() for ln in lines if ln.startswith("\t")]
+    store = re.compile(r"^(global|buffer|flat|scratch)_store_dwordx[34]\s")
+    stores = bad = 0
+    for i, ins in enumerate(insts):
+        if not store.match(ins):
+            continue
+        ops = [o.strip() for o in ins.split(None, 1)[1].split(",")]
+        data = _vgpr_range(ops[0] if ins.startswith("buffer") else ops[1])
+        if data is None:  # data in AGPRs
+            continue
+        stores += 1
+        waits = 0
+        for nxt in insts[i + 1:i + 3]:
+            if waits >= 2:
+                break
+            if nxt.startswith("s_nop"):
+                waits += int(nxt.split()[1], 0) + 1
+                continue
+            if nxt.startswith("v_"):
+                dst = _vgpr_range(nxt.split(None, 1)[1].split(",")[0].strip()) if " " in nxt else None
+                if dst and dst[0] <= data[1] and data[0] <= dst[1]:
+                    bad += 1
+                    break
+            waits += 1
+    assert stores > 100
+    assert bad == 0
+
+
 def test_library_has_no_kernels():
     """libmxfa.so holds no kernels (they live in the code object): its only
     device code is the scratch array of mxfa_run_bwd_noalloc."""
