@@ -445,6 +445,47 @@ def test_code_object_store_data_hazard(which):
     assert bad == 0
 
 
+def _sgprs(op: str):
+    m = re.fullmatch(r"s\[(\d+):(\d+)\]", op) or re.fullmatch(r"s(\d+)", op)
+    return set(range(int(m.group(1)), int(m.group(m.lastindex)) + 1)) if m else set()
+
+
+@pytest.mark.parametrize("which", ["CODE_OBJECT_PATH", "TIMELINE_CODE_OBJECT_PATH"])
+def test_code_object_sgpr_vmem_hazard(which):
+    """No vector-memory instruction reads an SGPR (its saddr or resource) that a
+    VALU instruction wrote within the five wait states gfx950 requires: the
+    staging loads with a scalar base are inline asm, which the compiler does
+    not pad."""
+    objdump = "/opt/rocm/llvm/bin/llvm-objdump"
+    path = getattr(mx, which)
+    if not os.path.exists(objdump) or not os.path.exists(path):
+        pytest.skip("llvm-objdump or the code object is missing")
+    lines = subprocess.run([objdump, "-d", "--mcpu=gfx950", path], capture_output=True, text=True,
+                           check=True).stdout.splitlines()
+    insts = [ln.split("//")[0].strip() for ln in lines if ln.startswith("\t")]
+    vmem = re.compile(r"^(global|buffer|scratch)_(load|store)")
+    checked = bad = 0
+    for i, ins in enumerate(insts):
+        if not vmem.match(ins) or " " not in ins:
+            continue
+        used = set()
+        for op in ins.split(None, 1)[1].split(","):
+            used |= _sgprs(op.strip())
+        if not used:
+            continue
+        checked += 1
+        waits = 0
+        for prev in reversed(insts[max(0, i - 5):i]):
+            if waits >= 5:
+                break
+            if prev.startswith("v_") and " " in prev and _sgprs(prev.split(None, 1)[1].split(",")[0].strip()) & used:
+                bad += 1
+                break
+            waits += int(prev.split()[1], 0) + 1 if prev.startswith("s_nop") else 1
+    assert checked > 500
+    assert bad == 0
+
+
 def test_library_has_no_kernels():
     """libmxfa.so holds no kernels (they live in the code object): its only
     device code is the scratch array of mxfa_run_bwd_noalloc."""
