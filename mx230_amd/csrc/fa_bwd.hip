@@ -79,19 +79,20 @@ __device__ __forceinline__ void preprocess_body(const T *dout, const T *o, float
     if (row < rows && part == 0) delta[row] = acc;
 }
 
-// One dK/dV stage: the Pol::ROWS query rows from qs of Q and dO of head bh,
-// and their LSE and Delta, into LDS buffers.
+// One dK/dV stage: the Pol::ROWS query rows from row `row` of Q and dO (row =
+// bh N + qs: query qs of head bh; nvalid = N - qs of them exist), and their
+// LSE and Delta, into LDS buffers.
+// The buffers are given as LDS addresses.
 template <class Pol, int NT = 256, bool STAGE_DELTA = true>
-__device__ __forceinline__ void stage_qdo(typename Pol::T *sq, typename Pol::T *sdo, float *sl, float *sd,
-                                          const Params &p, size_t bh, int qs, int N, const RowPlan<Pol, NT> &pl,
-                                          int wave, int lane) {
+__device__ __forceinline__ void stage_qdo(uint32_t sq, uint32_t sdo, uint32_t sl, uint32_t sd, const Params &p,
+                                          size_t row, int nvalid, const RowPlan<Pol, NT> &pl, int wave, int lane) {
     using T = typename Pol::T;
-    const size_t off = (bh * N + qs) * Pol::D;
-    stage_rows<Pol, NT>(sq, static_cast<const T *>(p.q) + off, N - qs, pl, wave);
-    stage_rows<Pol, NT>(sdo, static_cast<const T *>(p.dout) + off, N - qs, pl, wave);
+    const size_t off = row * Pol::D;
+    stage_rows<Pol, NT>(sq, static_cast<const T *>(p.q) + off, nvalid, pl, wave);
+    stage_rows<Pol, NT>(sdo, static_cast<const T *>(p.dout) + off, nvalid, pl, wave);
     // rows past N: LSE = +inf makes their p (and so dS) exactly 0
-    if (wave == 0) stage_vec64(sl, p.lse + bh * N + qs, N - qs, lane, &kPosInf);
-    if (STAGE_DELTA && wave == 1) stage_vec64(sd, p.delta + bh * N + qs, N - qs, lane, p.delta + bh * N + qs);
+    if (wave == 0) stage_vec64(sl, p.lse + row, nvalid, lane, &kPosInf);
+    if (STAGE_DELTA && wave == 1) stage_vec64(sd, p.delta + row, nvalid, lane, p.delta + row);
 }
 
 // Delta flags of the one-launch backward (see Params::epoch). Zero at load;
@@ -675,14 +676,14 @@ __device__ __forceinline__ void dkv_body(const Params &p, const DkvWork wk, DkvS
     const size_t bh0 = (size_t)b * p.Hq + (size_t)kvh * p.group;  // the group's first query head
     wg_info(1, kb, nsteps);
 
-    // Stages are loaded strictly in order; (ld_h, ld_i) = query head and stage
-    // within it of the next one (kept incrementally: no division per stage).
+    // Stages are loaded strictly in order. The next one's query head ld_bh,
+    // its place ld_i in that head, its first query ld_qs and row ld_row =
+    // ld_bh N + ld_qs, and the head's first Delta flag ld_fb = ld_bh nfb are
+    // kept incrementally (wave-uniform, so in scalar registers): a stage then
+    // costs a few scalar adds, not the products of the full index.
     const RowPlan<Pol, NT> plan(tid);
-    int ld_h = 0, ld_i = 0;
-    if (g0 > 0) {
-        ld_h = g0 / nqs;
-        ld_i = g0 - ld_h * nqs;
-    }
+    int ld_i = 0;
+    if (g0 > 0) ld_i = g0 - (g0 / nqs) * nqs;
     const int i_first = ld_i;  // the first stage's place in its query head
     // WAIT: the flag of each stage's Delta block is fetched into sm.sF one
     // issue ahead, with a load that misses the caches (as are the Delta rows
@@ -694,18 +695,32 @@ __device__ __forceinline__ void dkv_body(const Params &p, const DkvWork wk, DkvS
     // with nothing fetched ahead, is polled directly.
     const int nfb = (N + kFlagRows - 1) / kFlagRows;
     const uint32_t *flags = g_delta_flags + (size_t)p.flag_slot * kMaxFlagBlocks;
+    size_t ld_bh = bh0 + (size_t)(g0 / nqs);
+    int ld_qs = qstart + ld_i * BQ;
+    size_t ld_row = ld_bh * N + ld_qs;
+    size_t ld_fb = ld_bh * nfb;
+    // the buffers' LDS addresses (buffer bf: the first's plus bf times a buffer)
+    const uint32_t lds_q = lds_addr(&sQ[0][0]), lds_do = lds_addr(&sdO[0][0]);
+    const uint32_t lds_l = lds_addr(&sL[0][0]), lds_d = lds_addr(&sD[0][0]), lds_f = lds_addr(&sm.sF[0]);
     auto issue = [&](int st) __attribute__((always_inline)) {
-        const int bf = st % NBUF;
-        const size_t bh = bh0 + ld_h;
-        const int qs = qstart + ld_i * BQ;
-        stage_qdo<Pol, NT, !WAIT>(sQ[bf], sdO[bf], sL[bf], sD[bf], p, bh, qs, N, plan, wave, lane);
-        if (++ld_i == nqs) {
+        const int bf = (int)((unsigned)st % NBUF);
+        const size_t bh = ld_bh, row = ld_row, fb = ld_fb;
+        const int qs = ld_qs;
+        const uint32_t ld_sd = lds_d + bf * (uint32_t)sizeof(sD[0]);
+        stage_qdo<Pol, NT, !WAIT>(lds_q + bf * (uint32_t)sizeof(sQ[0]), lds_do + bf * (uint32_t)sizeof(sdO[0]),
+                                  lds_l + bf * (uint32_t)sizeof(sL[0]), ld_sd, p, row, N - qs, plan, wave, lane);
+        ld_qs += BQ;
+        ld_row += BQ;
+        if (++ld_i == nqs) {  // the next query head's first stage
             ld_i = 0;
-            ++ld_h;
+            ld_qs = qstart;
+            ld_row = row + (size_t)(N - qs) + (size_t)qstart;
+            ++ld_bh;
+            ld_fb += nfb;
         }
         if constexpr (WAIT) {
             if (wave == 1) {
-                const uint32_t *f = flags + bh * nfb + qs / kFlagRows;
+                const uint32_t *f = flags + fb + (uint32_t)qs / kFlagRows;
                 // delta_wait < 0 trusts no flag (every stage takes the fallback)
                 bool ready = p.delta_wait >= 0 && st > 0 && sm.sF[st & 1] == p.epoch;
                 if (!ready && p.delta_wait >= 0) {
@@ -717,7 +732,7 @@ __device__ __forceinline__ void dkv_body(const Params &p, const DkvWork wk, DkvS
                     }
                 }
                 if (ready) {
-                    lds_dma4_uc(lds_addr(sD[bf]), p.delta + bh * N + min(qs + lane, N - 1));
+                    lds_dma4_uc(ld_sd, p.delta + row + min(lane, N - 1 - qs));
                 } else {
                     DqTile::delta_fallback(sD[bf], p, bh, qs, N, lane);
                     if (lane == 0) atomicAdd(&mxfa_delta_fallbacks, 1ull);
@@ -726,8 +741,7 @@ __device__ __forceinline__ void dkv_body(const Params &p, const DkvWork wk, DkvS
             // the next stage's flag; one lane: the DMA writes each active
             // lane's dword at base + 4 lane
             if (wave == 1 && st + 1 < nsteps && lane == 0) {
-                const int qs_next = qstart + ld_i * BQ;
-                lds_dma4_uc(lds_addr(&sm.sF[(st + 1) & 1]), flags + (bh0 + ld_h) * nfb + qs_next / kFlagRows);
+                lds_dma4_uc(lds_f + ((st + 1) & 1) * 4u, flags + ld_fb + (uint32_t)ld_qs / kFlagRows);
             }
         }
     };
@@ -747,7 +761,7 @@ __device__ __forceinline__ void dkv_body(const Params &p, const DkvWork wk, DkvS
     // other's code (two bodies behind one branch make the register allocator
     // spill).
     auto run = [&](int st, int i) __attribute__((always_inline)) {
-        const int cur = st % NBUF;
+        const int cur = (int)((unsigned)st % NBUF);
         if (st + 1 < nsteps) issue(st + 1);
         const int qs = qstart + i * BQ;
         // a wave whose keys all follow the stage's queries has nothing to do

@@ -706,16 +706,22 @@ struct RowPlan {
 };
 
 // stage_rows with a RowPlan: rows >= nvalid re-read row nvalid - 1, as there.
+// The tile as an LDS address (tile_lds), or as a pointer below.
 template <class Pol, int NT = 256>
-__device__ __forceinline__ void stage_rows(typename Pol::T *tile, const typename Pol::T *src, int nvalid,
+__device__ __forceinline__ void stage_rows(uint32_t tile_lds, const typename Pol::T *src, int nvalid,
                                            const RowPlan<Pol, NT> &pl, int wave, int row_stride = Pol::D) {
-    const uint32_t base = lds_addr(tile) + wave * 64 * 16;
+    const uint32_t base = tile_lds + wave * 64 * 16;
     const uint32_t rs_bytes = (uint32_t)row_stride * sizeof(typename Pol::T);
 #pragma unroll
     for (int k = 0; k < RowPlan<Pol, NT>::NK; ++k) {
         const uint32_t grow = (uint32_t)min((int)(pl.rc[k] & 255u), nvalid - 1);
         lds_dma16_s(base + k * NT * 16, src, grow * rs_bytes + (pl.rc[k] >> 8));
     }
+}
+template <class Pol, int NT = 256>
+__device__ __forceinline__ void stage_rows(typename Pol::T *tile, const typename Pol::T *src, int nvalid,
+                                           const RowPlan<Pol, NT> &pl, int wave, int row_stride = Pol::D) {
+    stage_rows<Pol, NT>(lds_addr(tile), src, nvalid, pl, wave, row_stride);
 }
 
 // One K/V stage: Pol::ROWS key rows from k0 of K and V (rows row_stride
@@ -780,9 +786,14 @@ __device__ const float kPosInf = __builtin_inff();
 extern __device__ const float kPosInf;
 #endif
 
-// 64 fp32 values src[l] (l < nvalid, else *pad) -> dst[l], by one wave.
+// 64 fp32 values src[l] (l < nvalid, else *pad) -> dst[l], by one wave (dst
+// as an LDS address, or as a pointer).
+__device__ __forceinline__ void stage_vec64(uint32_t dst_lds, const float *src, int nvalid, int lane,
+                                            const float *pad) {
+    lds_dma4(dst_lds, lane < nvalid ? src + lane : pad);
+}
 __device__ __forceinline__ void stage_vec64(float *dst, const float *src, int nvalid, int lane, const float *pad) {
-    lds_dma4(lds_addr(dst), lane < nvalid ? src + lane : pad);
+    stage_vec64(lds_addr(dst), src, nvalid, lane, pad);
 }
 
 // Waits for this wave's outstanding global->LDS loads (the caller then
