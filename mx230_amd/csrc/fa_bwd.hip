@@ -401,6 +401,10 @@ struct DkvTile16 {
     template <bool CAUSAL, bool MASK, bool PRIO>
     __device__ __forceinline__ void stage(const T *sq, const T *sdo, const float *sl, const float *sd, int qs, int kw0,
                                           int lane) {
+        if constexpr (kBatchedReads) {
+            stage_batched<CAUSAL, MASK>(sq, sdo, sl, sd, qs, kw0, lane);
+            return;
+        }
         const int g = lane >> 4, l16 = lane & 15;
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
@@ -466,6 +470,92 @@ struct DkvTile16 {
                 }
             }
             wave_priority<PRIO>(0);
+        }
+    }
+
+    // The same stage with every LDS operand of a 32-query block read ahead of the
+    // products that take it (kBatchedReads: one key tile per wave at d = 128,
+    // two waves per SIMD, where the default order reads each operand one or two
+    // MFMAs before its use and the wave then waits out the LDS latency): all the
+    // score and dP operands first, then the products; the chained products'
+    // operands right after those, so they arrive while the softmax runs. The
+    // scheduling barriers keep the compiler from sinking the reads back to
+    // their uses. The arithmetic and its order are those of stage().
+    static constexpr bool kBatchedReads = D == 128 && KT == 1;
+    template <bool CAUSAL, bool MASK>
+    __device__ __forceinline__ void stage_batched(const T *sq, const T *sdo, const float *sl, const float *sd, int qs,
+                                                  int kw0, int lane) {
+        const int g = lane >> 4, l16 = lane & 15;
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+            Frag aq[2][NC], ad[2][NC];
+            f32x4 nl[2], dl[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int q4 = 32 * blk + Pol::bidx(t, g, 0);
+                nl[t] = nl_of(sl + q4);
+                dl[t] = *reinterpret_cast<const f32x4 *>(sd + q4);
+                const int n = 32 * blk + Pol::arow(t, l16);
+                Pol::lds_row_frags(aq[t], sq, n, g);
+                Pol::lds_row_frags(ad[t], sdo, n, g);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            f32x4 s[2][KT], dp[2][KT];  // [t][kt]
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+#pragma unroll
+                for (int kt = 0; kt < KT; ++kt) {
+                    f32x4 c = nl[t];
+#pragma unroll
+                    for (int kc = 0; kc < NC; ++kc) c = Pol::mma(aq[t][kc], kf[kt][kc], c);
+                    s[t][kt] = c;
+                }
+#pragma unroll
+                for (int kt = 0; kt < KT; ++kt) {
+                    f32x4 c = dl[t];
+#pragma unroll
+                    for (int kc = 0; kc < NC; ++kc) c = Pol::mma(ad[t][kc], vf[kt][kc], c);
+                    dp[t][kt] = c;
+                }
+            }
+            Frag ov[XT], ok[XT];
+#pragma unroll
+            for (int xt = 0; xt < XT; ++xt) {
+                ov[xt] = Pol::chain_a(sdo, 16 * xt, 32 * blk, g, l16);
+                ok[xt] = Pol::chain_a(sq, 16 * xt, 32 * blk, g, l16);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+#pragma unroll
+                    for (int kt = 0; kt < KT; ++kt) {
+                        float x = Pol::kExactScale || P2 ? s[t][kt][r] * xmul : s[t][kt][r];
+                        if constexpr (MASK) {
+                            const bool before = Pol::bidx(t, g, r) - l16 < kw0 - qs + 16 * kt - 32 * blk;
+                            x = before ? -INFINITY : x;
+                        }
+                        const float pv = fast_exp2(x);
+                        s[t][kt][r] = pv;
+                        dp[t][kt][r] = pv * dp[t][kt][r];  // -dS / scale
+                    }
+                }
+            }
+            typename Pol::ChainB cp[KT], cds[KT];
+#pragma unroll
+            for (int kt = 0; kt < KT; ++kt) {
+                cp[kt] = Pol::pack(s[0][kt], s[1][kt]);
+                cds[kt] = Pol::pack(dp[0][kt], dp[1][kt]);
+            }
+#pragma unroll
+            for (int xt = 0; xt < XT; ++xt) {
+#pragma unroll
+                for (int kt = 0; kt < KT; ++kt) {
+                    accV[xt][kt] = Pol::mma(ov[xt], cp[kt], accV[xt][kt]);
+                    accK[xt][kt] = Pol::mma(ok[xt], cds[kt], accK[xt][kt]);
+                }
+            }
         }
     }
 
