@@ -132,15 +132,17 @@ constexpr int kFlagRows = 128;  // query rows per flag: one dQ work-group's bloc
 // where dQ and dK/dV waves share each SIMD).
 
 // 16x16 MFMA tiles (Pol = PolF32<64> or PolBF16<128>): lane l holds column
-// l%16 and rows 4(l/16) + r of each 16x16 C tile.
-template <class Pol_, int QT>
+// l%16 and rows 4(l/16) + r of each 16x16 C tile. W2 (bf16 d = 64, the
+// one-launch backward of small grids): compiled for two waves per SIMD, with
+// the stages' LDS operands read ahead of their products (stage_batched).
+template <class Pol_, int QT, bool W2 = false>
 struct DqTile16 {
     using Pol = Pol_;
     using T = typename Pol::T;
     using Frag = typename Pol::Frag;
     static constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
     static constexpr int ROWS = 16 * QT;
-    static constexpr int kWaves = Pol::kWavesDq;
+    static constexpr int kWaves = W2 ? 2 : Pol::kWavesDq;
     static constexpr bool kPrioFused = D == 64;
 
     Frag qf[QT][NC], dof[QT][NC];
@@ -256,6 +258,10 @@ struct DqTile16 {
     // Q scale log2(e) and nL2 is -L log2(e).
     template <bool CAUSAL, bool MASK, bool PRIO>
     __device__ __forceinline__ void stage(const T *sk, const T *sv, int k0, int q0, int N, int lane, float xmul) {
+        if constexpr (kBatchedReads) {
+            stage_batched<CAUSAL, MASK>(sk, sv, k0, q0, N, lane, xmul);
+            return;
+        }
         const int g = lane >> 4, l16 = lane & 15;
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
@@ -315,6 +321,75 @@ struct DqTile16 {
         }
     }
 
+    // The same stage with every LDS operand of a 32-key block read ahead of the
+    // products that take it (W2: two waves per SIMD leave the registers for it;
+    // as DkvTile16's stage_batched, the same arithmetic in the same order as
+    // stage()).
+    static constexpr bool kBatchedReads = W2;
+    template <bool CAUSAL, bool MASK>
+    __device__ __forceinline__ void stage_batched(const T *sk, const T *sv, int k0, int q0, int N, int lane,
+                                                  float xmul) {
+        const int g = lane >> 4, l16 = lane & 15;
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+            Frag ak[2][NC], av[2][NC];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int n = 32 * blk + Pol::arow(t, l16);
+                Pol::lds_row_frags(ak[t], sk, n, g);
+                Pol::lds_row_frags(av[t], sv, n, g);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            f32x4 s[2][QT], dp[2][QT];  // [t][qt]
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) {
+                    f32x4 c = f32x4{nL2[qt], nL2[qt], nL2[qt], nL2[qt]};
+#pragma unroll
+                    for (int kc = 0; kc < NC; ++kc) c = Pol::mma(ak[t][kc], qf[qt][kc], c);
+                    s[t][qt] = c;
+                }
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) {
+                    f32x4 c = f32x4{Dl[qt], Dl[qt], Dl[qt], Dl[qt]};
+#pragma unroll
+                    for (int kc = 0; kc < NC; ++kc) c = Pol::mma(av[t][kc], dof[qt][kc], c);
+                    dp[t][qt] = c;
+                }
+            }
+            Frag ok[XT];
+#pragma unroll
+            for (int xt = 0; xt < XT; ++xt) ok[xt] = Pol::chain_a(sk, 16 * xt, 32 * blk, g, l16);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) {
+                const int qi = q0 + 16 * qt + l16;
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        float x = s[t][qt][r];
+                        if constexpr (MASK) {
+                            const int key = k0 + 32 * blk + Pol::bidx(t, g, r);
+                            x = (key >= N || (CAUSAL && key > qi)) ? -INFINITY : x;
+                        }
+                        const float pv = fast_exp2(Pol::kExactScale ? x * xmul : x);
+                        s[t][qt][r] = pv * dp[t][qt][r];  // -dS / scale
+                    }
+                }
+            }
+            typename Pol::ChainB cb[QT];
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) cb[qt] = Pol::pack(s[0][qt], s[1][qt]);
+#pragma unroll
+            for (int xt = 0; xt < XT; ++xt) {
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) acc[xt][qt] = Pol::mma(ok[xt], cb[qt], acc[xt][qt]);
+            }
+        }
+    }
+
     __device__ __forceinline__ void store(const Params &p, int bh, int q0, int lane) const {
         const int g = lane >> 4, l16 = lane & 15;
         const int N = p.N;
@@ -342,14 +417,14 @@ struct DqTile16 {
 // itself and come out as L - s scale; the exponent is that times -log2(e). This
 // saves the per-block multiply of the staged LSE rows (16 VALU per stage at
 // d = 64) and its wait before the first score MFMA.
-template <class Pol_, int KT, bool P2 = false>
+template <class Pol_, int KT, bool P2 = false, bool W2 = false>
 struct DkvTile16 {
     using Pol = Pol_;
     using T = typename Pol::T;
     using Frag = typename Pol::Frag;
     static constexpr int D = Pol::D, NC = Pol::NC, XT = D / 16;
     static constexpr int ROWS = 16 * KT;
-    static constexpr int kWaves = Pol::kWavesDkv;
+    static constexpr int kWaves = W2 ? 2 : Pol::kWavesDkv;
     static constexpr bool kPrioFused = D == 64;
 
     Frag kf[KT][NC], vf[KT][NC];
@@ -481,7 +556,7 @@ struct DkvTile16 {
     // operands right after those, so they arrive while the softmax runs. The
     // scheduling barriers keep the compiler from sinking the reads back to
     // their uses. The arithmetic and its order are those of stage().
-    static constexpr bool kBatchedReads = D == 128 && KT == 1;
+    static constexpr bool kBatchedReads = (D == 128 && KT == 1) || W2;
     template <bool CAUSAL, bool MASK>
     __device__ __forceinline__ void stage_batched(const T *sq, const T *sdo, const float *sl, const float *sd, int qs,
                                                   int kw0, int lane) {
@@ -1086,6 +1161,10 @@ __device__ __forceinline__ void dkv_reduce_body(const Params &p, unsigned n4, in
 using DqB64 = DqTile16<PolBF16<64>, PolBF16<64>::kDqTiles>;
 using DkvB64 = DkvTile16<PolBF16<64>, 2>;
 using DkvB64P2 = DkvTile16<PolBF16<64>, 2, true>;
+// the one launch of small grids (launch_fused_k): two waves per SIMD, LDS reads batched
+using DqB64W2 = DqTile16<PolBF16<64>, PolBF16<64>::kDqTiles, true>;
+using DkvB64W2 = DkvTile16<PolBF16<64>, 2, false, true>;
+using DkvB64P2W2 = DkvTile16<PolBF16<64>, 2, true, true>;
 using DqF32 = DqTile16<PolF32<64>, PolF32<64>::kDqTiles>;
 using DkvF32 = DkvTile16<PolF32<64>, 2>;
 using DqB128 = DqTile16<PolBF16<128>, PolBF16<128>::kDqTiles>;
@@ -1140,6 +1219,10 @@ MXFA_FUSED(mxfa_bwd_b64_c, DqB64, DkvB64, true)
 MXFA_FUSED(mxfa_bwd_b64_n, DqB64, DkvB64, false)
 MXFA_FUSED(mxfa_bwd_b64_c_p2, DqB64, DkvB64P2, true)
 MXFA_FUSED(mxfa_bwd_b64_n_p2, DqB64, DkvB64P2, false)
+MXFA_FUSED(mxfa_bwd_b64_c_w2, DqB64W2, DkvB64W2, true)
+MXFA_FUSED(mxfa_bwd_b64_n_w2, DqB64W2, DkvB64W2, false)
+MXFA_FUSED(mxfa_bwd_b64_c_p2_w2, DqB64W2, DkvB64P2W2, true)
+MXFA_FUSED(mxfa_bwd_b64_n_p2_w2, DqB64W2, DkvB64P2W2, false)
 MXFA_FUSED(mxfa_bwd_b128_c, DqB128, DkvB128, true)
 MXFA_FUSED(mxfa_bwd_b128_n, DqB128, DkvB128, false)
 MXFA_REDUCE(mxfa_dkv_reduce_bf16, u16)
@@ -1165,6 +1248,15 @@ struct KernelsB64 {
     static constexpr bool kHasP2 = true;
     static constexpr KernelId dkv_p2[2] = {k_mxfa_dkv_b64_n_p2, k_mxfa_dkv_b64_c_p2};
     static constexpr KernelId fused_p2[2] = {k_mxfa_bwd_b64_n_p2, k_mxfa_bwd_b64_c_p2};
+    // the one launch at two waves per SIMD with batched LDS reads (DqB64W2,
+    // DkvB64W2 / DkvB64P2W2), for launches whose dQ and dK/dV work-groups
+    // the three-wave kernel would hold all at once: each work-group then runs
+    // faster, and the heaviest ones set the launch's time (A/B, µs: causal
+    // B4 H12 N1024 41.6 -> 34.5, B2 H12 N2048 65.4 -> 56.5, B1 H16 N2048
+    // 58.0 -> 50.2; grids of two rounds and more ran 3-8% slower with it)
+    static constexpr bool kHasW2 = true;
+    static constexpr KernelId fused_w2[2] = {k_mxfa_bwd_b64_n_w2, k_mxfa_bwd_b64_c_w2};
+    static constexpr KernelId fused_p2_w2[2] = {k_mxfa_bwd_b64_n_p2_w2, k_mxfa_bwd_b64_c_p2_w2};
     static constexpr KernelId reduce = k_mxfa_dkv_reduce_bf16;
 };
 struct KernelsB128 {
@@ -1177,6 +1269,9 @@ struct KernelsB128 {
     static constexpr bool kHasP2 = false;
     static constexpr KernelId dkv_p2[2] = {k_mxfa_dkv_b128_n, k_mxfa_dkv_b128_c};
     static constexpr KernelId fused_p2[2] = {k_mxfa_bwd_b128_n, k_mxfa_bwd_b128_c};
+    static constexpr bool kHasW2 = false;
+    static constexpr KernelId fused_w2[2] = {k_mxfa_bwd_b128_n, k_mxfa_bwd_b128_c};
+    static constexpr KernelId fused_p2_w2[2] = {k_mxfa_bwd_b128_n, k_mxfa_bwd_b128_c};
     static constexpr KernelId reduce = k_mxfa_dkv_reduce_bf16;
 };
 struct KernelsF64 {
@@ -1435,7 +1530,13 @@ static hipError_t launch_fused_k(Params p, int causal, hipStream_t stream) {
         p.share_nonce = next_share_nonce();
     }
     if (ndq + ndkv + nred > 0x7fffffffLL) return hipErrorInvalidValue;
-    const KernelId id = K::kHasP2 && scale_is_pow2(p.scale) ? K::fused_p2[causal ? 1 : 0] : K::fused[causal ? 1 : 0];
+    // the two-wave form where the three-wave kernel would hold every dQ and
+    // dK/dV work-group at once (256 CUs x its work-groups per CU); the split
+    // plan above is the three-wave tile's either way, so both give the same bits
+    const bool w2 = K::kHasW2 && ndq + ndkv <= 256LL * K::Dkv::kWaves;
+    const bool p2 = K::kHasP2 && scale_is_pow2(p.scale);
+    const int c = causal ? 1 : 0;
+    const KernelId id = w2 ? (p2 ? K::fused_p2_w2[c] : K::fused_w2[c]) : (p2 ? K::fused_p2[c] : K::fused[c]);
     void *args[] = {&p};
     const hipError_t err = launch_kernel(id, dim3((unsigned)(ndq + ndkv + nred)), dim3(256), args, stream);
     if (err != hipSuccess || p.dkv_split == 1 || p.red_rows > 0) return err;

@@ -32,6 +32,7 @@
     X(mxfa_dkv_f64_c) X(mxfa_dkv_f64_n) X(mxfa_dkv_b64_c_p2) X(mxfa_dkv_b64_n_p2)             \
     X(mxfa_bwd_b64_c) X(mxfa_bwd_b64_n) X(mxfa_bwd_b128_c) X(mxfa_bwd_b128_n)                 \
     X(mxfa_bwd_b64_c_p2) X(mxfa_bwd_b64_n_p2)                                                 \
+    X(mxfa_bwd_b64_c_w2) X(mxfa_bwd_b64_n_w2) X(mxfa_bwd_b64_c_p2_w2) X(mxfa_bwd_b64_n_p2_w2)  \
     X(mxfa_dkv_reduce_bf16) X(mxfa_dkv_reduce_f32)                                            \
     /* naive baselines (fa_naive.hip) */                                                      \
     X(mxfa_naive_scores) X(mxfa_naive_softmax) X(mxfa_naive_av) X(mxfa_naive_bwd)            \

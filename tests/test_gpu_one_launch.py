@@ -6,7 +6,10 @@ themselves after a wait bounded in time.
 - With flags it is bitwise equal to the two-launch backward
   (set_bwd_options(one_launch=False)), over shapes and over repeated runs,
   since it stages the same Delta values. A stale or early read of Delta would
-  show as a mismatch.
+  show as a mismatch. At d = 64 the shapes whose dQ and dK/dV work-groups fit
+  the three-wave kernel's slots at once (all but the north star and cfg5 here)
+  run the two-wave form with batched LDS reads (kernels mxfa_bwd_b64_*_w2),
+  which computes the same arithmetic in the same order.
 - With every wait forced to give up (delta_wait_us < 0) the dK/dV work-groups
   compute Delta from O and dO with the dQ work-groups' own arithmetic, so the
   results are still bitwise equal, and the device's fallback counter grows by
@@ -34,6 +37,9 @@ SHAPES = [
     ("d128-gqa-noncausal", (1, 4, 1, 2048, 128), False),
     ("n1", (1, 4, 4, 1, 64), True),
     ("n130", (2, 3, 3, 130, 64), False),
+    ("w2-edge", (4, 12, 12, 1024, 64), True),    # 768 dQ + dK/dV work-groups: the two-wave form's limit
+    ("w2-noncausal", (4, 12, 12, 1024, 64), False),
+    ("past-w2", (4, 12, 12, 1152, 64), True),    # 864: the three-wave form
 ]
 
 
