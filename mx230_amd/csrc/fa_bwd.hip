@@ -549,9 +549,10 @@ struct DkvTile16 {
     }
 
     // The same stage with every LDS operand of a 32-query block read ahead of the
-    // products that take it (kBatchedReads: one key tile per wave at d = 128,
+    // products that take it (kBatchedReads: d = 128, one key tile per wave at
     // two waves per SIMD, where the default order reads each operand one or two
-    // MFMAs before its use and the wave then waits out the LDS latency): all the
+    // MFMAs before its use and the wave then waits out the LDS latency; and the
+    // two-wave W2 tiles at d = 64, which have the registers for it): all the
     // score and dP operands first, then the products; the chained products'
     // operands right after those, so they arrive while the softmax runs. The
     // scheduling barriers keep the compiler from sinking the reads back to
