@@ -548,3 +548,14 @@ def test_prepare_checks_arguments_once_and_rejects_other_functions():
     assert names == sorted(["run_flash", "run_flash_lse", "run_preprocess", "run_bwd", "run_bwd_ws",
                             "run_bwd_noalloc", "run_bwd_flash", "run_bwd_dq", "run_bwd_dq_delta",
                             "run_bwd_dkv", "run_bwd_dkv_ws", "run_bwd_naive"])
+
+
+def test_bench_refuses_several_gpus():
+    """bench.py --gpus N > 1 exits with status 2 and says why, before touching a
+    device (this build runs on one GPU; the path shards with no exchange)."""
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120, cwd=root)
+    assert r.returncode == 2
+    assert "one GPU only" in r.stderr and r.stdout == ""
