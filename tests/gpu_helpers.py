@@ -22,17 +22,47 @@ ORACLE_THREADS = min(16, os.cpu_count() or 1)
 # Denominator floor of the parity metric. An output whose exact value is
 # identically zero (N = 1 gives dQ = dK = 0, since dP - Delta cancels) has no
 # magnitude to be relative to; the GPU returns fp32 cancellation noise there
-# (~5e-7 for N(0,1) inputs), so such outputs are compared against 1e-2 of the
-# O(1) input scale instead.
+# (~5e-7 for N(0,1) inputs), so without the inputs such outputs are compared
+# against 1e-2 of the O(1) input scale. Given the inputs, parity() uses
+# cancel_scale() instead.
 ZERO_FLOOR = 1e-2
 
 
-def rel_err(got, want) -> float:
+def rel_err(got, want, denom=None) -> float:
+    """max|got - want| / max|want| (floored at ZERO_FLOOR), or over denom when given."""
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)
     if want.size == 0:
         return 0.0
-    return float(np.abs(got - want).max() / max(float(np.abs(want).max()), ZERO_FLOOR))
+    if denom is None:
+        denom = max(float(np.abs(want).max()), ZERO_FLOOR)
+    return float(np.abs(got - want).max() / denom)
+
+
+def cancel_scale(q, k, v, do, scale=None):
+    """The magnitudes of the terms that cancel in dQ and dK when N = 1.
+
+    With one key every query's softmax weight is 1, O = V_0 and Delta_i =
+    dO_i . O_i equals dP_i = dO_i . V_0, so dS = P (dP - Delta) and with it dQ
+    and dK are exactly zero (the oracle's own sums cancel to 0). A kernel that
+    forms dP and Delta in different summation orders leaves fp32 rounding of
+    the size u |dP| there, summed over the group's query heads for dK. The
+    relative bar applied to the magnitude of what cancels is
+        dQ_i: scale |dP_i| max|K_0|,    dK_0: scale max_x sum_h |dP_h| |Q_hx|,
+    so a kernel that drops or mis-weights the Delta term (error of that
+    magnitude) fails it, and rounding noise (u of it) passes. Returns
+    (dQ denominator, dK denominator)."""
+    B, Hq, N, d = q.shape
+    Hkv = k.shape[1]
+    assert N == 1, "the exact cancellation holds for one key only"
+    g = Hq // Hkv
+    s = float(scale) if scale else 1.0 / np.sqrt(d)
+    kv = np.arange(Hq) // g  # query head h reads KV head h / (Hq / Hkv), as the oracle
+    q64, k64, v64, do64 = (np.asarray(x, np.float64) for x in (q, k, v, do))
+    dp = np.abs((do64 * v64[:, kv]).sum(-1, keepdims=True))  # [B, Hq, 1, 1]
+    dq_den = s * float((dp * np.abs(k64[:, kv])).max())
+    dk_den = s * float((dp * np.abs(q64)).reshape(B, Hkv, g, 1, d).sum(axis=2).max())
+    return max(dq_den, 1e-30), max(dk_den, 1e-30)
 
 
 def make_inputs(B, Hq, Hkv, N, d, mult_qkv=1.0, bf16=False, seeds=(1, 2, 3, 4), uniform=False):
@@ -111,11 +141,15 @@ def oracle_fwd_bwd(q, k, v, do, causal, scale=None):
     return o, lse, dq, dk, dv
 
 
-def parity(gpu, ref, tol):
+def parity(gpu, ref, tol, inputs=None):
     """gpu = (O, LSE, Delta, dQ, dK, dV), ref = (O, LSE, dQ, dK, dV): dict of errors
-    and the list of outputs over tolerance."""
+    and the list of outputs over tolerance. inputs = (q, k, v, do, scale): with
+    one key (N = 1) dQ and dK are measured against cancel_scale()."""
     names = ("O", "LSE", "dQ", "dK", "dV")
     got = (gpu[0], gpu[1], gpu[3], gpu[4], gpu[5])
-    errs = {n: rel_err(g, r) for n, g, r in zip(names, got, ref)}
+    dens = [None] * 5
+    if inputs is not None and inputs[0].shape[2] == 1:
+        dens[2], dens[3] = cancel_scale(*inputs)
+    errs = {n: rel_err(g, r, den) for n, g, r, den in zip(names, got, ref, dens)}
     bad = [n for n, e in errs.items() if not e <= tol]
     return errs, bad

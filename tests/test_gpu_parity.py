@@ -23,7 +23,7 @@ def _check(case, q, k, v, do, causal, bf16, tol=None, scale=None):
     print(f"\n[{case}] q{q.shape} k{k.shape} causal={causal} bf16={bf16}", flush=True)
     gpu = gpu_fwd_bwd(q, k, v, do, causal, bf16, scale=scale or 0.0)
     ref = oracle_fwd_bwd(q, k, v, do, causal, scale=scale)
-    errs, bad = parity(gpu, ref, tol)
+    errs, bad = parity(gpu, ref, tol, inputs=(q, k, v, do, scale))
     print(f"[{case}] " + " ".join(f"{n}={e:.2e}" for n, e in errs.items()), flush=True)
     assert not bad, f"{case}: {bad} over {tol}: {errs}"
     # Delta from the GPU's own O (attention_bwd.cu:32-44) against the oracle's

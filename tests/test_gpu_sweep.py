@@ -36,7 +36,17 @@ def _cases(n=24, seed=20261202):
     return cases
 
 
-CASES = _cases()
+# One-row heads (N = 1: dQ and dK cancel to exactly zero in the oracle, and the
+# GPU's rounding is measured against the size of what cancels, cancel_scale),
+# with wide groups and a large scale, where that rounding is largest: the first
+# is a shape a wider seeded sweep found over the fixed 1e-2 floor
+ONE_ROW = [
+    (2, 12, 1, 1, 64, True, False, 0.3, 9001),
+    (1, 32, 1, 1, 128, True, True, 0.3, 9005),
+    (3, 16, 2, 1, 64, False, True, 0.0, 9009),
+    (1, 8, 1, 1, 64, False, False, 0.05, 9013),
+]
+CASES = _cases() + ONE_ROW
 
 
 def _id(c):
@@ -51,6 +61,6 @@ def test_sweep_timed_path(case):
     print(f"\n[sweep] {_id(case)} scale={scale or 'default'} seed={seed}", flush=True)
     ref = oracle_fwd_bwd(q, k, v, do, causal, scale=scale or None)
     gpu = gpu_fwd_bwd_timed(q, k, v, do, causal, bf16, scale=scale)
-    errs, bad = parity(gpu, ref, TOL_BF16 if bf16 else TOL_F32)
+    errs, bad = parity(gpu, ref, TOL_BF16 if bf16 else TOL_F32, inputs=(q, k, v, do, scale or None))
     print("[sweep] " + " ".join(f"{n}={e:.2e}" for n, e in errs.items()), flush=True)
     assert not bad, errs
